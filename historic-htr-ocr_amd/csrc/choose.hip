@@ -1,0 +1,212 @@
+// The GPU token choice of greedy presets for gfx950: the windowed repetition penalty fused with a two-pass argmax.
+//
+// Semantics: ocr-decode sampling.rs:38-62 (`choose`, greedy), bit for bit — the reference GPU kernels
+// choose_pen.wgsl:85-106, choose_max.wgsl:28-61 and choose_pick.wgsl:32-69 restate the same (text.rs:222-231):
+//   - each DISTINCT id among hist[len − window … len) (its first occurrence) → logit < 0: logit·rp, else logit / rp,
+//     both one IEEE-754 f32 operation rounded to nearest even (hipcc's f32 division is correctly rounded), written
+//     back in place;
+//   - frequency penalty: a token with counts > 0 compares as logit − fpen (fpen = fp·count, stored by the pick);
+//   - first maximum wins (ties → lowest index); NaN never wins; a NaN at index 0 (after the penalty) → token 0, as the
+//     CPU loop `if l > logits[best]` starting at best = 0 decides; every logit NaN → 0.
+//
+// Schedule: grid (groups, rows); a workgroup owns 1024 consecutive logits of one row, stages them in LDS, applies the
+// penalties of the window ids that fall in its range, and reduces (value, index) to one partial (pass 1). The last
+// workgroup of the row (atomic ticket) reduces the partials (pass 2), writes the token, appends it to the history and
+// updates the counts. One launch per choice; the ticket counter resets itself.
+#include <cmath>
+
+#include "htr_internal.h"
+
+namespace {
+
+constexpr int CW = 256;
+constexpr int SPAN = 1024;
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float w, uint32_t j) { return v > w || (v == w && i < j); }
+
+__device__ __forceinline__ void wave_best(float &v, uint32_t &i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const uint32_t oi = __shfl_xor(i, off, 64);
+        if (better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+
+// block-wide best of (v, i) → returned to every thread
+__device__ __forceinline__ void block_best(float &v, uint32_t &i) {
+    __shared__ float s_v[CW / 64];
+    __shared__ uint32_t s_i[CW / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    wave_best(v, i);
+    __syncthreads();
+    if (lane == 0) {
+        s_v[wave] = v;
+        s_i[wave] = i;
+    }
+    __syncthreads();
+    v = s_v[0];
+    i = s_i[0];
+#pragma unroll
+    for (int w = 1; w < CW / 64; w++)
+        if (better(s_v[w], s_i[w], v, i)) {
+            v = s_v[w];
+            i = s_i[w];
+        }
+}
+
+__global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
+    __shared__ float s_l[SPAN];
+    __shared__ int s_last;
+    const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int lo = g * SPAN, hi = min(a.n_vocab, lo + SPAN);
+    float *logits = a.logits + (size_t)row * a.n_vocab;
+    uint32_t *hist = a.hist + (size_t)row * a.hist_stride;
+    const int len = a.len_dev ? *a.len_dev : a.len;
+
+    for (int i = tid; i < hi - lo; i += CW) s_l[i] = logits[lo + i];
+    __syncthreads();
+    // the window's distinct ids in [lo, hi)
+    if (a.rp != 1.0f) {
+        const int start = len - min(len, a.window);
+        for (int j = start + tid; j < len; j += CW) {
+            const uint32_t t = hist[j];
+            if (t < (uint32_t)lo || t >= (uint32_t)hi) continue;
+            bool first = true;
+            for (int i = start; i < j; i++)
+                if (hist[i] == t) {
+                    first = false;
+                    break;
+                }
+            if (!first) continue;
+            const float x = s_l[t - lo];
+            const float y = x < 0.0f ? x * a.rp : x / a.rp;
+            s_l[t - lo] = y;
+            logits[t] = y;
+        }
+        __syncthreads();
+    }
+    // pass 1: this workgroup's best
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (int i = tid; i < hi - lo; i += CW) {
+        float x = s_l[i];
+        const uint32_t k = (uint32_t)(lo + i);
+        if (a.fp != 0.0f && a.counts[k] != 0u) x = x - a.fpen[k];
+        if (better(x, k, bv, bi)) {
+            bv = x;
+            bi = k;
+        }
+    }
+    block_best(bv, bi);
+    uint32_t *part = a.part + ((size_t)row * gridDim.x + g) * 2;
+    if (tid == 0) {
+        part[0] = __float_as_uint(bv);
+        part[1] = bi;
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&a.counters[row], 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    // pass 2: the row's best over every workgroup's partial
+    bv = -INFINITY;
+    bi = 0xffffffffu;
+    const uint32_t *rp = a.part + (size_t)row * gridDim.x * 2;
+    for (int p = tid; p < (int)gridDim.x; p += CW) {
+        const float v = __uint_as_float(__builtin_nontemporal_load(rp + 2 * p));
+        const uint32_t i = __builtin_nontemporal_load(rp + 2 * p + 1);
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    block_best(bv, bi);
+    if (tid == 0) {
+        const float l0 = __builtin_nontemporal_load(logits);  // index 0 after the penalty (its owner wrote it back)
+        uint32_t t = bi == 0xffffffffu ? 0u : bi;
+        if (l0 != l0) t = 0u;
+        a.tok[row] = t;
+        hist[len] = t;
+        if (a.fp != 0.0f) {
+            const uint32_t c = a.counts[t] + 1u;
+            a.counts[t] = c;
+            a.fpen[t] = a.fp * (float)c;
+        }
+        if (a.len_dev) *(int *)a.len_dev = len + 1;
+        if (a.advance) a.advance[0] += 1;
+        a.counters[row] = 0u;
+    }
+}
+
+}  // namespace
+
+int choose_groups(int n_vocab) { return (n_vocab + SPAN - 1) / SPAN; }
+
+int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a) {
+    if (a.n_vocab <= 0 || a.rows <= 0) return htr_fail("choose: %d logits, %d rows", a.n_vocab, a.rows);
+    hipLaunchKernelGGL(k_choose, dim3(choose_groups(a.n_vocab), a.rows), dim3(CW), 0, st, a);
+    return htr_launched(dev, "k_choose");
+}
+
+// the penalty must be 1 or a positive normal f32 (gpu_choice_capable, text.rs:154-163)
+static int check_rp(float rp) {
+    if (rp == 1.0f) return 0;
+    if (!(rp > 0.0f) || !std::isnormal(rp)) return htr_fail("repetition penalty %g: 1 or a positive normal f32", rp);
+    return 0;
+}
+
+static int choose_scratch(htr_device *dev, int rows, int groups, uint32_t **part, uint32_t **counters) {
+    HTR_TRY(htr_scratch(dev, SCR_CHOOSE_PART, (size_t)rows * groups * 8, (void **)part));
+    return htr_scratch(dev, SCR_CHOOSE_CNT, (size_t)rows * 4, (void **)counters);
+}
+
+extern "C" int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_t *d_hist, int len, int window, float rp,
+                          float fp, uint32_t *d_counts, float *d_fpen, uint32_t *d_tok) {
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(check_rp(rp));
+    if (!d_logits || !d_hist || !d_tok) return htr_fail("htr_choose: null argument");
+    if (len < 0 || window < 1 || n_vocab < 1) return htr_fail("htr_choose: len %d, window %d, %d logits", len, window, n_vocab);
+    if (fp < 0.0f || (fp > 0.0f && (!d_counts || !d_fpen))) return htr_fail("htr_choose: fp %g needs counts and fpen", fp);
+    ChooseArgs a{};
+    a.logits = d_logits;
+    a.n_vocab = n_vocab;
+    a.hist = d_hist;
+    a.hist_stride = 0;
+    a.len = len;
+    a.window = window;
+    a.rp = rp;
+    a.fp = fp;
+    a.counts = d_counts;
+    a.fpen = d_fpen;
+    a.tok = d_tok;
+    a.rows = 1;
+    HTR_TRY(choose_scratch(dev, 1, choose_groups(n_vocab), &a.part, &a.counters));
+    return launch_choose(dev, dev->stream, a);
+}
+
+extern "C" int htr_choose_many(htr_device *dev, float *d_logits, int n_vocab, int n, uint32_t *d_hist, int hist_stride,
+                               int len, int window, float rp, uint32_t *d_tok) {
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(check_rp(rp));
+    if (!d_logits || !d_hist || !d_tok || n < 1) return htr_fail("htr_choose_many: null argument or n < 1");
+    if (len < 0 || len >= hist_stride || window < 1)
+        return htr_fail("htr_choose_many: len %d, history stride %d, window %d", len, hist_stride, window);
+    if (n > 65535) return htr_fail("htr_choose_many: %d rows (at most 65535 per launch)", n);
+    ChooseArgs a{};
+    a.logits = d_logits;
+    a.n_vocab = n_vocab;
+    a.hist = d_hist;
+    a.hist_stride = hist_stride;
+    a.len = len;
+    a.window = window;
+    a.rp = rp;
+    a.tok = d_tok;
+    a.rows = n;
+    HTR_TRY(choose_scratch(dev, n, choose_groups(n_vocab), &a.part, &a.counters));
+    return launch_choose(dev, dev->stream, a);
+}

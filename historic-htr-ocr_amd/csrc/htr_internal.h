@@ -1,0 +1,139 @@
+// Internal declarations of libhtr: the device object, the sticky error latch, weights, and the kernel launchers the
+// host-side decoder (text_model.hip) composes. Kernels are compiled for gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "htr.h"
+
+// ---- errors ---------------------------------------------------------------------------------------------------------
+
+// sets the calling thread's message; returns -1 (the ABI's error code)
+int htr_fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+struct htr_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    // sticky health (gpu.rs:900-970): the first failure's kind and message; every later call fails with it
+    std::string dead_kind, dead_msg;
+    htr_fatal_hook hook = nullptr;
+    void *hook_user = nullptr;
+    htr_gpu_bytes live{};
+    std::unordered_map<void *, std::pair<size_t, int>> allocs;
+    char name[256] = {0};
+    int n_cu = 0;
+    // pinned host staging for small transfers (token ids, positions)
+    void *pinned = nullptr;
+    size_t pinned_bytes = 0;
+    // scratch of the standalone kernel entry points, grown on demand (zero-filled when (re)allocated)
+    void *scratch[8] = {nullptr};
+    size_t scratch_bytes[8] = {0};
+    // the measurement timer's events
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3 };
+// the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it, zero-filled)
+int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out);
+
+// the device is dead: latch the first reason and fire the hook once; returns -1
+int htr_latch(htr_device *dev, const char *kind, const char *msg);
+// -1 with the sticky reason if the device is dead, else 0
+int htr_check_alive(htr_device *dev);
+// a HIP error on dev → latched death (kind from the error code); returns -1. ok → 0.
+int htr_hip(htr_device *dev, hipError_t e, const char *what);
+// after a kernel launch: hipGetLastError → htr_hip
+int htr_launched(htr_device *dev, const char *kernel);
+
+// device memory counted in the ledger (zero-filled)
+int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out);
+int htr_dev_free(htr_device *dev, void *p);
+
+#define HTR_TRY(expr)                                                                                                  \
+    do {                                                                                                               \
+        int htr_rc_ = (expr);                                                                                          \
+        if (htr_rc_ < 0) return htr_rc_;                                                                               \
+    } while (0)
+
+// ---- weights --------------------------------------------------------------------------------------------------------
+
+struct htr_weight {
+    htr_device *dev = nullptr;
+    size_t rows = 0, cols = 0;
+    // q8_0 repacked: quants [rows][cols] int8, scales [rows][cols/32] f16
+    int8_t *q = nullptr;
+    _Float16 *d = nullptr;
+    // dequantised f16 [rows][cols] (MFMA GEMM weights)
+    _Float16 *h = nullptr;
+};
+
+// ---- kernel launchers (each returns 0 or -1 with the device latched) -------------------------------------------------
+
+// the matvec family (q8_0.hip)
+enum DmvMode { DMV_PLAIN = 0, DMV_NORM = 1, DMV_QKV = 2, DMV_FFN = 3 };
+struct DmvMat {
+    const int8_t *q;
+    const _Float16 *d;
+    int rows;
+};
+int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, int n_mats, int k, const float *x,
+               const float *nw, float eps, float *y, int acc);
+int launch_dmv_many(htr_device *dev, hipStream_t st, const DmvMat *mats, int n, int k, const float *x, float *y);
+int launch_embed(htr_device *dev, hipStream_t st, const htr_weight *w, const uint32_t *tok, int n_tok, float *x);
+
+// attention (attention.hip)
+int launch_qkv_post(htr_device *dev, hipStream_t st, float *qkv, const float *qn, const float *kn, const float *rope,
+                    int n_head, int n_kv, const int *pos_dev, int pos, int n_ctx, float eps, uint16_t *kc,
+                    uint16_t *vc);
+// split-K decode attention; n_keys = *n_keys_dev (+ add) when n_keys_dev != NULL, else n_keys. Scratch: part
+// [n_head][max_chunk][130] f32 and counters [n_kv] u32 (zero, self-resetting)
+struct AttnScratch {
+    float *part;
+    uint32_t *counters;
+    int max_chunk, chunk;
+};
+int attn_chunk_for(int n_ctx);
+int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
+                       int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
+                       const AttnScratch &sc, float *out);
+// prefill pieces: per-head norm + rope + KV store over n_tok rows
+int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k, const float *v, const float *qn,
+                             const float *kn, const float *rope, int n_tok, int n_head, int n_kv, int pos0, int n_ctx,
+                             float eps, uint16_t *kc, uint16_t *vc);
+int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
+                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out);
+
+// token choice (choose.hip)
+struct ChooseArgs {
+    float *logits;
+    int n_vocab;
+    uint32_t *hist;
+    int hist_stride;
+    const int *len_dev;  // NULL → len
+    int len;
+    int window;
+    float rp;  // 1 → no penalty
+    float fp;  // 0 → no frequency penalty
+    uint32_t *counts;
+    float *fpen;
+    uint32_t *tok;
+    int *advance;  // NULL, or { pos, len } incremented by the pick (the decode loop's device-resident counters)
+    uint32_t *part;      // [rows][n_groups][2]
+    uint32_t *counters;  // [rows], zero, self-resetting
+    int rows;
+};
+int choose_groups(int n_vocab);
+int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a);
+
+// dense kernels (gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ with W q8_0 (exact dequant), f32; rms_norm rows; swiglu
+int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
+                         int acc);
+int launch_rms_norm(htr_device *dev, hipStream_t st, const float *x, const float *w, float *y, int rows, int dim,
+                    float eps);
+int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, size_t n);

@@ -1,0 +1,553 @@
+// The text decoder's host side: TextModel (text.rs:30-130, 332-375), Session (text.rs:242-434), the prefill
+// (text.rs:437-521), the CPU-choice step (text.rs:524-537), the GPU token choice (text.rs:165-232) and the run-ahead
+// decode (text.rs:587-625), on the kernels of q8_0.hip / attention.hip / choose.hip / gemm.hip.
+//
+// The decode step (record_step, text.rs:540-578 with layers_fused, text.rs:630-647) is 1 + 6·n_layer + 1 launches:
+//   embed → per layer: qkv matvec (attn_norm fused) → qkv_post (q/k norm, RoPE, f16 KV store) → split-K attention
+//   (merge fused) → o matvec (+ residual) → gate/up matvec (ffn_norm + SwiGLU fused) → down matvec (+ residual)
+//   → LM head (output_norm fused) [→ token choice].
+// Position and history length live in device memory (state[0] = pos, state[1] = len), so one captured HIP graph of
+// `chunk` steps is replayed for the whole read: the choice kernel advances both, the next step's embed reads the
+// chosen token from device memory. Only the chosen ids (4 bytes a token) come back to the host.
+#include <cmath>
+#include <cstring>
+#include <deque>
+#include <vector>
+
+#include "htr_internal.h"
+
+namespace {
+
+constexpr int HEAD = 128;
+
+struct Layer {
+    htr_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr,
+               *down = nullptr;
+    float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *ffn_norm = nullptr;
+};
+
+// text.rs:132-142: θ = f32(pos)·powf(base, −2i/d), cos / sin in f32
+std::vector<float> rope_table(float base, int d_head, int n_pos) {
+    const int half = d_head / 2;
+    std::vector<float> out((size_t)n_pos * half * 2);
+    for (int pos = 0; pos < n_pos; pos++)
+        for (int i = 0; i < half; i++) {
+            const float theta = (float)pos * powf(base, -((float)(2 * i)) / (float)d_head);
+            out[2 * ((size_t)pos * half + i)] = cosf(theta);
+            out[2 * ((size_t)pos * half + i) + 1] = sinf(theta);
+        }
+    return out;
+}
+
+}  // namespace
+
+struct htr_text_model {
+    htr_device *dev = nullptr;
+    htr_text_config cfg{};
+    htr_weight *tok_embd = nullptr;
+    float *output_norm = nullptr;
+    std::vector<Layer> layers;
+};
+
+struct htr_session {
+    htr_text_model *m = nullptr;
+    htr_device *dev = nullptr;
+    int n_ctx = 0, n_past = 0;
+    size_t kv_layer = 0;  // halves per layer and cache (n_kv · n_ctx · 128)
+    uint16_t *kc = nullptr, *vc = nullptr;
+    float *rope = nullptr;
+    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *g = nullptr, *logits = nullptr;
+    uint32_t *tok = nullptr;
+    int *state = nullptr;  // [pos, len]
+    AttnScratch asc{};
+    hipGraphExec_t step_graph = nullptr;  // the CPU-choice step (no token choice)
+};
+
+struct htr_choice {
+    htr_session *s = nullptr;
+    int seed_len = 0, window = 1;
+    float rp = 1.0f, fp = 0.0f;
+    size_t max_new = 0, chunk = 1, depth = 1;
+    int n_vocab = 0;
+    uint32_t *hist = nullptr, *counts = nullptr, *part = nullptr, *counters = nullptr;
+    float *fpen = nullptr;
+    uint32_t *h_ids = nullptr;  // pinned [depth][chunk]
+    std::vector<hipEvent_t> events;
+    hipGraphExec_t g_first = nullptr, g_one = nullptr, g_chunk = nullptr;
+};
+
+namespace {
+
+int check_model_cfg(const htr_text_config &c) {
+    if (c.n_layer < 1 || c.dim < 32 || c.n_head < 1 || c.n_kv < 1 || c.n_ff < 32 || c.n_vocab < 1)
+        return htr_fail("text config: %d layers, dim %d, %d / %d heads, ffn %d, vocab %d", c.n_layer, c.dim, c.n_head,
+                        c.n_kv, c.n_ff, c.n_vocab);
+    if (c.d_head != HEAD) return htr_fail("head dim %d: the attention kernels are written for 128", c.d_head);
+    if (c.n_head % c.n_kv != 0) return htr_fail("%d q heads on %d kv heads", c.n_head, c.n_kv);
+    const int qd = c.n_head * c.d_head;
+    if (c.dim % 32 || c.n_ff % 32 || qd % 32)
+        return htr_fail("dims %d / %d / %d: q8_0 rows must be whole blocks", c.dim, c.n_ff, qd);
+    if (c.dim > 4096 || c.n_ff > 4096 || qd > 4096)
+        return htr_fail("dims %d / %d / %d: the matvec kernels take K ≤ 4096", c.dim, c.n_ff, qd);
+    return 0;
+}
+
+int upload_vec(htr_device *dev, const float *h, size_t n, float **out) {
+    if (!h) return htr_fail("missing f32 tensor of %zu values", n);
+    HTR_TRY(htr_dev_alloc(dev, n * 4, HTR_MEM_WEIGHTS, (void **)out));
+    return htr_upload(dev, *out, h, n * 4);
+}
+
+int upload_w(htr_device *dev, const void *h, size_t rows, size_t cols, const char *what, htr_weight **out) {
+    if (!h) return htr_fail("missing q8_0 tensor %s [%zu x %zu]", what, rows, cols);
+    if (htr_weight_q8_0(dev, h, rows, cols, out) < 0) return htr_fail("%s: %s", what, htr_last_error());
+    return 0;
+}
+
+// one decode step on the session's stream: token s->tok at position state[0] → s->logits
+int record_step(htr_session *s, hipStream_t st) {
+    htr_text_model *m = s->m;
+    htr_device *dev = s->dev;
+    const htr_text_config &c = m->cfg;
+    const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
+    const float scale = 1.0f / sqrtf((float)HEAD);
+    HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
+    for (int li = 0; li < c.n_layer; li++) {
+        const Layer &ly = m->layers[li];
+        uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
+        DmvMat qkv[3] = {{ly.q->q, ly.q->d, qd}, {ly.k->q, ly.k->d, kvd}, {ly.v->q, ly.v->d, kvd}};
+        HTR_TRY(launch_dmv(dev, st, DMV_QKV, qkv, 3, c.dim, s->x, ly.attn_norm, c.eps, s->qkv, 0));
+        HTR_TRY(launch_qkv_post(dev, st, s->qkv, ly.q_norm, ly.k_norm, s->rope, c.n_head, c.n_kv, s->state, 0, s->n_ctx,
+                                c.eps, kc, vc));
+        HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale, s->asc,
+                                   s->attn));
+        DmvMat o = {ly.o->q, ly.o->d, c.dim};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
+        DmvMat gu[2] = {{ly.gate->q, ly.gate->d, c.n_ff}, {ly.up->q, ly.up->d, c.n_ff}};
+        HTR_TRY(launch_dmv(dev, st, DMV_FFN, gu, 2, c.dim, s->x, ly.ffn_norm, c.eps, s->g, 0));
+        DmvMat dn = {ly.down->q, ly.down->d, c.dim};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &dn, 1, c.n_ff, s->g, nullptr, 0.0f, s->x, 1));
+    }
+    DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
+    return launch_dmv(dev, st, DMV_NORM, &head, 1, c.dim, s->x, m->output_norm, c.eps, s->logits, 0);
+}
+
+ChooseArgs choice_args(htr_choice *ch, bool advance) {
+    htr_session *s = ch->s;
+    ChooseArgs a{};
+    a.logits = s->logits;
+    a.n_vocab = ch->n_vocab;
+    a.hist = ch->hist;
+    a.hist_stride = 0;
+    a.len_dev = s->state + 1;
+    a.window = ch->window;
+    a.rp = ch->rp;
+    a.fp = ch->fp;
+    a.counts = ch->counts;
+    a.fpen = ch->fpen;
+    a.tok = s->tok;
+    a.advance = advance ? s->state : nullptr;
+    a.part = ch->part;
+    a.counters = ch->counters;
+    a.rows = 1;
+    return a;
+}
+
+// capture `n` repetitions of [step? + choice] into an executable graph
+int capture(htr_session *s, htr_choice *ch, int n, bool with_step, hipGraphExec_t *out) {
+    htr_device *dev = s->dev;
+    hipStream_t st = dev->stream;
+    HTR_TRY(htr_hip(dev, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
+    int rc = 0;
+    for (int i = 0; i < n && rc == 0; i++) {
+        if (with_step) rc = record_step(s, st);
+        if (rc == 0 && ch) rc = launch_choose(dev, st, choice_args(ch, with_step));
+    }
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &graph);
+    if (rc < 0) {
+        if (graph) hipGraphDestroy(graph);
+        return rc;
+    }
+    HTR_TRY(htr_hip(dev, e, "hipStreamEndCapture"));
+    e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    return htr_hip(dev, e, "hipGraphInstantiate");
+}
+
+int set_state(htr_session *s, int pos, int len) {
+    int v[2] = {pos, len};
+    // pinned staging: the copy reads it when the stream gets there, so wait for it before the staging is reused
+    memcpy(s->dev->pinned, v, sizeof v);
+    HTR_TRY(htr_hip(s->dev, hipMemcpyAsync(s->state, s->dev->pinned, sizeof v, hipMemcpyHostToDevice, s->dev->stream),
+                    "state upload"));
+    return htr_hip(s->dev, hipStreamSynchronize(s->dev->stream), "state upload sync");
+}
+
+}  // namespace
+
+// ---- model ----------------------------------------------------------------------------------------------------------
+
+extern "C" int htr_text_model_free(htr_text_model *m) {
+    if (!m) return 0;
+    htr_device *dev = m->dev;
+    for (Layer &l : m->layers) {
+        for (htr_weight *w : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) htr_weight_free(w);
+        for (float *p : {l.attn_norm, l.q_norm, l.k_norm, l.ffn_norm})
+            if (p) htr_dev_free(dev, p);
+    }
+    htr_weight_free(m->tok_embd);
+    if (m->output_norm) htr_dev_free(dev, m->output_norm);
+    delete m;
+    return 0;
+}
+
+extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg, const void *tok_embd,
+                                     const float *output_norm, const htr_layer_tensors *layers, htr_text_model **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!cfg || !layers || !out) return htr_fail("htr_text_model_create: null argument");
+    HTR_TRY(check_model_cfg(*cfg));
+    const htr_text_config &c = *cfg;
+    const size_t d = c.dim, f = c.n_ff, qd = (size_t)c.n_head * HEAD, kvd = (size_t)c.n_kv * HEAD;
+    auto *m = new htr_text_model;
+    m->dev = dev;
+    m->cfg = c;
+    m->layers.resize(c.n_layer);
+    int rc = 0;
+    for (int i = 0; i < c.n_layer && rc == 0; i++) {
+        const htr_layer_tensors &t = layers[i];
+        Layer &l = m->layers[i];
+        rc = upload_vec(dev, t.attn_norm, d, &l.attn_norm);
+        if (rc == 0) rc = upload_w(dev, t.q, qd, d, "attn_q", &l.q);
+        if (rc == 0) rc = upload_w(dev, t.k, kvd, d, "attn_k", &l.k);
+        if (rc == 0) rc = upload_w(dev, t.v, kvd, d, "attn_v", &l.v);
+        if (rc == 0) rc = upload_w(dev, t.o, d, qd, "attn_output", &l.o);
+        if (rc == 0) rc = upload_vec(dev, t.q_norm, HEAD, &l.q_norm);
+        if (rc == 0) rc = upload_vec(dev, t.k_norm, HEAD, &l.k_norm);
+        if (rc == 0) rc = upload_vec(dev, t.ffn_norm, d, &l.ffn_norm);
+        if (rc == 0) rc = upload_w(dev, t.gate, f, d, "ffn_gate", &l.gate);
+        if (rc == 0) rc = upload_w(dev, t.up, f, d, "ffn_up", &l.up);
+        if (rc == 0) rc = upload_w(dev, t.down, d, f, "ffn_down", &l.down);
+        if (rc < 0) rc = htr_fail("blk.%d: %s", i, std::string(htr_last_error()).c_str());
+    }
+    if (rc == 0) rc = upload_w(dev, tok_embd, c.n_vocab, d, "token_embd", &m->tok_embd);
+    if (rc == 0) rc = upload_vec(dev, output_norm, d, &m->output_norm);
+    if (rc < 0) {
+        std::string keep = htr_last_error();
+        htr_text_model_free(m);
+        return htr_fail("%s", keep.c_str());
+    }
+    *out = m;
+    return 0;
+}
+
+// ---- session --------------------------------------------------------------------------------------------------------
+
+extern "C" int htr_session_free(htr_session *s) {
+    if (!s) return 0;
+    htr_device *dev = s->dev;
+    if (s->step_graph) hipGraphExecDestroy(s->step_graph);
+    for (void *p : {(void *)s->kc, (void *)s->vc, (void *)s->rope, (void *)s->x, (void *)s->qkv, (void *)s->attn,
+                    (void *)s->g, (void *)s->logits, (void *)s->tok, (void *)s->state, (void *)s->asc.part,
+                    (void *)s->asc.counters})
+        if (p) htr_dev_free(dev, p);
+    delete s;
+    return 0;
+}
+
+extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out) {
+    if (!m || !out) return htr_fail("htr_session_create: null argument");
+    htr_device *dev = m->dev;
+    HTR_TRY(htr_check_alive(dev));
+    const htr_text_config &c = m->cfg;
+    if (c.n_head != 2 * c.n_kv)
+        return htr_fail("%d q heads on %d kv heads: the split decode attention is written for groups of 2", c.n_head,
+                        c.n_kv);
+    if (n_ctx < 1 || (c.n_ctx_train > 0 && n_ctx > (size_t)c.n_ctx_train))
+        return htr_fail("%zu positions asked, the model was trained on %d", n_ctx, c.n_ctx_train);
+    if (n_ctx > (1u << 20)) return htr_fail("%zu positions: at most %u", n_ctx, 1u << 20);
+    auto *s = new htr_session;
+    s->m = m;
+    s->dev = dev;
+    s->n_ctx = (int)n_ctx;
+    s->kv_layer = (size_t)c.n_kv * n_ctx * HEAD;
+    const size_t qd = (size_t)c.n_head * HEAD, kvd = (size_t)c.n_kv * HEAD;
+    s->asc.chunk = attn_chunk_for(s->n_ctx);
+    s->asc.max_chunk = (s->n_ctx + s->asc.chunk - 1) / s->asc.chunk;
+    std::vector<float> rope = rope_table(c.rope_base, HEAD, s->n_ctx);
+    int rc = htr_dev_alloc(dev, s->kv_layer * c.n_layer * 2, HTR_MEM_KV_CACHE, (void **)&s->kc);
+    if (rc == 0) rc = htr_dev_alloc(dev, s->kv_layer * c.n_layer * 2, HTR_MEM_KV_CACHE, (void **)&s->vc);
+    if (rc == 0) rc = htr_dev_alloc(dev, rope.size() * 4, HTR_MEM_WORK, (void **)&s->rope);
+    if (rc == 0) rc = htr_upload(dev, s->rope, rope.data(), rope.size() * 4);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.dim * 4, HTR_MEM_WORK, (void **)&s->x);
+    if (rc == 0) rc = htr_dev_alloc(dev, (qd + 2 * kvd) * 4, HTR_MEM_WORK, (void **)&s->qkv);
+    if (rc == 0) rc = htr_dev_alloc(dev, qd * 4, HTR_MEM_WORK, (void **)&s->attn);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_ff * 4, HTR_MEM_WORK, (void **)&s->g);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_vocab * 4, HTR_MEM_WORK, (void **)&s->logits);
+    if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->tok);
+    if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->state);
+    if (rc == 0)
+        rc = htr_dev_alloc(dev, (size_t)c.n_head * s->asc.max_chunk * (HEAD + 2) * 4, HTR_MEM_WORK,
+                           (void **)&s->asc.part);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_kv * 4, HTR_MEM_WORK, (void **)&s->asc.counters);
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc < 0) {
+        std::string keep = htr_last_error();
+        htr_session_free(s);
+        return htr_fail("%s", keep.c_str());
+    }
+    *out = s;
+    return 0;
+}
+
+extern "C" int htr_session_n_past(htr_session *s, size_t *out) {
+    if (!s || !out) return htr_fail("htr_session_n_past: null argument");
+    *out = (size_t)s->n_past;
+    return 0;
+}
+
+extern "C" int htr_session_logits(htr_session *s, float *h_logits) {
+    if (!s || !h_logits) return htr_fail("htr_session_logits: null argument");
+    return htr_download(s->dev, h_logits, s->logits, (size_t)s->m->cfg.n_vocab * 4);
+}
+
+extern "C" int htr_session_rewind(htr_session *s, size_t n_past) {
+    if (!s) return htr_fail("htr_session_rewind: null session");
+    if (n_past > (size_t)s->n_past) return htr_fail("rewind to %zu: the session is at %d", n_past, s->n_past);
+    s->n_past = (int)n_past;
+    return 0;
+}
+
+// text.rs:437-521
+extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *h_logits) {
+    if (!s || !ids) return htr_fail("htr_prefill: null argument");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    htr_text_model *m = s->m;
+    const htr_text_config &c = m->cfg;
+    if (n == 0) return htr_fail("empty prompt");
+    if ((size_t)s->n_past + n > (size_t)s->n_ctx)
+        return htr_fail("%d + %zu positions overflow the session's %d", s->n_past, n, s->n_ctx);
+    std::vector<uint32_t> tok(n);
+    for (size_t i = 0; i < n; i++) {
+        if (ids[i] < 0 || ids[i] >= c.n_vocab) return htr_fail("token %d is outside the vocabulary", ids[i]);
+        tok[i] = (uint32_t)ids[i];
+    }
+    const int l = (int)n, d = c.dim, f = c.n_ff, qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
+    const int pos0 = s->n_past;
+    hipStream_t st = dev->stream;
+    uint32_t *d_tok = nullptr;
+    float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *a = nullptr, *g = nullptr,
+          *u = nullptr;
+    auto cleanup = [&] {
+        for (void *p : {(void *)d_tok, (void *)x, (void *)h, (void *)q, (void *)k, (void *)v, (void *)a, (void *)g,
+                        (void *)u})
+            if (p) htr_dev_free(dev, p);
+    };
+    int rc = htr_dev_alloc(dev, n * 4, HTR_MEM_WORK, (void **)&d_tok);
+    if (rc == 0) rc = htr_upload(dev, d_tok, tok.data(), n * 4);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * d * 4, HTR_MEM_WORK, (void **)&x);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * d * 4, HTR_MEM_WORK, (void **)&h);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * qd * 4, HTR_MEM_WORK, (void **)&q);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * kvd * 4, HTR_MEM_WORK, (void **)&k);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * kvd * 4, HTR_MEM_WORK, (void **)&v);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * qd * 4, HTR_MEM_WORK, (void **)&a);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * f * 4, HTR_MEM_WORK, (void **)&g);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * f * 4, HTR_MEM_WORK, (void **)&u);
+    const float scale = 1.0f / sqrtf((float)HEAD);
+    if (rc == 0) rc = launch_embed(dev, st, m->tok_embd, d_tok, l, x);
+    for (int li = 0; li < c.n_layer && rc == 0; li++) {
+        const Layer &ly = m->layers[li];
+        uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
+        rc = launch_rms_norm(dev, st, x, ly.attn_norm, h, l, d, c.eps);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.q, q, l, 0);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.k, k, l, 0);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.v, v, l, 0);
+        if (rc == 0)
+            rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
+                                          s->n_ctx, c.eps, kc, vc);
+        if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, a);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, a, ly.o, x, l, 1);
+        if (rc == 0) rc = launch_rms_norm(dev, st, x, ly.ffn_norm, h, l, d, c.eps);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.gate, g, l, 0);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.up, u, l, 0);
+        if (rc == 0) rc = launch_swiglu(dev, st, g, u, (size_t)l * f);
+        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, g, ly.down, x, l, 1);
+    }
+    // head (text.rs:655-658): output_norm + the tied LM head on the last row
+    if (rc == 0) {
+        DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
+        rc = launch_dmv(dev, st, DMV_NORM, &head, 1, d, x + (size_t)(l - 1) * d, m->output_norm, c.eps, s->logits, 0);
+    }
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc == 0 && h_logits) rc = htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4);
+    std::string keep = rc < 0 ? htr_last_error() : "";
+    cleanup();
+    if (rc < 0) return htr_fail("%s", keep.c_str());
+    s->n_past += l;
+    return 0;
+}
+
+// text.rs:524-537
+extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
+    if (!s) return htr_fail("htr_step: null session");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    const htr_text_config &c = s->m->cfg;
+    if (token < 0 || token >= c.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
+    if (s->n_past + 1 > s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
+    uint32_t t = (uint32_t)token;
+    HTR_TRY(htr_upload(dev, s->tok, &t, 4));
+    HTR_TRY(set_state(s, s->n_past, 0));
+    if (!s->step_graph) HTR_TRY(capture(s, nullptr, 1, true, &s->step_graph));
+    HTR_TRY(htr_hip(dev, hipGraphLaunch(s->step_graph, dev->stream), "hipGraphLaunch"));
+    HTR_TRY(htr_sync(dev));
+    s->n_past += 1;
+    if (h_logits) HTR_TRY(htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4));
+    return 0;
+}
+
+// ---- the GPU token choice -------------------------------------------------------------------------------------------
+
+extern "C" int htr_choice_free(htr_choice *ch) {
+    if (!ch) return 0;
+    htr_device *dev = ch->s->dev;
+    for (hipGraphExec_t g : {ch->g_first, ch->g_one, ch->g_chunk})
+        if (g) hipGraphExecDestroy(g);
+    for (hipEvent_t e : ch->events) hipEventDestroy(e);
+    for (void *p : {(void *)ch->hist, (void *)ch->counts, (void *)ch->fpen, (void *)ch->part, (void *)ch->counters})
+        if (p) htr_dev_free(dev, p);
+    if (ch->h_ids) hipHostFree(ch->h_ids);
+    delete ch;
+    return 0;
+}
+
+// text.rs:154-218
+extern "C" int htr_choice_create(htr_session *s, const htr_preset *p, const int32_t *history, size_t n, size_t chunk,
+                                 size_t depth, htr_choice **out) {
+    if (!s || !p || !out || (n && !history)) return htr_fail("htr_choice_create: null argument");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    if (p->temperature != 0.0) return htr_fail("sampled (temperature > 0): the token is drawn on the CPU");
+    const float rp = (float)p->repetition_penalty;
+    if (p->repetition_penalty != 1.0 && !(std::isnormal(rp) && rp > 0.0f))
+        return htr_fail("the repetition penalty is no positive normal f32");
+    if (p->repetition_window < 1 || p->max_new_tokens < 1 || p->frequency_penalty < 0.0)
+        return htr_fail("preset: window %zu, max new tokens %zu, fp %g", p->repetition_window, p->max_new_tokens,
+                        p->frequency_penalty);
+    if (chunk < 1 || chunk > 64 || depth < 1)
+        return htr_fail("run-ahead %zu choices × %zu launches: 1…64 × ≥ 1", chunk, depth);
+    const int n_vocab = s->m->cfg.n_vocab;
+    const size_t seed_len = std::min(n, p->repetition_window);
+    const int32_t *seed = history + (n - seed_len);
+    std::vector<uint32_t> hist(seed_len + p->max_new_tokens, 0);
+    for (size_t i = 0; i < seed_len; i++) {
+        if (seed[i] < 0 || seed[i] >= n_vocab) return htr_fail("history token %d is outside the vocabulary", seed[i]);
+        hist[i] = (uint32_t)seed[i];
+    }
+    auto *ch = new htr_choice;
+    ch->s = s;
+    ch->seed_len = (int)seed_len;
+    ch->window = (int)std::min<size_t>(p->repetition_window, 1u << 30);
+    ch->rp = p->repetition_penalty != 1.0 ? rp : 1.0f;
+    ch->fp = p->frequency_penalty > 0.0 ? (float)p->frequency_penalty : 0.0f;
+    ch->max_new = p->max_new_tokens;
+    ch->chunk = chunk;
+    ch->depth = depth;
+    ch->n_vocab = n_vocab;
+    const size_t words = ch->fp > 0.0f ? (size_t)n_vocab : 1;
+    int rc = htr_dev_alloc(dev, hist.size() * 4, HTR_MEM_WORK, (void **)&ch->hist);
+    if (rc == 0) rc = htr_upload(dev, ch->hist, hist.data(), hist.size() * 4);
+    if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->counts);
+    if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->fpen);
+    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)choose_groups(n_vocab) * 8, HTR_MEM_WORK, (void **)&ch->part);
+    if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&ch->counters);
+    if (rc == 0) rc = htr_hip(dev, hipHostMalloc((void **)&ch->h_ids, depth * chunk * 4, hipHostMallocDefault), "hipHostMalloc");
+    for (size_t i = 0; i < depth && rc == 0; i++) {
+        hipEvent_t e;
+        rc = htr_hip(dev, hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+        if (rc == 0) ch->events.push_back(e);
+    }
+    if (rc < 0) {
+        std::string keep = htr_last_error();
+        htr_choice_free(ch);
+        return htr_fail("%s", keep.c_str());
+    }
+    *out = ch;
+    return 0;
+}
+
+// text.rs:587-625
+extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_token_cb on_token, void *user) {
+    if (!s || !ch || ch->s != s) return htr_fail("htr_decode_gpu: null argument or a choice of another session");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    const size_t cap = ch->max_new;
+    if (max > cap) return htr_fail("%zu choices: the history holds %zu", max, cap);
+    if (max == 0) return 0;
+    if ((size_t)s->n_past + (max - 1) > (size_t)s->n_ctx)
+        return htr_fail("%zu choices need %zu positions, the session holds %d", max, s->n_past + max - 1, s->n_ctx);
+    hipStream_t st = dev->stream;
+    if (!ch->g_first) HTR_TRY(capture(s, ch, 1, false, &ch->g_first));
+    if (!ch->g_one) HTR_TRY(capture(s, ch, 1, true, &ch->g_one));
+    if (!ch->g_chunk && ch->chunk > 1) HTR_TRY(capture(s, ch, (int)ch->chunk, true, &ch->g_chunk));
+    HTR_TRY(set_state(s, s->n_past, ch->seed_len));
+
+    struct Pending {
+        size_t slot, n;
+    };
+    std::deque<Pending> queue;
+    std::vector<size_t> free_slots;
+    for (size_t i = ch->depth; i-- > 0;) free_slots.push_back(i);
+    size_t next = 0;  // choices launched
+    int rc = 0;
+    bool stop = false;
+    while (rc == 0) {
+        while (!stop && next < max && !free_slots.empty()) {
+            const size_t slot = free_slots.back();
+            free_slots.pop_back();
+            size_t n_launched = 0;
+            if (next == 0) {
+                rc = htr_hip(dev, hipGraphLaunch(ch->g_first, st), "hipGraphLaunch");
+                n_launched = 1;
+            }
+            // fill the slot up to `chunk` choices: whole chunk graphs, else single steps
+            while (rc == 0 && n_launched < ch->chunk && next + n_launched < max) {
+                const size_t left = std::min(ch->chunk - n_launched, max - next - n_launched);
+                if (left == ch->chunk && ch->g_chunk) {
+                    rc = htr_hip(dev, hipGraphLaunch(ch->g_chunk, st), "hipGraphLaunch");
+                    n_launched += ch->chunk;
+                } else {
+                    rc = htr_hip(dev, hipGraphLaunch(ch->g_one, st), "hipGraphLaunch");
+                    n_launched += 1;
+                }
+            }
+            if (rc < 0) break;
+            rc = htr_hip(dev,
+                         hipMemcpyAsync(ch->h_ids + slot * ch->chunk, ch->hist + ch->seed_len + next, n_launched * 4,
+                                        hipMemcpyDeviceToHost, st),
+                         "token readback");
+            if (rc == 0) rc = htr_hip(dev, hipEventRecord(ch->events[slot], st), "hipEventRecord");
+            queue.push_back({slot, n_launched});
+            next += n_launched;
+        }
+        if (rc < 0 || queue.empty()) break;
+        Pending pd = queue.front();
+        queue.pop_front();
+        rc = htr_hip(dev, hipEventSynchronize(ch->events[pd.slot]), "hipEventSynchronize");
+        if (rc < 0) break;
+        for (size_t i = 0; i < pd.n && !stop; i++) {
+            if (on_token && !on_token((int32_t)ch->h_ids[pd.slot * ch->chunk + i], user)) stop = true;
+        }
+        free_slots.push_back(pd.slot);
+        if (stop) {
+            // the launches already queued finish on the device unseen
+            while (!queue.empty()) queue.pop_front();
+        }
+    }
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc < 0) return rc;
+    // the steps launched: every choice but the first of the read advanced the position by one
+    s->n_past += (int)(next - 1);
+    return 0;
+}

@@ -1,0 +1,455 @@
+"""ctypes binding of libhtr.so — the gfx950 LightOnOCR decode path behind include/htr.h.
+
+The classes mirror the reference engine's types on this path (app/crates/ocr-wgpu/src): ``Device`` ≙ ``Gpu``
+(gpu.rs:1101-1485), ``Weight`` ≙ ``Weight`` (gpu.rs, WeightType::Q8_0), ``TextModel`` / ``Session`` / ``Choice`` ≙
+text.rs's ``TextModel`` / ``Session`` / ``Choice``, ``Session.decode_gpu`` ≙ ``TextModel::decode_gpu``. Errors raise
+``HtrError`` with the library's message (the reference's anyhow messages carry the same numbers).
+
+There is no fallback: without the built library every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhtr.so")
+
+MEM_WEIGHTS, MEM_KV_CACHE, MEM_WORK, MEM_READBACK = 0, 1, 2, 3
+
+# every symbol include/htr.h declares
+SYMBOLS = [
+    "htr_last_error", "htr_device_open", "htr_device_close", "htr_alive", "htr_set_fatal_hook", "htr_debug_mark_lost",
+    "htr_sync", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free", "htr_upload", "htr_download", "htr_phase",
+    "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
+    "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
+    "htr_choose_many", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
+    "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
+    "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
+]
+
+
+class HtrError(RuntimeError):
+    pass
+
+
+class GpuBytes(C.Structure):
+    _fields_ = [("weights", C.c_uint64), ("kv_cache", C.c_uint64), ("work", C.c_uint64), ("readback", C.c_uint64)]
+
+
+class TextConfigC(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("dim", C.c_int), ("n_head", C.c_int), ("n_kv", C.c_int), ("d_head", C.c_int),
+                ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx_train", C.c_int), ("eps", C.c_float),
+                ("rope_base", C.c_float)]
+
+
+class LayerTensorsC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm", "k_norm",
+                                          "ffn_norm")]
+
+
+class PresetC(C.Structure):
+    _fields_ = [("temperature", C.c_double), ("top_p", C.c_double), ("repetition_penalty", C.c_double),
+                ("frequency_penalty", C.c_double), ("repetition_window", C.c_size_t),
+                ("max_new_tokens", C.c_size_t)]
+
+
+FATAL_HOOK = C.CFUNCTYPE(None, C.c_char_p, C.c_char_p, C.c_void_p)
+TOKEN_CB = C.CFUNCTYPE(C.c_int, C.c_int32, C.c_void_p)
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libhtr.so (raises if it is not built: there is no other implementation)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HtrError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C historic-htr-ocr_amd)")
+        l = C.CDLL(LIB_PATH)
+        vp, sz, i32, f32 = C.c_void_p, C.c_size_t, C.c_int, C.c_float
+        pp = C.POINTER(C.c_void_p)
+        sig = {
+            "htr_last_error": (C.c_char_p, []),
+            "htr_device_open": (i32, [i32, pp]),
+            "htr_device_close": (i32, [vp]),
+            "htr_alive": (i32, [vp]),
+            "htr_set_fatal_hook": (i32, [vp, FATAL_HOOK, vp]),
+            "htr_debug_mark_lost": (i32, [vp, C.c_char_p]),
+            "htr_sync": (i32, [vp]),
+            "htr_device_info": (i32, [vp, C.c_char_p, sz, C.POINTER(i32)]),
+            "htr_timer_begin": (i32, [vp]),
+            "htr_timer_end": (i32, [vp, C.POINTER(f32)]),
+            "htr_mem_live": (i32, [vp, C.POINTER(GpuBytes)]),
+            "htr_alloc": (i32, [vp, sz, i32, pp]),
+            "htr_free": (i32, [vp, vp]),
+            "htr_upload": (i32, [vp, vp, vp, sz]),
+            "htr_download": (i32, [vp, vp, vp, sz]),
+            "htr_phase": (i32, [vp, C.c_char_p]),
+            "htr_weight_q8_0": (i32, [vp, vp, sz, sz, pp]),
+            "htr_weight_q8_0_f16": (i32, [vp, vp, sz, sz, f32, pp]),
+            "htr_weight_free": (i32, [vp]),
+            "htr_weight_shape": (i32, [vp, C.POINTER(sz), C.POINTER(sz)]),
+            "htr_matvec_q8_0": (i32, [vp, vp, vp, vp, f32, vp, i32]),
+            "htr_matvec_q8_0_many": (i32, [vp, C.POINTER(vp), sz, vp, vp]),
+            "htr_matvec_qkv": (i32, [vp, vp, vp, vp, vp, vp, f32, vp]),
+            "htr_matvec_ffn": (i32, [vp, vp, vp, vp, vp, f32, vp]),
+            "htr_qkv_post": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, vp, vp]),
+            "htr_decode_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
+            "htr_choose": (i32, [vp, vp, i32, vp, i32, i32, f32, f32, vp, vp, vp]),
+            "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),
+            "htr_text_model_create": (i32, [vp, C.POINTER(TextConfigC), vp, vp, C.POINTER(LayerTensorsC), pp]),
+            "htr_text_model_free": (i32, [vp]),
+            "htr_session_create": (i32, [vp, sz, pp]),
+            "htr_session_free": (i32, [vp]),
+            "htr_session_n_past": (i32, [vp, C.POINTER(sz)]),
+            "htr_prefill": (i32, [vp, vp, sz, vp]),
+            "htr_step": (i32, [vp, C.c_int32, vp]),
+            "htr_session_logits": (i32, [vp, vp]),
+            "htr_session_rewind": (i32, [vp, sz]),
+            "htr_choice_create": (i32, [vp, C.POINTER(PresetC), vp, sz, sz, sz, pp]),
+            "htr_choice_free": (i32, [vp]),
+            "htr_decode_gpu": (i32, [vp, vp, sz, TOKEN_CB, vp]),
+            "htr_synth_q8_0": (i32, [C.c_uint64, sz, sz, vp]),
+            "htr_synth_normal": (i32, [C.c_uint64, sz, f32, f32, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc < 0:
+        raise HtrError(lib().htr_last_error().decode(errors="replace"))
+
+
+def last_error() -> str:
+    return lib().htr_last_error().decode(errors="replace")
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data
+
+
+# ---- synthetic inputs ----------------------------------------------------------------------------------------------
+
+def synth_q8_0(seed: int, rows: int, cols: int) -> np.ndarray:
+    """GGUF q8_0 block bytes [rows·cols/32·34]: quants uniform in [−127, 127], d = f16(|N(0,1)|·0.002)."""
+    out = np.empty(rows * cols // 32 * 34, dtype=np.uint8)
+    _check(lib().htr_synth_q8_0(seed, rows, cols, _ptr(out)))
+    return out
+
+
+def synth_normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().htr_synth_normal(seed, n, mean, std, _ptr(out)))
+    return out
+
+
+# ---- device and memory ---------------------------------------------------------------------------------------------
+
+class Buffer:
+    """Device memory (gpu.rs Buf): ``ptr`` is the device address."""
+
+    def __init__(self, dev: "Device", nbytes: int, kind: int = MEM_WORK):
+        self.dev, self.nbytes = dev, nbytes
+        p = C.c_void_p()
+        _check(lib().htr_alloc(dev.h, nbytes, kind, C.byref(p)))
+        self.ptr = p.value
+
+    def upload(self, a: np.ndarray) -> "Buffer":
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError(f"{a.nbytes} bytes into a {self.nbytes}-byte buffer")
+        _check(lib().htr_upload(self.dev.h, self.ptr, _ptr(a), a.nbytes))
+        return self
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        _check(lib().htr_download(self.dev.h, _ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            _check(lib().htr_free(self.dev.h, self.ptr))
+            self.ptr = None
+
+
+class Device:
+    """One GPU (gpu.rs Gpu): the stream, the ledger, the sticky health."""
+
+    def __init__(self, ordinal: int = 0):
+        h = C.c_void_p()
+        _check(lib().htr_device_open(ordinal, C.byref(h)))
+        self.h = h.value
+        self._hook = None
+
+    def close(self) -> None:
+        if self.h:
+            lib().htr_device_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def alive(self) -> None:
+        _check(lib().htr_alive(self.h))
+
+    def sync(self) -> None:
+        _check(lib().htr_sync(self.h))
+
+    def info(self) -> tuple[str, int]:
+        name = C.create_string_buffer(256)
+        n_cu = C.c_int()
+        _check(lib().htr_device_info(self.h, name, 256, C.byref(n_cu)))
+        return name.value.decode(), n_cu.value
+
+    def timer_begin(self) -> None:
+        _check(lib().htr_timer_begin(self.h))
+
+    def timer_end(self) -> float:
+        """milliseconds since timer_begin, by HIP events on the library's stream"""
+        ms = C.c_float()
+        _check(lib().htr_timer_end(self.h, C.byref(ms)))
+        return ms.value
+
+    def mem_live(self) -> dict:
+        b = GpuBytes()
+        _check(lib().htr_mem_live(self.h, C.byref(b)))
+        return {"weights": b.weights, "kv_cache": b.kv_cache, "work": b.work, "readback": b.readback}
+
+    def set_fatal_hook(self, fn) -> None:
+        self._hook = FATAL_HOOK(lambda k, m, u: fn(k.decode(), m.decode()))
+        _check(lib().htr_set_fatal_hook(self.h, self._hook, None))
+
+    def mark_lost(self, why: str = "") -> None:
+        _check(lib().htr_debug_mark_lost(self.h, why.encode()))
+
+    def alloc(self, nbytes: int, kind: int = MEM_WORK) -> Buffer:
+        return Buffer(self, nbytes, kind)
+
+    def upload(self, a: np.ndarray, kind: int = MEM_WORK) -> Buffer:
+        a = np.ascontiguousarray(a)
+        return Buffer(self, max(a.nbytes, 4), kind).upload(a)
+
+
+class Weight:
+    """A q8_0 weight [rows × cols] repacked on the device (or dequantised to f16 with ``f16=True``)."""
+
+    def __init__(self, dev: Device, blocks: np.ndarray, rows: int, cols: int, f16: bool = False, scale: float = 1.0):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        if blocks.size != rows * cols // 32 * 34:
+            raise ValueError(f"{blocks.size} bytes for a [{rows} x {cols}] q8_0 tensor")
+        h = C.c_void_p()
+        if f16:
+            _check(lib().htr_weight_q8_0_f16(dev.h, _ptr(blocks), rows, cols, scale, C.byref(h)))
+        else:
+            _check(lib().htr_weight_q8_0(dev.h, _ptr(blocks), rows, cols, C.byref(h)))
+        self.dev, self.h, self.rows, self.cols = dev, h.value, rows, cols
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_weight_free(self.h)
+            self.h = None
+
+
+# ---- kernels on device buffers -------------------------------------------------------------------------------------
+
+def _p(b) -> int | None:
+    return None if b is None else b.ptr
+
+
+def matvec_q8_0(dev: Device, w: Weight, x: Buffer, y: Buffer, norm_w: Buffer | None = None, eps: float = 1e-6,
+                acc: bool = False) -> None:
+    _check(lib().htr_matvec_q8_0(dev.h, w.h, x.ptr, _p(norm_w), eps, y.ptr, int(acc)))
+
+
+def matvec_q8_0_many(dev: Device, ws: list[Weight], x: Buffer, y: Buffer) -> None:
+    arr = (C.c_void_p * len(ws))(*[w.h for w in ws])
+    _check(lib().htr_matvec_q8_0_many(dev.h, arr, len(ws), x.ptr, y.ptr))
+
+
+def matvec_qkv(dev: Device, wq: Weight, wk: Weight, wv: Weight, x: Buffer, norm_w: Buffer, eps: float,
+               qkv: Buffer) -> None:
+    _check(lib().htr_matvec_qkv(dev.h, wq.h, wk.h, wv.h, x.ptr, norm_w.ptr, eps, qkv.ptr))
+
+
+def matvec_ffn(dev: Device, wg: Weight, wu: Weight, x: Buffer, norm_w: Buffer, eps: float, g: Buffer) -> None:
+    _check(lib().htr_matvec_ffn(dev.h, wg.h, wu.h, x.ptr, norm_w.ptr, eps, g.ptr))
+
+
+def qkv_post(dev: Device, qkv: Buffer, q_norm: Buffer, k_norm: Buffer, rope: Buffer, n_head: int, n_kv: int, pos: int,
+             n_ctx: int, eps: float, kc: Buffer, vc: Buffer) -> None:
+    _check(lib().htr_qkv_post(dev.h, qkv.ptr, q_norm.ptr, k_norm.ptr, rope.ptr, n_head, n_kv, pos, n_ctx, eps, kc.ptr,
+                              vc.ptr))
+
+
+def decode_attention(dev: Device, q: Buffer, kc: Buffer, vc: Buffer, n_head: int, n_kv: int, n_ctx: int, n_keys: int,
+                     scale: float, out: Buffer) -> None:
+    _check(lib().htr_decode_attention(dev.h, q.ptr, kc.ptr, vc.ptr, n_head, n_kv, n_ctx, n_keys, scale, out.ptr))
+
+
+def choose(dev: Device, logits: Buffer, n_vocab: int, hist: Buffer, length: int, window: int, rp: float, tok: Buffer,
+           fp: float = 0.0, counts: Buffer | None = None, fpen: Buffer | None = None) -> None:
+    _check(lib().htr_choose(dev.h, logits.ptr, n_vocab, hist.ptr, length, window, rp, fp, _p(counts), _p(fpen),
+                            tok.ptr))
+
+
+def choose_many(dev: Device, logits: Buffer, n_vocab: int, n: int, hist: Buffer, hist_stride: int, length: int,
+                window: int, rp: float, tok: Buffer) -> None:
+    _check(lib().htr_choose_many(dev.h, logits.ptr, n_vocab, n, hist.ptr, hist_stride, length, window, rp, tok.ptr))
+
+
+# ---- the text decoder ----------------------------------------------------------------------------------------------
+
+@dataclass
+class TextConfig:
+    """text.rs:30-42 TextConfig."""
+    n_layer: int
+    dim: int
+    n_head: int
+    n_kv: int
+    d_head: int
+    n_ff: int
+    n_vocab: int
+    n_ctx_train: int = 0
+    eps: float = 1e-6
+    rope_base: float = 1e6
+
+    def c(self) -> TextConfigC:
+        return TextConfigC(self.n_layer, self.dim, self.n_head, self.n_kv, self.d_head, self.n_ff, self.n_vocab,
+                           self.n_ctx_train, self.eps, self.rope_base)
+
+
+@dataclass
+class Preset:
+    """ocr-decode presets.rs:17-29 (the fields the token choice reads)."""
+    repetition_penalty: float = 1.1
+    repetition_window: int = 64
+    frequency_penalty: float = 0.0
+    max_new_tokens: int = 512
+    temperature: float = 0.0
+    top_p: float = 1.0
+
+    def c(self) -> PresetC:
+        return PresetC(self.temperature, self.top_p, self.repetition_penalty, self.frequency_penalty,
+                       self.repetition_window, self.max_new_tokens)
+
+
+class TextModel:
+    """TextModel::load (text.rs:332-375) from host tensors: ``layers`` is a list of dicts with the q8_0 block bytes
+    (q, k, v, o, gate, up, down) and f32 norms (attn_norm, q_norm, k_norm, ffn_norm)."""
+
+    def __init__(self, dev: Device, cfg: TextConfig, tok_embd: np.ndarray, output_norm: np.ndarray,
+                 layers: list[dict]):
+        self.dev, self.cfg = dev, cfg
+        keep = []
+        arr = (LayerTensorsC * cfg.n_layer)()
+        for i, ly in enumerate(layers):
+            vals = {}
+            for name in ("q", "k", "v", "o", "gate", "up", "down"):
+                a = np.ascontiguousarray(ly[name], dtype=np.uint8)
+                keep.append(a)
+                vals[name] = _ptr(a)
+            for name in ("attn_norm", "q_norm", "k_norm", "ffn_norm"):
+                a = np.ascontiguousarray(ly[name], dtype=np.float32)
+                keep.append(a)
+                vals[name] = _ptr(a)
+            arr[i] = LayerTensorsC(**vals)
+        te = np.ascontiguousarray(tok_embd, dtype=np.uint8)
+        on = np.ascontiguousarray(output_norm, dtype=np.float32)
+        h = C.c_void_p()
+        cfg_c = cfg.c()
+        _check(lib().htr_text_model_create(dev.h, C.byref(cfg_c), _ptr(te), _ptr(on), arr, C.byref(h)))
+        self.h = h.value
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_text_model_free(self.h)
+            self.h = None
+
+    def session(self, n_ctx: int) -> "Session":
+        return Session(self, n_ctx)
+
+
+class Session:
+    """text.rs Session: the KV cache for n_ctx positions and the decode step's buffers."""
+
+    def __init__(self, m: TextModel, n_ctx: int):
+        h = C.c_void_p()
+        _check(lib().htr_session_create(m.h, n_ctx, C.byref(h)))
+        self.m, self.h, self.n_ctx = m, h.value, n_ctx
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_session_free(self.h)
+            self.h = None
+
+    @property
+    def n_past(self) -> int:
+        v = C.c_size_t()
+        _check(lib().htr_session_n_past(self.h, C.byref(v)))
+        return v.value
+
+    def prefill(self, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.m.cfg.n_vocab, dtype=np.float32)
+        _check(lib().htr_prefill(self.h, _ptr(ids), ids.size, _ptr(out)))
+        return out
+
+    def step(self, tok: int) -> np.ndarray:
+        out = np.empty(self.m.cfg.n_vocab, dtype=np.float32)
+        _check(lib().htr_step(self.h, int(tok), _ptr(out)))
+        return out
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.m.cfg.n_vocab, dtype=np.float32)
+        _check(lib().htr_session_logits(self.h, _ptr(out)))
+        return out
+
+    def rewind(self, n_past: int) -> None:
+        _check(lib().htr_session_rewind(self.h, n_past))
+
+    def choice(self, preset: Preset, history, chunk: int = 4, depth: int = 2) -> "Choice":
+        return Choice(self, preset, history, chunk, depth)
+
+    def decode_gpu(self, ch: "Choice", max_tokens: int, on_token=None) -> list[int]:
+        toks: list[int] = []
+
+        def cb(t, _u):
+            toks.append(int(t))
+            return 1 if on_token is None else int(bool(on_token(int(t))))
+
+        fn = TOKEN_CB(cb)
+        _check(lib().htr_decode_gpu(self.h, ch.h, max_tokens, fn, None))
+        return toks
+
+
+class Choice:
+    """text.rs Choice::new: the GPU token choice of a greedy preset."""
+
+    def __init__(self, s: Session, preset: Preset, history, chunk: int = 4, depth: int = 2):
+        hist = np.ascontiguousarray(history, dtype=np.int32)
+        h = C.c_void_p()
+        p = preset.c()
+        _check(lib().htr_choice_create(s.h, C.byref(p), _ptr(hist) if hist.size else None, hist.size, chunk, depth,
+                                       C.byref(h)))
+        self.s, self.h = s, h.value
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_choice_free(self.h)
+            self.h = None

@@ -1,0 +1,184 @@
+/*
+ * htr.h — the C ABI of the MI355X (gfx950) LightOnOCR decode path.
+ *
+ * This boundary stands where the reference engine's wgpu device / buffer / dispatch layer stands for this path
+ * (app/crates/ocr-wgpu/src/gpu.rs, the `Gpu` and `Batch` types) and under the decoder graph that drives it
+ * (app/crates/ocr-wgpu/src/text.rs). Its callers are the ones the reference layer has: the decoder (TextModel /
+ * Session / Choice), the vision encoder, and above them the engine's read loop (engine.rs read_text). Every entry point
+ * names the reference function it replaces (paths relative to the reference repository root; `gpu.rs`, `text.rs`,
+ * `vision.rs`, `engine.rs` are under app/crates/ocr-wgpu/src/).
+ *
+ * Conventions (gpu.rs:1391-1396, 884-897, text.rs:111-128):
+ *   - every function returns int: 0 = ok, < 0 = error; htr_last_error() gives the calling thread's last message, with
+ *     the numbers that failed (shape, limit, token id);
+ *   - a device whose GPU failed is dead for good (sticky): every later call on it fails with the FIRST reason, and the
+ *     fatal hook fires once;
+ *   - handles are opaque and freed explicitly; a model must outlive its sessions, a session its choices;
+ *   - device pointers (void* / float* named d_*) are device memory from htr_alloc; host pointers are named h_*;
+ *   - one thread uses a device at a time (the reference's Gpu is !Sync); callbacks run on the calling thread;
+ *   - all work is ordered on the device's one stream; the calls that return host data synchronise it.
+ */
+#ifndef HTR_H
+#define HTR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct htr_device htr_device;
+typedef struct htr_weight htr_weight;
+typedef struct htr_text_model htr_text_model;
+typedef struct htr_session htr_session;
+typedef struct htr_choice htr_choice;
+
+/* ---- errors ------------------------------------------------------------------------------------------------ */
+/* the calling thread's last error message ("" if none) */
+const char *htr_last_error(void);
+
+/* ---- device (gpu.rs:1101-1345 Gpu::with_compute / drop, gpu.rs:1386-1396 alive, gpu.rs:884-897 FatalHook) ----- */
+int htr_device_open(int ordinal, htr_device **out);
+int htr_device_close(htr_device *dev);
+/* 0 while the device is healthy; < 0 with the sticky reason once it is dead (gpu.rs:1386-1396 Gpu::alive) */
+int htr_alive(htr_device *dev);
+/* kind ∈ {"lost", "destroyed", "outOfMemory", "validation", "internal"} — called once, on the first failure */
+typedef void (*htr_fatal_hook)(const char *kind, const char *message, void *user);
+int htr_set_fatal_hook(htr_device *dev, htr_fatal_hook hook, void *user);
+/* the reference tests' device.destroy() (gpu.rs:2421-2448): marks the device lost from the host, no GPU fault */
+int htr_debug_mark_lost(htr_device *dev, const char *why);
+/* wait for the device's queue (gpu.rs:1458-1485 Gpu::wait) */
+int htr_sync(htr_device *dev);
+/* the device name and compute-unit count, for reports */
+int htr_device_info(htr_device *dev, char *name, size_t name_len, int *n_cu);
+/* HIP-event timing on the device's stream (measurement helpers, no reference counterpart — the reference's profiler
+ * is gpu.rs:1004-1016 timestamp queries): begin records the start event; end records the stop event, waits for it
+ * and returns the elapsed milliseconds */
+int htr_timer_begin(htr_device *dev);
+int htr_timer_end(htr_device *dev, float *ms);
+
+/* ---- memory (gpu.rs:509-561 ledger per MemKind; gpu.rs:1489-1590 upload / scratch / readback / read_f32) ------- */
+enum { HTR_MEM_WEIGHTS = 0, HTR_MEM_KV_CACHE = 1, HTR_MEM_WORK = 2, HTR_MEM_READBACK = 3 };
+typedef struct {
+    uint64_t weights, kv_cache, work, readback;
+} htr_gpu_bytes;
+int htr_mem_live(htr_device *dev, htr_gpu_bytes *out);
+/* device memory of `bytes` bytes counted under `kind`; freed by htr_free. Zero-filled. */
+int htr_alloc(htr_device *dev, size_t bytes, int kind, void **d_out);
+int htr_free(htr_device *dev, void *d_ptr);
+/* host ↔ device copies on the device's stream; htr_download waits for it */
+int htr_upload(htr_device *dev, void *d_dst, const void *h_src, size_t bytes);
+int htr_download(htr_device *dev, void *h_dst, const void *d_src, size_t bytes);
+/* a phase label for the profiler ranges (gpu.rs:1349-1358 Gpu::phase) */
+int htr_phase(htr_device *dev, const char *name);
+
+/* ---- weights (gpu.rs:1595-1677 upload_tensor with WeightType::Q8_0; text.rs:101-110 weight) -------------------- */
+/* a [rows × cols] q8_0 tensor from its GGUF block bytes (rows × cols/32 blocks of 34 bytes: f16 d LE + 32 × i8 q;
+ * ocr-gguf lib.rs:128-135). Repacked at load into an int8 plane [rows][cols] and an f16 scale plane [rows][cols/32]:
+ * every matvec lane then issues 16-byte loads of contiguous quants. cols must be a multiple of 32. */
+int htr_weight_q8_0(htr_device *dev, const void *h_blocks, size_t rows, size_t cols, htr_weight **out);
+/* the same weight dequantised to f16 (q·d rounded to nearest even) for the MFMA GEMMs (vision.rs:122-142: the
+ * reference converts its vision weights to f16 at load; scale multiplies every value first, as FFN_DOWN_SCALE) */
+int htr_weight_q8_0_f16(htr_device *dev, const void *h_blocks, size_t rows, size_t cols, float scale,
+                        htr_weight **out);
+int htr_weight_free(htr_weight *w);
+int htr_weight_shape(const htr_weight *w, size_t *rows, size_t *cols);
+
+/* ---- kernels on device buffers (gpu.rs:1864 Batch::dispatch of the named kernels) ------------------------------ */
+/* y[rows] (+)= W·x — dmv.wgsl (acc = 1 adds onto y); with d_norm_w != NULL the input is RMS-normed first
+ * (dmv_norm: x · 1/sqrt(mean(x²)+eps) · norm_w). gpu.rs:2094 Batch::matvec, text.rs:551-552, 642, 644 */
+int htr_matvec_q8_0(htr_device *dev, const htr_weight *w, const float *d_x, const float *d_norm_w, float eps,
+                    float *d_y, int acc);
+/* n matvecs y_i = W_i·x (one x, n weights of one shape, y [n][rows]) in ONE launch: the throughput of the matvec
+ * kernel over a rotation of weight copies larger than the Infinity Cache (no reference counterpart: a measurement
+ * entry) */
+int htr_matvec_q8_0_many(htr_device *dev, const htr_weight *const *ws, size_t n, const float *d_x, float *d_y);
+/* dmv_qkv.wgsl: attn_norm fused → [q | k | v] (text.rs:638) */
+int htr_matvec_qkv(htr_device *dev, const htr_weight *wq, const htr_weight *wk, const htr_weight *wv,
+                   const float *d_x, const float *d_norm_w, float eps, float *d_qkv);
+/* dmv_ffn.wgsl: ffn_norm fused → g = silu(Wg·xn)·(Wu·xn) (text.rs:643) */
+int htr_matvec_ffn(htr_device *dev, const htr_weight *wg, const htr_weight *wu, const float *d_x,
+                   const float *d_norm_w, float eps, float *d_g);
+/* qkv_post.wgsl (text.rs:639): per-head RMSNorm of q and k, RoPE NEOX at `pos` from the host table d_rope
+ * [n_pos][64] × (cos, sin) (text.rs:132-142), q written back in place, k and v stored f16 (RNE) into the head-major
+ * caches d_k / d_v [n_kv][n_ctx][128] at row pos. Head dim 128. */
+int htr_qkv_post(htr_device *dev, float *d_qkv, const float *d_q_norm, const float *d_k_norm, const float *d_rope,
+                 int n_head, int n_kv, int pos, int n_ctx, float eps, uint16_t *d_k, uint16_t *d_v);
+/* split-K GQA decode attention (attn_decode.wgsl + attn_merge.wgsl, text.rs:640-641): q [n_head·128] f32, the
+ * head-major f16 caches [n_kv][n_ctx][128], n_keys keys, scale → out [n_head·128] f32. GQA group 2. */
+int htr_decode_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v, int n_head,
+                         int n_kv, int n_ctx, int n_keys, float scale, float *d_out);
+/* the GPU token choice of a greedy preset on n_vocab logits (choose_pen → choose_max → choose_pick,
+ * text.rs:222-231; semantics of ocr-decode sampling.rs:38-62, bit-exact): the repetition penalty rp over the distinct
+ * ids of d_hist[len − window … len) applied in place (< 0: × rp, else ÷ rp, IEEE round-to-nearest), the frequency
+ * penalty (d_counts / d_fpen, both NULL when fp == 0) in the comparison, first maximum → d_tok[0] and d_hist[len].
+ * rp must be 1 or a positive normal f32 (text.rs:154-163). */
+int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_t *d_hist, int len, int window, float rp,
+               float fp, uint32_t *d_counts, float *d_fpen, uint32_t *d_tok);
+/* the same choice for n independent rows (logits [n][n_vocab], histories [n][hist_stride], tok[n]) in ONE launch:
+ * the 10k-step measurement of the choice kernel (no reference counterpart) */
+int htr_choose_many(htr_device *dev, float *d_logits, int n_vocab, int n, uint32_t *d_hist, int hist_stride, int len,
+                    int window, float rp, uint32_t *d_tok);
+
+/* ---- the text decoder (text.rs:30-130 TextConfig / TextModel, text.rs:332-375 load) ------------------------------ */
+typedef struct {
+    int n_layer, dim, n_head, n_kv, d_head, n_ff, n_vocab, n_ctx_train;
+    float eps, rope_base;
+} htr_text_config;
+
+/* one layer's tensors as host bytes: q8_0 GGUF blocks for the projections, f32 for the norms (text.rs:82-94) */
+typedef struct {
+    const void *q, *k, *v, *o, *gate, *up, *down;
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm;
+} htr_layer_tensors;
+
+/* TextModel::load (text.rs:332-375): same shape checks (d_head 128, q8_0 rows of whole blocks, GQA group 2) */
+int htr_text_model_create(htr_device *dev, const htr_text_config *cfg, const void *tok_embd, const float *output_norm,
+                          const htr_layer_tensors *layers, htr_text_model **out);
+int htr_text_model_free(htr_text_model *m);
+
+/* TextModel::session (text.rs:378-434): n_ctx positions (prompt + new tokens); the KV cache is sized once to n_ctx */
+int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out);
+int htr_session_free(htr_session *s);
+/* positions recorded so far (Session::n_past) */
+int htr_session_n_past(htr_session *s, size_t *out);
+/* TextModel::prefill (text.rs:437-521): ids at positions n_past …; the last row's logits → h_logits (may be NULL) */
+int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *h_logits);
+/* TextModel::step (text.rs:524-537), the CPU-choice path: one token at n_past → its logits into h_logits */
+int htr_step(htr_session *s, int32_t tok, float *h_logits);
+/* the session's last logits (after prefill / step / a GPU choice: penalised in place) → h_logits */
+int htr_session_logits(htr_session *s, float *h_logits);
+/* forget the positions ≥ n_past (≤ the current n_past): later steps rewrite their KV rows. No reference counterpart
+ * (a read's session only grows, text.rs:242-328); it lets a bench replay one read's decode */
+int htr_session_rewind(htr_session *s, size_t n_past);
+
+/* ---- the GPU token choice and the run-ahead decode (text.rs:165-232 Choice, text.rs:587-625 decode_gpu) -------- */
+/* the preset fields the choice reads (ocr-decode presets.rs:17-29) */
+typedef struct {
+    double temperature, top_p, repetition_penalty, frequency_penalty;
+    size_t repetition_window, max_new_tokens;
+} htr_preset;
+/* Choice::new (text.rs:185-218): greedy presets only, rp 1 or a positive normal f32 (gpu_choice_capable,
+ * text.rs:154-163), the history's last `window` ids seed the window (each inside the vocabulary), `chunk` choices per
+ * graph launch (1…64), `depth` launches in flight (≥ 1) */
+int htr_choice_create(htr_session *s, const htr_preset *p, const int32_t *history, size_t n, size_t chunk,
+                      size_t depth, htr_choice **out);
+int htr_choice_free(htr_choice *c);
+/* 0 ⇒ stop the read; nonzero ⇒ go on */
+typedef int (*htr_token_cb)(int32_t tok, void *user);
+/* TextModel::decode_gpu (text.rs:587-625): up to max choices, the first from the session's logits, each later one
+ * after a decode step that embeds the previous choice on the device. Steps are replayed as HIP graphs, `chunk` per
+ * launch, `depth` launches in flight; 4 bytes per token come back. on_token returning 0 ends the read. */
+int htr_decode_gpu(htr_session *s, htr_choice *c, size_t max, htr_token_cb on_token, void *user);
+
+/* ---- seeded synthetic inputs (host-side data generation for tests and benches; not on the decode path) ------- */
+/* q8_0 GGUF blocks: quants uniform in [−127, 127], d = f16(|N(0,1)|·0.002), from (seed, block index) */
+int htr_synth_q8_0(uint64_t seed, size_t rows, size_t cols, void *h_blocks);
+/* f32 values mean + std·N(0,1) from (seed, index) */
+int htr_synth_normal(uint64_t seed, size_t n, float mean, float std, float *h_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

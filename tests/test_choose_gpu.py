@@ -1,0 +1,128 @@
+"""The GPU token choice (windowed repetition penalty + two-pass argmax) — bit-exact against the oracle's restatement
+of ocr-decode's `choose` (sampling.rs:38-62)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import htr
+import oracle as orc
+from test_oracle import gpu_choice_matrix_inputs
+
+pytestmark = pytest.mark.gpu
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_cases.json")))
+
+
+def test_choice_matches_choose_on_reference_matrix(dev):
+    """text.rs:1001-1054: the real and odd vocabularies; rp off / > 1 / < 1; windows 1 … 64; fp 0 and > 0; ties,
+    ±0, −inf, all −inf; a dominant last token the penalties push down. The GPU keeps its own history and counts."""
+    for case in GOLD["gpu_choice_matrix"]["cases"]:
+        n_vocab, rp, window, fp, seed_hist = case
+        steps = GOLD["gpu_choice_matrix"]["steps"]
+        hist = dev.upload(np.array(list(seed_hist) + [0] * (steps + 1), np.uint32))
+        counts = dev.alloc(n_vocab * 4) if fp > 0 else None
+        fpen = dev.alloc(n_vocab * 4) if fp > 0 else None
+        tok = dev.alloc(4)
+        lb = dev.alloc(n_vocab * 4)
+        chosen = []
+        for i, (l, history, cnt, want) in enumerate(gpu_choice_matrix_inputs(case)):
+            lb.upload(l)
+            htr.choose(dev, lb, n_vocab, hist, len(seed_hist) + i, window, rp, tok, fp, counts, fpen)
+            got = int(tok.download(np.uint32)[0])
+            ref = l.copy()
+            assert orc.choose(ref, rp, window, fp, history, cnt) == want
+            assert got == want, f"vocab {n_vocab} rp {rp} window {window} fp {fp} step {i}"
+            if fp == 0:  # the penalised logits, in place, bit for bit
+                assert np.array_equal(lb.download(np.float32).view(np.uint32), ref.view(np.uint32)), i
+            chosen.append(want)
+        h = hist.download(np.uint32)
+        assert h[len(seed_hist):len(seed_hist) + steps].tolist() == chosen
+
+
+def test_choose_penalty_is_ieee_exact(dev):
+    """text.rs:1061-1099, stricter: subnormal products compared too"""
+    c = GOLD["choose_pen_exact"]
+    n = c["n"]
+    bits = orc.Lcg(c["seed"]).bits(n).astype(np.uint64)
+    raw = np.where(np.arange(n) % 3 == 2, (0x0D800000 + bits % (0x7F000000 - 0x0D800000)) | 0x80000000,
+                   bits % 0x7F800000).astype(np.uint32)
+    raw[:6] = c["special_bits"]
+    l0 = raw.view(np.float32)
+    hist = dev.upload(np.arange(n + 1, dtype=np.uint32))
+    tok = dev.alloc(4)
+    for rp in c["rp"]:
+        lb = dev.upload(l0)
+        htr.choose(dev, lb, n, hist, n, n, rp, tok)
+        r = np.float32(rp)
+        with np.errstate(under="ignore", over="ignore"):
+            want = np.where(l0 < 0, l0 * r, l0 / r)
+        assert np.array_equal(lb.download(np.float32).view(np.uint32), want.view(np.uint32)), rp
+        lb.free()
+
+
+def config1_inputs(seed: int, rows: int, n_vocab: int = 151936, window: int = 64):
+    """config 1: logits N(0, 3) + 8 planted equal maxima (3 of them on window ids, so the penalty reverses them),
+    history = 64 ids uniform over the vocabulary with 25 % repeats"""
+    logits = np.empty((rows, n_vocab), np.float32)
+    hist = np.empty((rows, window), np.int32)
+    for r in range(rows):
+        l = htr.synth_normal(seed * 100003 + r, n_vocab, 0.0, 3.0)
+        u = htr.synth_normal(seed * 100003 + r + 7 * rows + 11, 3 * window, 0.0, 1.0)
+        frac = (u - np.floor(u)).astype(np.float64)
+        fresh = (np.abs(u[:window]) * 1e6).astype(np.int64) % n_vocab
+        h = fresh.copy()
+        rep = np.arange(window)[frac[window:2 * window] < 0.25]
+        for j in rep[rep > 0]:
+            h[j] = h[int(frac[2 * window + j] * j)]
+        planted = (np.abs(u[2 * window - 8:2 * window]) * 7e5).astype(np.int64) % n_vocab
+        planted[:3] = h[[1, 17, 40]]
+        l[planted] = l.max() + np.float32(1.0)
+        logits[r] = l
+        hist[r] = h
+    return logits, hist
+
+
+def test_config1_choice_bit_exact(dev):
+    """config 1 at full size: 64 independent rows in one launch and 16 single launches, each against the oracle"""
+    rows, n_vocab, window, rp = 64, 151936, 64, 1.1
+    logits, hist = config1_inputs(1, rows)
+    hb = dev.upload(np.concatenate([hist, np.zeros((rows, 1), np.int32)], axis=1).astype(np.uint32))
+    lb = dev.upload(logits)
+    tok = dev.alloc(rows * 4)
+    htr.choose_many(dev, lb, n_vocab, rows, hb, window + 1, window, window, rp, tok)
+    got = tok.download(np.uint32)
+    pen = lb.download(np.float32).reshape(rows, n_vocab)
+    for r in range(rows):
+        ref = logits[r].copy()
+        want = orc.choose(ref, rp, window, 0.0, hist[r])
+        assert int(got[r]) == want, r
+        assert np.array_equal(pen[r].view(np.uint32), ref.view(np.uint32)), r
+    h = hb.download(np.uint32).reshape(rows, window + 1)
+    assert np.array_equal(h[:, window], got)
+    # single launches
+    one = dev.alloc(n_vocab * 4)
+    h1 = dev.alloc((window + 1) * 4)
+    for r in range(16):
+        one.upload(logits[r])
+        h1.upload(hist[r].astype(np.uint32))
+        htr.choose(dev, one, n_vocab, h1, window, window, rp, tok)
+        assert int(tok.download(np.uint32)[0]) == int(got[r])
+
+
+def test_choose_nan_rules(dev):
+    tok = dev.alloc(4)
+    hist = dev.upload(np.zeros(4, np.uint32))
+    for l, want in (([np.nan, 3.0, 5.0], 0), ([1.0, np.nan, 5.0], 2), ([-np.inf] * 5, 0), ([np.nan] * 3, 0)):
+        a = np.array(l, np.float32)
+        assert orc.choose(a.copy(), 1.0, 1, 0.0, []) == want
+        htr.choose(dev, dev.upload(a), a.size, hist, 0, 1, 1.0, tok)
+        assert int(tok.download(np.uint32)[0]) == want, l
+
+
+def test_choose_rejects_bad_penalty(dev):
+    tok = dev.alloc(4)
+    with pytest.raises(htr.HtrError, match="repetition penalty"):
+        htr.choose(dev, dev.alloc(16), 4, dev.alloc(16), 1, 1, 0.0, tok)
+    with pytest.raises(htr.HtrError, match="repetition penalty"):
+        htr.choose(dev, dev.alloc(16), 4, dev.alloc(16), 1, 1, 1e-40, tok)

@@ -1,0 +1,183 @@
+"""The text decoder on the GPU: prefill, the CPU-choice step and the run-ahead GPU-choice decode, against the oracle.
+
+Token identity is checked teacher-forced: at every position the oracle computes its own logits from the tokens the GPU
+chose so far and makes its own choice; a differing token is accepted only as a documented near-tie (the oracle's
+logits of the two tokens within 1e-6 relative). Float logits: rel-L2 against the oracle's f32 restatement."""
+import numpy as np
+import pytest
+
+import htr
+import oracle as orc
+from helpers import near_tie, rel_l2, synth_text_model, tiny_prompt, tiny_text_model, to_htr_cfg
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(dev):
+    cfg, te, on, layers = tiny_text_model()
+    m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    yield cfg, te, on, layers, m
+    m.free()
+
+
+def teacher_forced(o: orc.Session, first_logits, prompt, toks, rp, window, tie_log):
+    """the oracle's choice at every position given the GPU's earlier tokens; returns the number of near-ties"""
+    lo = first_logits
+    hist = [int(t) for t in prompt]
+    for i, t in enumerate(toks):
+        pen = lo.copy()
+        want = orc.choose(pen, rp, window, 0.0, hist)
+        if want != t:
+            assert near_tie(pen, want, t), f"step {i}: oracle {want} ({pen[want]!r}), GPU {t} ({pen[t]!r})"
+            tie_log.append((i, want, t))
+        hist.append(int(t))
+        if i + 1 < len(toks):
+            lo = o.step(int(t))
+
+
+def test_tiny_prefill_and_steps_match_oracle(dev, tiny):
+    """the reference's tiny model (text.rs:1297-1323) and prompt (text.rs:1333): prefill logits, then 40 greedy
+    CPU-choice steps (TextModel::step), every logits row against the oracle's"""
+    cfg, te, on, layers, m = tiny
+    prompt = tiny_prompt()
+    s = m.session(prompt.size + 150)
+    o = orc.Session(cfg, te, on, layers, prompt.size + 150)
+    lg, lo = s.prefill(prompt), o.prefill(prompt)
+    assert rel_l2(lg, lo) < 1e-5
+    assert s.n_past == prompt.size
+    for i in range(40):
+        t = int(np.argmax(lg))
+        lo_t = int(np.argmax(lo))
+        assert t == lo_t or near_tie(lo, lo_t, t), i
+        lg, lo = s.step(t), o.step(t)
+        assert rel_l2(lg, lo) < 1e-5, i
+    assert s.n_past == prompt.size + 40
+    s.free()
+
+
+def test_tiny_decode_gpu_matches_oracle_and_is_chunk_invariant(dev, tiny):
+    """text.rs:1366-1377: the GPU choice run ahead (4 × 2 in flight) for 150 tokens with rp 1.1 / window 20; the same
+    tokens for other chunk / depth settings and for the CPU-choice path with the oracle's choose on the GPU logits"""
+    cfg, te, on, layers, m = tiny
+    prompt = tiny_prompt()
+    n_new = 150
+    preset = htr.Preset(repetition_penalty=1.1, repetition_window=20, max_new_tokens=n_new)
+    runs = {}
+    for chunk, depth in ((4, 2), (1, 1), (16, 3), (64, 1)):
+        s = m.session(prompt.size + n_new)
+        s.prefill(prompt)
+        ch = s.choice(preset, prompt, chunk, depth)
+        runs[(chunk, depth)] = s.decode_gpu(ch, n_new)
+        assert len(runs[(chunk, depth)]) == n_new
+        assert s.n_past == prompt.size + n_new - 1  # the last choice needs no row
+        ch.free()
+        s.free()
+    first = runs[(4, 2)]
+    for k, v in runs.items():
+        assert v == first, k
+    # the CPU-choice path: GPU logits, the oracle's (bit-exact) choose on them
+    s = m.session(prompt.size + n_new)
+    lg = s.prefill(prompt)
+    hist, toks = list(prompt), []
+    for i in range(n_new):
+        t = orc.choose(lg.copy(), 1.1, 20, 0.0, hist)
+        toks.append(t)
+        hist.append(t)
+        if i + 1 < n_new:
+            lg = s.step(t)
+    assert toks == first
+    s.free()
+    # teacher-forced against the oracle's own logits
+    o = orc.Session(cfg, te, on, layers, prompt.size + n_new)
+    ties = []
+    teacher_forced(o, o.prefill(prompt), prompt, first, 1.1, 20, ties)
+    print(f"\n[tiny decode] {n_new} tokens, near-ties: {ties}")
+
+
+def test_decode_gpu_stops_when_the_callback_says_so(dev, tiny):
+    cfg, te, on, layers, m = tiny
+    prompt = tiny_prompt()
+    s = m.session(prompt.size + 64)
+    s.prefill(prompt)
+    ch = s.choice(htr.Preset(max_new_tokens=64), prompt, 4, 2)
+    seen = []
+    got = s.decode_gpu(ch, 64, lambda t: (seen.append(t), len(seen) < 10)[1])
+    assert len(got) == 10 and got == seen
+    with pytest.raises(htr.HtrError, match="history holds"):
+        s.decode_gpu(ch, 65)
+    ch.free()
+    s.free()
+
+
+def test_model_and_session_errors(dev, tiny):
+    cfg, te, on, layers, m = tiny
+    with pytest.raises(htr.HtrError, match="trained on"):
+        m.session(5000)
+    s = m.session(8)
+    with pytest.raises(htr.HtrError, match="outside the vocabulary"):
+        s.prefill([1, 1000])
+    with pytest.raises(htr.HtrError, match="overflow"):
+        s.prefill(list(range(9)))
+    with pytest.raises(htr.HtrError, match="empty prompt"):
+        s.prefill([])
+    with pytest.raises(htr.HtrError, match="temperature"):
+        s.choice(htr.Preset(temperature=0.7), [])
+    with pytest.raises(htr.HtrError, match="positive normal"):
+        s.choice(htr.Preset(repetition_penalty=1e-45), [])
+    with pytest.raises(htr.HtrError, match="run-ahead"):
+        s.choice(htr.Preset(), [], 65, 1)
+    s.free()
+    bad = dict(cfg, d_head=64)
+    with pytest.raises(htr.HtrError, match="head dim"):
+        htr.TextModel(dev, to_htr_cfg(bad), te, on, layers)
+
+
+def test_full_size_decoder_matches_oracle(dev):
+    """config 3's model shape (28 layers, dim 1024, 16 / 8 heads, ffn 3072, vocab 151936, tied head) with a 64-token
+    prompt and 24 greedy tokens (rp 1.1, window 64): prefill logits and the decode teacher-forced against the oracle"""
+    cfg, te, on, layers = synth_text_model()
+    m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    prompt = (np.abs(htr.synth_normal(77, 64)) * 1e5).astype(np.int64) % cfg["n_vocab"]
+    n_new = 24
+    s = m.session(prompt.size + n_new)
+    lg = s.prefill(prompt)
+    o = orc.Session(cfg, te, on, layers, prompt.size + n_new)
+    lo = o.prefill(prompt)
+    e = rel_l2(lg, lo)
+    print(f"\n[full prefill] rel-L2 vs oracle {e:.2e}")
+    assert e < 1e-4
+    ch = s.choice(htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new), prompt, 8, 2)
+    toks = s.decode_gpu(ch, n_new)
+    ties = []
+    teacher_forced(o, lo, prompt, toks, 1.1, 64, ties)
+    print(f"[full decode] tokens {toks[:8]}…, near-ties {ties}")
+    ch.free()
+    s.free()
+    m.free()
+
+
+def test_device_health_is_sticky():
+    """gpu.rs:900-961 / 2421-2448: a device marked lost fails every later call with the first reason; the hook
+    fires once; an impossible allocation latches outOfMemory (no GPU fault either way)"""
+    fired = []
+    d = htr.Device(0)
+    d.set_fatal_hook(lambda k, m: fired.append((k, m)))
+    d.alive()
+    with pytest.raises(htr.HtrError):
+        d.alloc(1 << 60)
+    assert fired and fired[0][0] == "outOfMemory"
+    with pytest.raises(htr.HtrError, match="outOfMemory"):
+        d.alive()
+    with pytest.raises(htr.HtrError, match="outOfMemory"):
+        d.alloc(16)
+    assert len(fired) == 1
+    d.close()
+    d = htr.Device(0)
+    d.set_fatal_hook(lambda k, m: fired.append((k, m)))
+    d.mark_lost("test: device.destroy()")
+    for _ in range(2):
+        with pytest.raises(htr.HtrError, match="device.destroy"):
+            d.sync()
+    assert fired[-1] == ("destroyed", "test: device.destroy()") and len(fired) == 2
+    d.close()
