@@ -27,7 +27,6 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "historic-htr-ocr_amd"))
-sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 import htr  # noqa: E402
 
@@ -40,14 +39,14 @@ def log(msg: str) -> None:
 
 
 def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
-    from helpers import synth_text_model, to_htr_cfg
+    from htr import synth
 
     t = time.time()
-    cfg, te, on, layers = synth_text_model()
+    cfg, te, on, layers = synth.text_model()
     log(f"decoder weights generated ({time.time() - t:.1f} s)")
-    m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    m = htr.TextModel(dev, htr.TextConfig(**cfg), te, on, layers)
     log("decoder weights uploaded")
-    prompt = (np.abs(htr.synth_normal(4242, prompt_len)) * 1e5).astype(np.int64) % cfg["n_vocab"]
+    prompt = synth.prompt_ids(4242, prompt_len, cfg["n_vocab"])
     s = m.session(prompt_len + n_new)
     dev.sync()
     t0 = time.perf_counter()
@@ -205,12 +204,17 @@ def bench_attention(dev, n_head=16, n_kv=8):
 
 def cpu_baseline(model_inputs, budget_s=12.0):
     """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores"""
+    # the oracle is the checker: imported here, for the CPU baseline leg only
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as orc
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("htr_oracle_py", os.path.join(ROOT, "oracle", "oracle.py"))
+    orc = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(orc)
 
     cfg, te, on, layers, prompt = model_inputs
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    o = orc.Session(cfg, te, on, layers, 64)
+    o = orc.Session(cfg, te, on, layers, 32 + 48 + 1)
     lo = o.prefill(prompt[:32])
     hist = [int(t) for t in prompt[:32]]
     t0 = time.perf_counter()

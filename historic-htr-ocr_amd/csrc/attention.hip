@@ -41,6 +41,7 @@ __global__ __launch_bounds__(64) void k_qkv_post(float *qkv, const float *qn, co
                                                  float eps, _Float16 *kc, _Float16 *vc) {
     const int h = blockIdx.x, lane = threadIdx.x;
     const int pos = pos_dev ? *pos_dev : pos_arg;
+    if (pos < 0 || pos >= n_ctx) return;  // the cache has no such row (the host checks positions first)
     float *x = qkv + (size_t)h * D;
     float x0 = x[lane], x1 = x[lane + 64];
     if (h >= n_head + n_kv) {
@@ -91,169 +92,243 @@ __global__ __launch_bounds__(64) void k_qk_rows(float *q, float *k, const float 
 
 // ---- split-K decode attention -----------------------------------------------------------------------------------------
 //
-// grid (chunks, n_kv), 256 threads = 4 waves. A workgroup takes `chunk` keys of one KV head and both of its q heads
-// (GQA group 2): every K / V byte is read once. Within a wave, 16 lanes share a key (8 dims = 16 bytes each), so a
-// wave reads 4 keys (1 KiB) per load instruction.
-//   1. scores s[h][t] = (q_h·scale)·k_t      → LDS
-//   2. m = max s, e = exp(s − m), l = Σ e     (per head, over the chunk)
-//   3. o[h][·] = Σ_t e[h][t]·v_t              → lane partials, summed across the wave's 4 key groups and the 4 waves
-//      in LDS
-//   4. the chunk's (m, l, o) → part; the last workgroup of the KV head (atomic ticket) merges every chunk's partials
-//      in LDS: M = max m_c, L = Σ l_c e^(m_c − M), O = Σ o_c e^(m_c − M) / L — no second launch.
+// grid (chunks, n_kv), 256 threads. A workgroup takes C = 16·NI keys of one KV head and both of its q heads (GQA
+// group 2), so every K / V byte is read once. Thread t owns the 16-byte slice j = t & 15 (dims 8j … 8j+7) of the keys
+// kk + 16·i (kk = t >> 4, i < NI): one wave-wide load reads 4 keys (1 KiB), and every K and V load of the chunk is
+// issued before the first use.
+//   1. scores s[h][key] = (q_h·scale)·k: 8 products per slice, summed over the 16 slices of a key by an
+//      exchange-and-halve butterfly over all 2·NI (key, head) values at once → LDS
+//   2. per head (one wave each): m = max s, p = exp(s − m), l = Σ p → LDS
+//   3. o[h][·] = Σ p·v from the V registers, summed over the 16 key positions (lanes, then the 4 waves in LDS)
+//   4. the chunk's (m, l, o) → partials [h][c][130]; the last workgroup of the KV head (atomic ticket) merges:
+//      M = max m_c, w_c = e^(m_c − M), O = Σ o_c·w_c / Σ l_c·w_c, every thread issuing its loads of all chunks at
+//      once. A single-chunk call writes O = o / l directly.
 constexpr int AW = 256;
-constexpr int MAX_CHUNK_KEYS = 256;
+constexpr int MAX_CHUNK_KEYS = 256;  // C ≤ 256 (NI ≤ 16)
+constexpr int MAX_CHUNKS = 256;      // chunks per KV head: n_ctx ≤ 65536
+constexpr int MERGE_PREFETCH = 64;   // chunk partials each merging thread holds in registers before the loop
 
+__device__ __forceinline__ int4 aload16(const void *p) { return *reinterpret_cast<const int4 *>(p); }
+
+__device__ __forceinline__ void unpack8(const int4 w, float (&f)[8]) {
+    const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        _Float16 lo, hi;
+        const uint16_t a = (uint16_t)(u[i] & 0xffff), b = (uint16_t)(u[i] >> 16);
+        __builtin_memcpy(&lo, &a, 2);
+        __builtin_memcpy(&hi, &b, 2);
+        f[2 * i] = (float)lo;
+        f[2 * i + 1] = (float)hi;
+    }
+}
+
+// exchange-and-halve over the lane bits of `masks` (high to low): v[0 … N) of every lane → each lane keeps N / 2^S
+// sums over the 2^S lanes that differ in those bits; lane bit (mask) set keeps the upper half at each step.
+template <int N, int M0, int S> __device__ __forceinline__ void halve(float (&v)[N], int lane) {
+#pragma unroll
+    for (int s = 0, n = N / 2, m = M0; s < S; s++, n >>= 1, m >>= 1) {
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; i++) {
+            if (i < n) {
+                const float send = hi ? v[i] : v[i + n];
+                const float keep = hi ? v[i + n] : v[i];
+                v[i] = keep + __shfl_xor(send, m, 64);
+            }
+        }
+    }
+}
+
+template <int NI>
 __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float16 *kc, const _Float16 *vc, int n_kv,
-                                                    int n_ctx, const int *pos_dev, int n_keys_arg, int chunk,
-                                                    int max_chunk, float scale, float *part, uint32_t *counters,
-                                                    float *out) {
-    __shared__ float s_sc[2][MAX_CHUNK_KEYS];
-    __shared__ float s_red[2][4];
+                                                    int n_ctx, const int *pos_dev, int n_keys_arg, int max_chunk,
+                                                    float scale, float *part, uint32_t *counters, float *out) {
+    constexpr int C = 16 * NI;
+    constexpr int N = 2 * NI;  // (key, head) values per thread
+    __shared__ float s_p[2][C];
+    __shared__ float s_ml[2][2];
     __shared__ float s_o[4][2][D];
+    __shared__ float s_w[2][MAX_CHUNKS];
+    __shared__ float s_red[2][4];
     __shared__ int s_last;
     const int c = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n_keys = pos_dev ? *pos_dev + 1 : n_keys_arg;
-    const int n_chunk = (n_keys + chunk - 1) / chunk;
-    if (c >= n_chunk) return;  // uniform per workgroup
-    const int k0 = c * chunk;
-    const int nk = min(chunk, n_keys - k0);
+    const int j = tid & 15, kk = tid >> 4;
+    // keys beyond the cache are never read (the host checks positions first; a bad one yields no output)
+    const int n_keys = min(pos_dev ? *pos_dev + 1 : n_keys_arg, n_ctx);
+    const int n_chunk = (n_keys + C - 1) / C;
+    if (c >= n_chunk || n_chunk > max_chunk) return;  // uniform per workgroup
+    const int k0 = c * C;
     const int h0 = 2 * kvh;
-    const int j = lane & 15, grp = lane >> 4;  // dims 8j … 8j+7; key group within the wave
 
-    // 1. scores
+    // 0. every K and V load of the chunk (keys past n_keys read the last key and are masked)
+    const _Float16 *kb = kc + (size_t)kvh * n_ctx * D, *vb = vc + (size_t)kvh * n_ctx * D;
+    int4 kr[NI], vr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int key = min(k0 + kk + 16 * i, n_keys - 1);
+        kr[i] = aload16(kb + (size_t)key * D + 8 * j);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int key = min(k0 + kk + 16 * i, n_keys - 1);
+        vr[i] = aload16(vb + (size_t)key * D + 8 * j);
+    }
     float qa[8], qb[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         qa[e] = q[h0 * D + 8 * j + e] * scale;
         qb[e] = q[(h0 + 1) * D + 8 * j + e] * scale;
     }
-    const _Float16 *kbase = kc + ((size_t)kvh * n_ctx + k0) * D;
-    for (int t0 = wave * 4; t0 < nk; t0 += 16) {
-        const int t = t0 + grp;
+
+    // 1. scores
+    float v[N];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        float kf[8];
+        unpack8(kr[i], kf);
         float da = 0.0f, db = 0.0f;
-        if (t < nk) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(kbase + (size_t)t * D + 8 * j);
-            const _Float16 *kh = reinterpret_cast<const _Float16 *>(&w);
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float kv = (float)kh[e];
-                da = fmaf(qa[e], kv, da);
-                db = fmaf(qb[e], kv, db);
-            }
-        }
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) {
-            da += __shfl_xor(da, off, 64);
-            db += __shfl_xor(db, off, 64);
-        }
-        if (j == 0 && t < nk) {
-            s_sc[0][t] = da;
-            s_sc[1][t] = db;
-        }
-    }
-    __syncthreads();
-
-    // 2. max, exp, sum per head (threads over keys)
-    float ma = -INFINITY, mb = -INFINITY;
-    for (int t = tid; t < nk; t += AW) {
-        ma = fmaxf(ma, s_sc[0][t]);
-        mb = fmaxf(mb, s_sc[1][t]);
-    }
-    ma = wave_max(ma);
-    mb = wave_max(mb);
-    if (lane == 0) {
-        s_red[0][wave] = ma;
-        s_red[1][wave] = mb;
-    }
-    __syncthreads();
-    ma = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
-    mb = fmaxf(fmaxf(s_red[1][0], s_red[1][1]), fmaxf(s_red[1][2], s_red[1][3]));
-    __syncthreads();
-    float la = 0.0f, lb = 0.0f;
-    for (int t = tid; t < nk; t += AW) {
-        const float ea = expf(s_sc[0][t] - ma), eb = expf(s_sc[1][t] - mb);
-        s_sc[0][t] = ea;
-        s_sc[1][t] = eb;
-        la += ea;
-        lb += eb;
-    }
-    la = wave_sum(la);
-    lb = wave_sum(lb);
-    if (lane == 0) {
-        s_red[0][wave] = la;
-        s_red[1][wave] = lb;
-    }
-    __syncthreads();
-    la = (s_red[0][0] + s_red[0][1]) + (s_red[0][2] + s_red[0][3]);
-    lb = (s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]);
-
-    // 3. values
-    float oa[8], ob[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) oa[e] = ob[e] = 0.0f;
-    const _Float16 *vbase = vc + ((size_t)kvh * n_ctx + k0) * D;
-    for (int t0 = wave * 4; t0 < nk; t0 += 16) {
-        const int t = t0 + grp;
-        if (t < nk) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(vbase + (size_t)t * D + 8 * j);
-            const _Float16 *vh = reinterpret_cast<const _Float16 *>(&w);
-            const float ea = s_sc[0][t], eb = s_sc[1][t];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float vv = (float)vh[e];
-                oa[e] = fmaf(ea, vv, oa[e]);
-                ob[e] = fmaf(eb, vv, ob[e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        oa[e] += __shfl_xor(oa[e], 16, 64);
-        oa[e] += __shfl_xor(oa[e], 32, 64);
-        ob[e] += __shfl_xor(ob[e], 16, 64);
-        ob[e] += __shfl_xor(ob[e], 32, 64);
-    }
-    if (grp == 0) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            s_o[wave][0][8 * j + e] = oa[e];
-            s_o[wave][1][8 * j + e] = ob[e];
+            da = fmaf(qa[e], kf[e], da);
+            db = fmaf(qb[e], kf[e], db);
+        }
+        v[2 * i] = da;
+        v[2 * i + 1] = db;
+    }
+    if (N >= 16) {
+        halve<N, 8, 4>(v, lane);  // lane j keeps values (N/16)·j + r
+#pragma unroll
+        for (int r = 0; r < (N >= 16 ? N / 16 : 1); r++) {
+            const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
+            const int key = kk + 16 * i;
+            s_p[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
+        }
+    } else {
+        constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;  // log2 N
+        halve<N, 8, S>(v, lane);                         // lane j keeps value j >> (4 − S)
+        float t = v[0];
+#pragma unroll
+        for (int m = 8 >> S; m > 0; m >>= 1) t += __shfl_xor(t, m, 64);
+        if ((j & ((16 >> S) - 1)) == 0) {
+            const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
+            const int key = kk + 16 * i;
+            s_p[h][key] = k0 + key < n_keys ? t : -INFINITY;
         }
     }
     __syncthreads();
-    {
-        const int hh = tid >> 7, d = tid & 127;  // 256 threads = 2 heads × 128 dims
-        const float o = (s_o[0][hh][d] + s_o[1][hh][d]) + (s_o[2][hh][d] + s_o[3][hh][d]);
-        float *p = part + ((size_t)(h0 + hh) * max_chunk + c) * (D + 2);
-        p[2 + d] = o;
-        if (d == 0) {
-            p[0] = hh ? mb : ma;
-            p[1] = hh ? lb : la;
+
+    // 2. softmax statistics, one wave per head
+    if (wave < 2) {
+        float sv[(C + 63) / 64], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < (C + 63) / 64; i++) {
+            const int key = lane + 64 * i;
+            sv[i] = key < C ? s_p[wave][key] : -INFINITY;
+            mx = fmaxf(mx, sv[i]);
         }
+        mx = wave_max(mx);
+        float l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < (C + 63) / 64; i++) {
+            const int key = lane + 64 * i;
+            const float p = expf(sv[i] - mx);  // masked keys: exp(−inf) = 0
+            if (key < C) s_p[wave][key] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            s_ml[wave][0] = mx;
+            s_ml[wave][1] = l;
+        }
+    }
+    __syncthreads();
+
+    // 3. values
+    float o[16];  // [h][e]
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        float vf[8];
+        unpack8(vr[i], vf);
+        const float pa = s_p[0][kk + 16 * i], pb = s_p[1][kk + 16 * i];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            o[e] = fmaf(pa, vf[e], o[e]);
+            o[8 + e] = fmaf(pb, vf[e], o[8 + e]);
+        }
+    }
+    halve<16, 32, 2>(o, lane);  // over lane bits 5, 4: lane keeps values 8·b5 + 4·b4 + r
+    {
+        const int base = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int idx = base + r, h = idx >> 3, e = idx & 7;
+            s_o[wave][h][8 * j + e] = o[r];
+        }
+    }
+    __syncthreads();
+    const int hh = tid >> 7, d = tid & 127;  // 256 threads = 2 heads × 128 dims
+    const float oc = (s_o[0][hh][d] + s_o[1][hh][d]) + (s_o[2][hh][d] + s_o[3][hh][d]);
+    const int h = h0 + hh;
+    if (n_chunk == 1) {
+        out[h * D + d] = oc / s_ml[hh][1];
+        return;
     }
 
-    // 4. the last chunk of this KV head merges
-    __threadfence();
+    // 4. partials, then the last workgroup of the KV head merges. Cross-workgroup traffic is device-scope (sc1)
+    // stores and loads plus the ticket atomic: a release fence per workgroup would write back the L2 each time.
+    float *pc = part + ((size_t)h * max_chunk + c) * (D + 2);  // [h][c][m, l, o[128]]
+    __hip_atomic_store(pc + 2 + d, oc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d < 2) __hip_atomic_store(pc + d, s_ml[hh][d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are performed
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&counters[kvh], 1u) == (uint32_t)(n_chunk - 1);
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&counters[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(n_chunk - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    {
-        const int hh = tid >> 7, d = tid & 127;
-        const float *p = part + (size_t)(h0 + hh) * max_chunk * (D + 2);
-        float m = -INFINITY;
-        for (int cc = 0; cc < n_chunk; cc++) m = fmaxf(m, __builtin_nontemporal_load(p + (size_t)cc * (D + 2)));
-        float l = 0.0f, o = 0.0f;
-        for (int cc = 0; cc < n_chunk; cc++) {
-            const float *pc = p + (size_t)cc * (D + 2);
-            const float w = expf(__builtin_nontemporal_load(pc) - m);
-            l = fmaf(__builtin_nontemporal_load(pc + 1), w, l);
-            o = fmaf(__builtin_nontemporal_load(pc + 2 + d), w, o);
-        }
-        out[(h0 + hh) * D + d] = o / l;
+    // this thread's o partials (the first MERGE_PREFETCH chunks) go out now, with m and l
+    const float *ph = part + (size_t)h * max_chunk * (D + 2);
+    float ov[MERGE_PREFETCH];
+#pragma unroll
+    for (int i = 0; i < MERGE_PREFETCH; i++)
+        ov[i] = i < n_chunk ? __hip_atomic_load(ph + (size_t)i * (D + 2) + 2 + d, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.0f;
+    // M and the weights w_c = e^(m_c − M) of each head: 128 threads per head, chunks c = i, i + 128
+    const int i0 = tid & 127;
+    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
+    if (i0 < n_chunk) {
+        m0 = __hip_atomic_load(ph + (size_t)i0 * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        l0 = __hip_atomic_load(ph + (size_t)i0 * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (i0 + 128 < n_chunk) {
+        m1 = __hip_atomic_load(ph + (size_t)(i0 + 128) * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        l1 = __hip_atomic_load(ph + (size_t)(i0 + 128) * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float mx = wave_max(fmaxf(m0, m1));
+    if (lane == 0) s_red[hh][wave & 1] = mx;
+    __syncthreads();
+    mx = fmaxf(s_red[hh][0], s_red[hh][1]);
+    const float w0 = expf(m0 - mx), w1 = expf(m1 - mx);  // chunks past the end: e^(−inf) = 0
+    if (i0 < n_chunk) s_w[hh][i0] = w0;
+    if (i0 + 128 < n_chunk) s_w[hh][i0 + 128] = w1;
+    float L = wave_sum(fmaf(l0, w0, l1 * w1));
+    __syncthreads();  // s_red reused below
+    if (lane == 0) s_red[hh][wave & 1] = L;
+    __syncthreads();
+    L = s_red[hh][0] + s_red[hh][1];
+    float O = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MERGE_PREFETCH; i++)
+        if (i < n_chunk) O = fmaf(ov[i], s_w[hh][i], O);
+    for (int cc = MERGE_PREFETCH; cc < n_chunk; cc++)
+        O = fmaf(__hip_atomic_load(ph + (size_t)cc * (D + 2) + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 s_w[hh][cc], O);
+    out[h * D + d] = O / L;
     if (tid == 0) counters[kvh] = 0;  // ready for the next launch
 }
 
@@ -318,11 +393,14 @@ __global__ __launch_bounds__(128) void k_attn_causal(const float *q, const _Floa
 }  // namespace
 
 int attn_chunk_for(int n_ctx) {
-    // chunks of 64 keys up to 2048 positions, then longer chunks so the chunk count (the grid's x) stays ≤ 64
-    int chunk = 64;
+    // 16 keys per workgroup, doubled while a KV head would need more than 64 chunks (so at most 64 partials per head
+    // are merged for n_ctx ≤ 16384), up to 256 keys
+    int chunk = 16;
     while ((n_ctx + chunk - 1) / chunk > 64 && chunk < MAX_CHUNK_KEYS) chunk *= 2;
     return chunk;
 }
+
+size_t attn_part_bytes(int n_head, int max_chunk) { return (size_t)n_head * max_chunk * (D + 2) * 4; }
 
 int launch_qkv_post(htr_device *dev, hipStream_t st, float *qkv, const float *qn, const float *kn, const float *rope,
                     int n_head, int n_kv, const int *pos_dev, int pos, int n_ctx, float eps, uint16_t *kc,
@@ -336,13 +414,23 @@ int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const ui
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
                        const AttnScratch &sc, float *out) {
     if (n_head != 2 * n_kv) return htr_fail("decode attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
-    if (sc.chunk > MAX_CHUNK_KEYS || sc.chunk % 16) return htr_fail("decode attention: chunk %d", sc.chunk);
+    if (sc.chunk < 16 || sc.chunk > MAX_CHUNK_KEYS || (sc.chunk & (sc.chunk - 1)))
+        return htr_fail("decode attention: chunk %d (a power of two, 16 … %d)", sc.chunk, MAX_CHUNK_KEYS);
     if (!pos_dev && (n_keys < 1 || n_keys > n_ctx)) return htr_fail("decode attention: %d keys, cache %d", n_keys, n_ctx);
+    if ((size_t)sc.max_chunk * sc.chunk < (size_t)n_ctx || sc.max_chunk > MAX_CHUNKS)
+        return htr_fail("decode attention: %d chunks of %d keys for a %d-row cache (at most %d chunks)", sc.max_chunk,
+                        sc.chunk, n_ctx, MAX_CHUNKS);
     const int grid_x = pos_dev ? sc.max_chunk : (n_keys + sc.chunk - 1) / sc.chunk;
-    if (grid_x > sc.max_chunk) return htr_fail("decode attention: %d chunks, scratch for %d", grid_x, sc.max_chunk);
-    hipLaunchKernelGGL(k_attn_decode, dim3(grid_x, n_kv), dim3(AW), 0, st, q, (const _Float16 *)kc,
-                       (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.chunk, sc.max_chunk, scale, sc.part,
-                       sc.counters, out);
+    const dim3 grid(grid_x, n_kv);
+#define HTR_ATTN(NI)                                                                                                       hipLaunchKernelGGL(k_attn_decode<NI>, grid, dim3(AW), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc, n_kv,                         n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part, sc.counters, out)
+    switch (sc.chunk / 16) {
+    case 1: HTR_ATTN(1); break;
+    case 2: HTR_ATTN(2); break;
+    case 4: HTR_ATTN(4); break;
+    case 8: HTR_ATTN(8); break;
+    default: HTR_ATTN(16); break;
+    }
+#undef HTR_ATTN
     return htr_launched(dev, "k_attn_decode");
 }
 
@@ -379,10 +467,12 @@ extern "C" int htr_decode_attention(htr_device *dev, const float *d_q, const uin
     HTR_TRY(htr_check_alive(dev));
     if (!d_q || !d_k || !d_v || !d_out) return htr_fail("htr_decode_attention: null argument");
     if (n_keys < 1 || n_keys > n_ctx) return htr_fail("htr_decode_attention: %d keys in a %d-row cache", n_keys, n_ctx);
+    if (n_ctx > MAX_CHUNKS * MAX_CHUNK_KEYS)
+        return htr_fail("htr_decode_attention: a %d-row cache (at most %d)", n_ctx, MAX_CHUNKS * MAX_CHUNK_KEYS);
     AttnScratch sc{};
     sc.chunk = attn_chunk_for(n_ctx);
     sc.max_chunk = (n_ctx + sc.chunk - 1) / sc.chunk;
-    HTR_TRY(htr_scratch(dev, SCR_ATTN_PART, (size_t)n_head * sc.max_chunk * (D + 2) * 4, (void **)&sc.part));
+    HTR_TRY(htr_scratch(dev, SCR_ATTN_PART, attn_part_bytes(n_head, sc.max_chunk), (void **)&sc.part));
     HTR_TRY(htr_scratch(dev, SCR_ATTN_CNT, (size_t)n_kv * 4, (void **)&sc.counters));
     return launch_attn_decode(dev, dev->stream, d_q, d_k, d_v, n_head, n_kv, n_ctx, nullptr, n_keys, scale, sc, d_out);
 }

@@ -10,9 +10,14 @@
 //     CPU loop `if l > logits[best]` starting at best = 0 decides; every logit NaN → 0.
 //
 // Schedule: grid (groups, rows); a workgroup owns 1024 consecutive logits of one row, stages them in LDS, applies the
-// penalties of the window ids that fall in its range, and reduces (value, index) to one partial (pass 1). The last
-// workgroup of the row (atomic ticket) reduces the partials (pass 2), writes the token, appends it to the history and
-// updates the counts. One launch per choice; the ticket counter resets itself.
+// penalties of the window ids that fall in its range, and reduces (value, index) to its best. The row's best of all
+// workgroups is one 64-bit atomic max on an order-preserving key (value bits mapped to unsigned order, −0 as +0, then
+// the complemented index, so ties go to the lowest index); the last workgroup of the row (atomic ticket) reads it,
+// writes the token, appends it to the history and updates the counts. One launch per choice; the key and the ticket
+// reset themselves.
+//
+// Cross-workgroup traffic is device-scope atomics only: on this multi-XCD GPU a release fence in every workgroup
+// would write back the L2 each time, which costs more than the whole scan.
 #include <cmath>
 
 #include "htr_internal.h"
@@ -21,8 +26,18 @@ namespace {
 
 constexpr int CW = 256;
 constexpr int SPAN = 1024;
+constexpr int WIN_LDS = CW;  // windows up to this many ids are staged in LDS (longer ones are read from memory)
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float w, uint32_t j) { return v > w || (v == w && i < j); }
+
+// (value, index) → a key whose unsigned order is `better`'s: the value's bits made order-preserving (−0 taken as +0,
+// so the two compare equal as in IEEE), then the complemented index (the lower index wins a tie). The workgroup's
+// placeholder (−inf, 0xffffffff) maps below every real logit.
+__device__ __forceinline__ uint64_t choose_key(float v, uint32_t i) {
+    uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)b << 32) | (uint64_t)(~i);
+}
 
 __device__ __forceinline__ void wave_best(float &v, uint32_t &i) {
 #pragma unroll
@@ -60,6 +75,7 @@ __device__ __forceinline__ void block_best(float &v, uint32_t &i) {
 
 __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
     __shared__ float s_l[SPAN];
+    __shared__ uint32_t s_win[WIN_LDS];
     __shared__ int s_last;
     const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lo = g * SPAN, hi = min(a.n_vocab, lo + SPAN);
@@ -67,17 +83,21 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
     uint32_t *hist = a.hist + (size_t)row * a.hist_stride;
     const int len = a.len_dev ? *a.len_dev : a.len;
 
+    // the window (≤ WIN_LDS ids) → LDS with one load per thread, issued with the logits' loads
+    const int start = len - min(len, a.window);
+    const int n_win = a.rp != 1.0f ? len - start : 0;
+    const bool win_lds = n_win <= WIN_LDS;
+    if (win_lds && tid < n_win) s_win[tid] = hist[start + tid];
     for (int i = tid; i < hi - lo; i += CW) s_l[i] = logits[lo + i];
     __syncthreads();
-    // the window's distinct ids in [lo, hi)
-    if (a.rp != 1.0f) {
-        const int start = len - min(len, a.window);
-        for (int j = start + tid; j < len; j += CW) {
-            const uint32_t t = hist[j];
+    // the window's distinct ids in [lo, hi): the first occurrence of each applies the penalty
+    if (n_win > 0) {
+        for (int j = tid; j < n_win; j += CW) {
+            const uint32_t t = win_lds ? s_win[j] : hist[start + j];
             if (t < (uint32_t)lo || t >= (uint32_t)hi) continue;
             bool first = true;
-            for (int i = start; i < j; i++)
-                if (hist[i] == t) {
+            for (int i = 0; i < j; i++)
+                if ((win_lds ? s_win[i] : hist[start + i]) == t) {
                     first = false;
                     break;
                 }
@@ -89,7 +109,7 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
         }
         __syncthreads();
     }
-    // pass 1: this workgroup's best
+    // pass 1: this workgroup's best (NaN never wins: `better` is false for it)
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     for (int i = tid; i < hi - lo; i += CW) {
@@ -102,45 +122,35 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
         }
     }
     block_best(bv, bi);
-    uint32_t *part = a.part + ((size_t)row * gridDim.x + g) * 2;
+    uint64_t *best = a.best + row;
     if (tid == 0) {
-        part[0] = __float_as_uint(bv);
-        part[1] = bi;
+        // a NaN at index 0 after the penalty decides token 0 (the CPU loop never finds a greater value): top key
+        const bool nan0 = lo == 0 && s_l[0] != s_l[0];
+        const uint64_t key = nan0 ? ~0ull : choose_key(bv, bi);
+        __hip_atomic_fetch_max(best, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the max is performed before the ticket: wait for its return
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        s_last = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.x - 1;
     }
-    __threadfence();
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.counters[row], 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    // pass 2: the row's best over every workgroup's partial
-    bv = -INFINITY;
-    bi = 0xffffffffu;
-    const uint32_t *rp = a.part + (size_t)row * gridDim.x * 2;
-    for (int p = tid; p < (int)gridDim.x; p += CW) {
-        const float v = __uint_as_float(__builtin_nontemporal_load(rp + 2 * p));
-        const uint32_t i = __builtin_nontemporal_load(rp + 2 * p + 1);
-        if (better(v, i, bv, bi)) {
-            bv = v;
-            bi = i;
-        }
+    if (!s_last || tid != 0) return;
+    // pass 2 (the row's last workgroup): the final key → token
+    const uint64_t key = __hip_atomic_load(best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t t = ~(uint32_t)key;
+    const uint32_t tk = t < (uint32_t)a.n_vocab ? t : 0u;  // 0xffffffff (every logit NaN) → 0; the NaN-at-0 key → 0
+    a.tok[row] = tk;
+    hist[len] = tk;
+    if (a.fp != 0.0f) {
+        const uint32_t c = a.counts[tk] + 1u;
+        a.counts[tk] = c;
+        a.fpen[tk] = a.fp * (float)c;
     }
-    block_best(bv, bi);
-    if (tid == 0) {
-        const float l0 = __builtin_nontemporal_load(logits);  // index 0 after the penalty (its owner wrote it back)
-        uint32_t t = bi == 0xffffffffu ? 0u : bi;
-        if (l0 != l0) t = 0u;
-        a.tok[row] = t;
-        hist[len] = t;
-        if (a.fp != 0.0f) {
-            const uint32_t c = a.counts[t] + 1u;
-            a.counts[t] = c;
-            a.fpen[t] = a.fp * (float)c;
-        }
-        if (a.len_dev) *(int *)a.len_dev = len + 1;
-        if (a.advance) a.advance[0] += 1;
-        a.counters[row] = 0u;
-    }
+    if (a.len_dev) *(int *)a.len_dev = len + 1;
+    if (a.advance) a.advance[0] += 1;
+    // ready for the next launch (seen by it: a kernel boundary)
+    *best = 0ull;
+    a.counters[row] = 0u;
 }
 
 }  // namespace
@@ -160,8 +170,8 @@ static int check_rp(float rp) {
     return 0;
 }
 
-static int choose_scratch(htr_device *dev, int rows, int groups, uint32_t **part, uint32_t **counters) {
-    HTR_TRY(htr_scratch(dev, SCR_CHOOSE_PART, (size_t)rows * groups * 8, (void **)part));
+static int choose_scratch(htr_device *dev, int rows, uint64_t **best, uint32_t **counters) {
+    HTR_TRY(htr_scratch(dev, SCR_CHOOSE_PART, (size_t)rows * 8, (void **)best));
     return htr_scratch(dev, SCR_CHOOSE_CNT, (size_t)rows * 4, (void **)counters);
 }
 
@@ -185,7 +195,7 @@ extern "C" int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_
     a.fpen = d_fpen;
     a.tok = d_tok;
     a.rows = 1;
-    HTR_TRY(choose_scratch(dev, 1, choose_groups(n_vocab), &a.part, &a.counters));
+    HTR_TRY(choose_scratch(dev, 1, &a.best, &a.counters));
     return launch_choose(dev, dev->stream, a);
 }
 
@@ -207,6 +217,6 @@ extern "C" int htr_choose_many(htr_device *dev, float *d_logits, int n_vocab, in
     a.rp = rp;
     a.tok = d_tok;
     a.rows = n;
-    HTR_TRY(choose_scratch(dev, n, choose_groups(n_vocab), &a.part, &a.counters));
+    HTR_TRY(choose_scratch(dev, n, &a.best, &a.counters));
     return launch_choose(dev, dev->stream, a);
 }

@@ -36,6 +36,8 @@ struct htr_device {
     size_t scratch_bytes[8] = {0};
     // the measurement timer's events
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // decode steps replayed as captured HIP graphs (HTR_GRAPHS=0 at open: launched one by one)
+    bool use_graphs = true;
 };
 
 enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3 };
@@ -99,6 +101,8 @@ struct AttnScratch {
     int max_chunk, chunk;
 };
 int attn_chunk_for(int n_ctx);
+// bytes of the split-K partials for n_head q heads and max_chunk chunks ([h][c][m, l, o[128]] f32)
+size_t attn_part_bytes(int n_head, int max_chunk);
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
                        const AttnScratch &sc, float *out);
@@ -124,7 +128,7 @@ struct ChooseArgs {
     float *fpen;
     uint32_t *tok;
     int *advance;  // NULL, or { pos, len } incremented by the pick (the decode loop's device-resident counters)
-    uint32_t *part;      // [rows][n_groups][2]
+    uint64_t *best;      // [rows], zero, self-resetting: the row's best key
     uint32_t *counters;  // [rows], zero, self-resetting
     int rows;
 };

@@ -6,18 +6,24 @@
 //   weights   repacked at load (runtime.hip) into an int8 plane q[rows][K] and an f16 scale plane d[rows][K/32];
 //   lanes     a row is cut into groups of 16 quants (16 bytes); lane ℓ of a wave takes the groups ℓ, ℓ+64, … of every
 //             row the wave computes, so one wave-wide load instruction reads 1 KiB of contiguous quants (a whole row
-//             at K = 1024); the lane's 16 inputs x[16g…16g+15] sit in registers for all its rows;
-//   schedule  a wave computes R consecutive rows; all R·NG 16-byte loads (and their scales) are issued before the
-//             first use; a 256-thread workgroup = 4 waves = 4R rows;
-//   reduce    per row, the 64 lane partials are summed across the wave (cross-lane butterfly);
-//   norm      the fused RMS norm computes Σx² once per workgroup (x is ≤ 16 KiB and L2-resident);
-//   math      f32: the 16 int8·x products of a group are an fma chain, times the block's f16 scale into the row's
-//             accumulator (the scale is exact in f32).
+//             at K = 1024); the lane's 16·NG inputs sit in registers for all its rows (loaded once per wave);
+//   tile      a 256-thread workgroup (4 waves) owns 4·RW consecutive output rows, RW per wave. Every quant load of
+//             the wave's rows is issued before the first use; the tile's f16 scales (contiguous: rows are back to
+//             back) are copied into LDS by the whole workgroup while those loads are in flight;
+//   reduce    the RW per-lane partials of a wave are summed across the 64 lanes by one transposing butterfly:
+//             exchange-and-halve steps (masks 32, 16, …) leave one row per lane group, then a plain butterfly over
+//             the rest — RW−1 + log2(64/RW) cross-lane moves instead of 6·RW;
+//   norm      the fused RMS norm is computed on the registers: the wave's lanes hold all K inputs, so Σx² is one
+//             wave sum (no workgroup barrier, no second read of x);
+//   math      f32 (the reference's numbers: exact int8·f16-scale dequant, f32 products and sums): the 16 products
+//             of a group are an fma chain, times the block's scale into the row's accumulator. The int8 → f32
+//             conversion is one v_cvt_f32_i32 with a sign-extended byte select per quant.
 #include "htr_internal.h"
 
 namespace {
 
 constexpr int WG = 256;
+constexpr int WAVES = WG / 64;
 constexpr int MAX_MANY = 128;
 
 struct DmvK {
@@ -30,6 +36,47 @@ struct DmvK {
     float *y;
     int acc;
 };
+
+// n matvecs y_i = W_i · x in one launch: rows of the n matrices back to back (y [n][rows])
+struct DmvManyK {
+    DmvMat m[MAX_MANY];
+    int rows;  // rows of each matrix
+    int n_rows;
+    int k;
+    const float *x;
+    float *y;
+};
+
+// a kernel argument's pointer as a wave-uniform value (scalar registers): selects between such values stay selects of
+// values — a select between argument fields themselves would become one per-lane load from the argument buffer
+template <typename T> __device__ __forceinline__ T *uniform_ptr(T *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+// 16 / 2 bytes from global memory (address space 1: a global_load, not a flat one — pointers that went through
+// uniform_ptr have lost their address space)
+typedef int gint4 __attribute__((ext_vector_type(4)));
+typedef float gfloat4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 gload16(const void *p) {
+    const gint4 v = *(const __attribute__((address_space(1))) gint4 *)(uintptr_t)p;
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 gload16u(const void *p) {
+    const gint4 v = *(const __attribute__((address_space(1))) gint4 *)(uintptr_t)p;
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ float4 gload16f(const float *p) {
+    const gfloat4 v = *(const __attribute__((address_space(1))) gfloat4 *)(uintptr_t)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ _Float16 gload2h(const _Float16 *p) {
+    return *(const __attribute__((address_space(1))) _Float16 *)(uintptr_t)p;
+}
+__device__ __forceinline__ DmvMat uniform_mat(const DmvMat &m) {
+    return DmvMat{uniform_ptr(m.q), uniform_ptr(m.d), __builtin_amdgcn_readfirstlane(m.rows)};
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -49,181 +96,255 @@ __device__ __forceinline__ float dot16(const int4 q, const float *x) {
     return s;
 }
 
-// 1/sqrt(mean(x²) + eps) over k inputs, the whole workgroup
-__device__ __forceinline__ float norm_scale(const float *x, int k, float eps) {
-    __shared__ float red[WG / 64];
-    const int tid = threadIdx.x;
-    float s = 0.0f;
-    for (int i = tid; i < k / 4; i += WG) {
-        float4 v = reinterpret_cast<const float4 *>(x)[i];
-        s = fmaf(v.x, v.x, s);
-        s = fmaf(v.y, v.y, s);
-        s = fmaf(v.z, v.z, s);
-        s = fmaf(v.w, v.w, s);
+// Sums v[r] over the wave for every r < N (a power of two ≤ 64). On return the lanes whose low log2(64/N) bits are
+// zero hold a total: lane ℓ holds row ℓ / (64/N). Exchange-and-halve: at mask m the lane keeps the half of its values
+// its bit m selects and adds the partner's copy of that half.
+template <int N> __device__ __forceinline__ float wave_sum_rows(float (&v)[N], int lane) {
+#pragma unroll
+    for (int n = N / 2, m = 32; n >= 1; n >>= 1, m >>= 1) {
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < (N > 1 ? N / 2 : 1); i++) {
+            if (i < n) {
+                const float send = hi ? v[i] : v[i + n];
+                const float keep = hi ? v[i + n] : v[i];
+                v[i] = keep + __shfl_xor(send, m, 64);
+            }
+        }
     }
-    s = wave_sum(s);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
-    __syncthreads();
-    float t = (red[0] + red[1]) + (red[2] + red[3]);
-    return 1.0f / sqrtf(t / (float)k + eps);
+    float s = v[0];
+#pragma unroll
+    for (int m = 32 / N; m > 0; m >>= 1) s += __shfl_xor(s, m, 64);
+    return s;
 }
 
-template <int R, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv(const DmvK a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int k = a.k, ng = k >> 4, nb = k >> 5;
-    float scale = 1.0f;
-    if (MODE != DMV_PLAIN) scale = norm_scale(a.x, k, a.eps);
-
-    // the lane's inputs: groups lane + 64·i
-    float xv[NG][16];
+// the lane's inputs x[16g … 16g+15] for its groups g = lane + 64·i (zero beyond K), and with NORM the norm weights
+// of the same positions. The wave's lanes together hold all K inputs. Loads are unconditional (a lane past K reads
+// group 0 and drops it) so that no branch separates them from the quant loads that follow.
+template <int NG, bool NORM>
+__device__ __forceinline__ void load_x(float (&xv)[NG][16], float (&wv)[NG][16], const float *x, const float *nw,
+                                       int lane, int ng) {
 #pragma unroll
     for (int i = 0; i < NG; i++) {
         const int g = lane + 64 * i;
+        const int gg = g < ng ? g : 0;
+        const float keep = g < ng ? 1.0f : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) xv[i][j] = 0.0f;
-        if (g < ng) {
-            const float4 *xp = reinterpret_cast<const float4 *>(a.x + 16 * g);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float4 v = xp[j];
-                xv[i][4 * j + 0] = v.x;
-                xv[i][4 * j + 1] = v.y;
-                xv[i][4 * j + 2] = v.z;
-                xv[i][4 * j + 3] = v.w;
-            }
-            if (MODE != DMV_PLAIN) {
-                const float4 *wp = reinterpret_cast<const float4 *>(a.nw + 16 * g);
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float4 w = wp[j];
-                    xv[i][4 * j + 0] = (xv[i][4 * j + 0] * scale) * w.x;
-                    xv[i][4 * j + 1] = (xv[i][4 * j + 1] * scale) * w.y;
-                    xv[i][4 * j + 2] = (xv[i][4 * j + 2] * scale) * w.z;
-                    xv[i][4 * j + 3] = (xv[i][4 * j + 3] * scale) * w.w;
-                }
+        for (int j = 0; j < 4; j++) {
+            const float4 v = gload16f(x + 16 * gg + 4 * j);
+            xv[i][4 * j + 0] = v.x * keep;
+            xv[i][4 * j + 1] = v.y * keep;
+            xv[i][4 * j + 2] = v.z * keep;
+            xv[i][4 * j + 3] = v.w * keep;
+            if (NORM) {
+                const float4 w = gload16f(nw + 16 * gg + 4 * j);
+                wv[i][4 * j + 0] = w.x;
+                wv[i][4 * j + 1] = w.y;
+                wv[i][4 * j + 2] = w.z;
+                wv[i][4 * j + 3] = w.w;
             }
         }
     }
+}
 
-    constexpr int NM = MODE == DMV_FFN ? 2 : 1;  // matrices read per output row
-    const int row0 = (blockIdx.x * (WG / 64) + wave) * R;
-    int4 qv[NM][R][NG];
-    float dv[NM][R][NG];
-    // issue every load of the wave's rows first
+// the fused RMS norm (dmv_common.wgsl:23-30) on the registers: x · 1/sqrt(Σx²/K + eps) · nw. Σx² is a wave sum: the
+// wave holds all of x, so no workgroup barrier.
+template <int NG>
+__device__ __forceinline__ void norm_x(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k) {
+    float s = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; r++) {
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) s = fmaf(xv[i][j], xv[i][j], s);
+    const float scale = 1.0f / sqrtf(wave_sum(s) / (float)k + eps);
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) xv[i][j] = (xv[i][j] * scale) * wv[i][j];
+}
+
+// The tile's f16 scales → LDS s_d[r][nb] for rows [row0, row0 + RT). When nb is a multiple of 8 every row is whole
+// 16-byte units and a thread moves at most one unit (the host keeps RT·nb/8 ≤ 256): `issue` loads it into a register
+// before the quant loads go out, `store` writes it to LDS after. Other K (small reference-test shapes) copy halves.
+struct ScaleStage {
+    uint4 v;
+    int at;  // LDS offset in halves, −1 = none
+};
+
+template <typename MatOf>
+__device__ __forceinline__ ScaleStage scales_issue(int row0, int rt, int n_rows, int nb, MatOf mat_of) {
+    // branch-free (a branch would make the compiler wait for this load before the quant loads): every thread loads
+    // 16 bytes; a thread without a unit reads the tile's first row (the scale plane has 16 bytes of slack past its
+    // end, so a row of fewer than 8 scales is still a safe read) and stores nothing
+    const int per_row = nb % 8 == 0 ? nb / 8 : 1;
+    const int u = threadIdx.x;
+    const int r = u / per_row, part = u - r * per_row;
+    const bool valid = nb % 8 == 0 && u < rt * per_row && row0 + r < n_rows;
+    int lr;
+    const DmvMat m = mat_of(valid ? row0 + r : row0, lr);
+    ScaleStage st;
+    st.v = gload16u(m.d + (size_t)lr * nb + (valid ? 8 * part : 0));
+    st.at = valid ? r * nb + 8 * part : -1;
+    return st;
+}
+
+template <typename MatOf>
+__device__ __forceinline__ void scales_store(_Float16 *s_d, const ScaleStage &st, int row0, int rt, int n_rows, int nb,
+                                             MatOf mat_of) {
+    if (nb % 8 == 0) {
+        if (st.at >= 0) *reinterpret_cast<uint4 *>(s_d + st.at) = st.v;
+        return;
+    }
+    for (int u = threadIdx.x; u < rt * nb; u += WG) {
+        const int r = u / nb, b = u - r * nb;
         const int row = row0 + r;
-        const bool ok = row < a.n_rows;
-        int mi = 0, lr = row;
-        if (MODE == DMV_QKV) {
-            if (lr >= a.m[0].rows) {
-                lr -= a.m[0].rows;
-                mi = 1;
-                if (lr >= a.m[1].rows) {
-                    lr -= a.m[1].rows;
-                    mi = 2;
-                }
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < NM; t++) {
-            const DmvMat &m = a.m[MODE == DMV_FFN ? t : mi];
-            const int8_t *qrow = m.q + (size_t)lr * k;
-            const _Float16 *drow = m.d + (size_t)lr * nb;
-#pragma unroll
-            for (int i = 0; i < NG; i++) {
-                const int g = lane + 64 * i;
-                if (ok && g < ng) {
-                    qv[t][r][i] = *reinterpret_cast<const int4 *>(qrow + 16 * g);
-                    dv[t][r][i] = (float)drow[g >> 1];
-                } else {
-                    qv[t][r][i] = make_int4(0, 0, 0, 0);
-                    dv[t][r][i] = 0.0f;
-                }
-            }
+        if (row < n_rows) {
+            int lr;
+            const DmvMat m = mat_of(row, lr);
+            s_d[u] = gload2h(m.d + (size_t)lr * nb + b);
         }
     }
-    float acc[NM][R];
+}
+
+// the lane's quants of one row (lr must be a row of m: callers clamp rows past the end and drop their result)
+template <int NG>
+__device__ __forceinline__ void load_row(int4 (&qv)[NG], const DmvMat &m, int lr, int k, int lane, int ng) {
+    const int8_t *qrow = m.q + (size_t)lr * k;
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = lane + 64 * i;
+        const int4 v = gload16(qrow + 16 * (g < ng ? g : 0));
+        qv[i] = g < ng ? v : make_int4(0, 0, 0, 0);
+    }
+}
+
+template <int NG>
+__device__ __forceinline__ float row_dot(const int4 (&qv)[NG], const float (&xv)[NG][16], const _Float16 *s_row,
+                                         int lane, int ng) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = lane + 64 * i;
+        const float d = g < ng ? (float)s_row[g >> 1] : 0.0f;
+        s = fmaf(dot16(qv[i], xv[i]), d, s);
+    }
+    return s;
+}
+
+// The general kernel: PLAIN / NORM (dmv, dmv_norm), QKV (three matrices, attn_norm fused), FFN (gate and up, ffn_norm
+// and SwiGLU fused). RW output rows per wave. Order: inputs, then the scale loads, then every quant load of the wave's
+// rows; the norm and the scales' LDS store overlap the quant loads' flight.
+template <int RW, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv(const DmvK a) {
+    constexpr int NM = MODE == DMV_FFN ? 2 : 1;  // matrices read per output row
+    constexpr int RT = WAVES * RW;                 // rows per workgroup
+    __shared__ _Float16 s_d[NM][RT * NG * 32];     // scales: RT rows × nb ≤ 32·NG
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int k = a.k, ng = k >> 4, nb = k >> 5;
+    const int row0 = blockIdx.x * RT;
+    const int wrow0 = row0 + wave * RW;
+
+    // the row's matrix (QKV: rows of q, then k, then v), by selects of the kernel arguments' pointers (a per-thread
+    // row must not index the argument array: that would be a vector load and a wait before the quant loads)
+    auto mat_of = [&](int row, int &lr) -> DmvMat {
+        if (MODE != DMV_QKV) {
+            lr = row;
+            return a.m[0];
+        }
+        const DmvMat m0 = uniform_mat(a.m[0]), m1 = uniform_mat(a.m[1]), m2 = uniform_mat(a.m[2]);
+        const int r0 = m0.rows, r01 = r0 + m1.rows;
+        const bool in1 = row >= r0, in2 = row >= r01;
+        lr = row - (in2 ? r01 : in1 ? r0 : 0);
+        DmvMat m;
+        m.q = in2 ? m2.q : in1 ? m1.q : m0.q;
+        m.d = in2 ? m2.d : in1 ? m1.d : m0.d;
+        m.rows = in2 ? m2.rows : in1 ? m1.rows : m0.rows;
+        return m;
+    };
+    auto up_of = [&](int row, int &lr) -> DmvMat {
+        lr = row;
+        return a.m[NM - 1];
+    };
+
+    float xv[NG][16], wv[NG][16];
+    load_x<NG, MODE != DMV_PLAIN>(xv, wv, a.x, a.nw, lane, ng);
+    ScaleStage ss[NM];
+    ss[0] = scales_issue(row0, RT, a.n_rows, nb, mat_of);
+    if (NM == 2) ss[NM - 1] = scales_issue(row0, RT, a.n_rows, nb, up_of);
+    int4 qv[NM][RW][NG];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int row = min(wrow0 + r, a.n_rows - 1);  // rows past the end repeat the last (their result is dropped)
+        int lr;
+        const DmvMat m = mat_of(row, lr);
+        load_row<NG>(qv[0][r], m, lr, k, lane, ng);
+        if (NM == 2) load_row<NG>(qv[NM - 1][r], a.m[1], lr, k, lane, ng);
+    }
+    if (MODE != DMV_PLAIN) norm_x<NG>(xv, wv, a.eps, k);
+    scales_store(s_d[0], ss[0], row0, RT, a.n_rows, nb, mat_of);
+    if (NM == 2) scales_store(s_d[NM - 1], ss[NM - 1], row0, RT, a.n_rows, nb, up_of);
+    __syncthreads();
+
+    float acc[NM][RW];
 #pragma unroll
     for (int t = 0; t < NM; t++) {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NG; i++) s = fmaf(dot16(qv[t][r][i], xv[i]), dv[t][r][i], s);
-            acc[t][r] = wave_sum(s);
-        }
+        for (int r = 0; r < RW; r++) acc[t][r] = row_dot<NG>(qv[t][r], xv, s_d[t] + (wave * RW + r) * nb, lane, ng);
     }
-    if (lane < R) {
-        // lane r writes row r (a select chain keeps the accumulators in registers)
-        float v[NM];
+    float v[NM];
 #pragma unroll
-        for (int t = 0; t < NM; t++) {
-            v[t] = acc[t][0];
-#pragma unroll
-            for (int r = 1; r < R; r++) v[t] = lane == r ? acc[t][r] : v[t];
-        }
-        const int row = row0 + lane;
+    for (int t = 0; t < NM; t++) v[t] = wave_sum_rows<RW>(acc[t], lane);
+    constexpr int SPREAD = 64 / RW;
+    if ((lane & (SPREAD - 1)) == 0) {
+        const int row = wrow0 + lane / SPREAD;
         if (row < a.n_rows) {
             float out = v[0];
-            if (MODE == DMV_FFN) out = (v[0] / (1.0f + expf(-v[0]))) * v[1];
+            if (MODE == DMV_FFN) out = (v[0] / (1.0f + expf(-v[0]))) * v[NM - 1];
             if (a.acc) out = a.y[row] + out;
             a.y[row] = out;
         }
     }
 }
 
-// n matvecs y_i = W_i · x in one launch (blockIdx.y = i), the plain kernel's schedule
-struct DmvManyK {
-    DmvMat m[MAX_MANY];
-    int k;
-    const float *x;
-    float *y;
-};
-
-template <int R, int NG> __global__ __launch_bounds__(WG) void k_dmv_many(const DmvManyK a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+template <int RW, int NG> __global__ __launch_bounds__(WG) void k_dmv_many(const DmvManyK a) {
+    constexpr int RT = WAVES * RW;
+    __shared__ _Float16 s_d[RT * NG * 32];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int k = a.k, ng = k >> 4, nb = k >> 5;
-    const DmvMat m = a.m[blockIdx.y];
-    float xv[NG][16];
+    const int row0 = blockIdx.x * RT;
+    const int wrow0 = row0 + wave * RW;
+    // the row's matrix: one of the tile's two (the host keeps RT ≤ rows, so a tile spans at most two), by selects
+    const int mi0 = row0 / a.rows;
+    const DmvMat m0 = uniform_mat(a.m[mi0]), m1 = uniform_mat(a.m[min(mi0 + 1, MAX_MANY - 1)]);
+    auto mat_of = [&](int row, int &lr) -> DmvMat {
+        const bool second = row - mi0 * a.rows >= a.rows;
+        lr = row - (mi0 + (second ? 1 : 0)) * a.rows;
+        DmvMat m;
+        m.q = second ? m1.q : m0.q;
+        m.d = second ? m1.d : m0.d;
+        m.rows = a.rows;
+        return m;
+    };
+    float xv[NG][16], wv[NG][16];
+    load_x<NG, false>(xv, wv, a.x, nullptr, lane, ng);
+    const ScaleStage ss = scales_issue(row0, RT, a.n_rows, nb, mat_of);
+    int4 qv[RW][NG];
 #pragma unroll
-    for (int i = 0; i < NG; i++) {
-        const int g = lane + 64 * i;
-#pragma unroll
-        for (int j = 0; j < 16; j++) xv[i][j] = g < ng ? a.x[16 * g + j] : 0.0f;
+    for (int r = 0; r < RW; r++) {
+        const int row = min(wrow0 + r, a.n_rows - 1);  // rows past the end repeat the last (their result is dropped)
+        int lr;
+        const DmvMat m = mat_of(row, lr);
+        load_row<NG>(qv[r], m, lr, k, lane, ng);
     }
-    const int row0 = (blockIdx.x * (WG / 64) + wave) * R;
-    int4 qv[R][NG];
-    float dv[R][NG];
+    scales_store(s_d, ss, row0, RT, a.n_rows, nb, mat_of);
+    __syncthreads();
+    float acc[RW];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int row = row0 + r;
-#pragma unroll
-        for (int i = 0; i < NG; i++) {
-            const int g = lane + 64 * i;
-            if (row < m.rows && g < ng) {
-                qv[r][i] = *reinterpret_cast<const int4 *>(m.q + (size_t)row * k + 16 * g);
-                dv[r][i] = (float)m.d[(size_t)row * nb + (g >> 1)];
-            } else {
-                qv[r][i] = make_int4(0, 0, 0, 0);
-                dv[r][i] = 0.0f;
-            }
-        }
-    }
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NG; i++) s = fmaf(dot16(qv[r][i], xv[i]), dv[r][i], s);
-        acc[r] = wave_sum(s);
-    }
-    if (lane < R) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < R; r++) v = lane == r ? acc[r] : v;
-        const int row = row0 + lane;
-        if (row < m.rows) a.y[(size_t)blockIdx.y * m.rows + row] = v;
+    for (int r = 0; r < RW; r++) acc[r] = row_dot<NG>(qv[r], xv, s_d + (wave * RW + r) * nb, lane, ng);
+    const float v = wave_sum_rows<RW>(acc, lane);
+    constexpr int SPREAD = 64 / RW;
+    if ((lane & (SPREAD - 1)) == 0) {
+        const int row = wrow0 + lane / SPREAD;
+        if (row < a.n_rows) a.y[row] = v;
     }
 }
 
@@ -239,31 +360,37 @@ __global__ __launch_bounds__(WG) void k_embed(const int8_t *q, const _Float16 *d
     }
 }
 
-template <int R, int MODE> int dispatch_ng(hipStream_t st, int ng_lane, dim3 grid, const DmvK &a) {
+template <int RW, int MODE> int dispatch_ng(hipStream_t st, int ng_lane, const DmvK &a) {
+    const dim3 grid((a.n_rows + WAVES * RW - 1) / (WAVES * RW));
     switch (ng_lane) {
-    case 1: hipLaunchKernelGGL((k_dmv<R, 1, MODE>), grid, dim3(WG), 0, st, a); return 0;
-    case 2: hipLaunchKernelGGL((k_dmv<R, 2, MODE>), grid, dim3(WG), 0, st, a); return 0;
-    case 3: hipLaunchKernelGGL((k_dmv<R, 3, MODE>), grid, dim3(WG), 0, st, a); return 0;
-    case 4: hipLaunchKernelGGL((k_dmv<R, 4, MODE>), grid, dim3(WG), 0, st, a); return 0;
+    case 1: hipLaunchKernelGGL((k_dmv<RW, 1, MODE>), grid, dim3(WG), 0, st, a); return 0;
+    case 2: hipLaunchKernelGGL((k_dmv<RW, 2, MODE>), grid, dim3(WG), 0, st, a); return 0;
+    case 3: hipLaunchKernelGGL((k_dmv<RW, 3, MODE>), grid, dim3(WG), 0, st, a); return 0;
+    case 4: hipLaunchKernelGGL((k_dmv<RW, 4, MODE>), grid, dim3(WG), 0, st, a); return 0;
     }
     return -1;
 }
 
-template <int MODE> int dispatch_r(hipStream_t st, int r, int ng_lane, const DmvK &a) {
-    dim3 grid((a.n_rows + 4 * r - 1) / (4 * r));
-    switch (r) {
-    case 1: return dispatch_ng<1, MODE>(st, ng_lane, grid, a);
-    case 2: return dispatch_ng<2, MODE>(st, ng_lane, grid, a);
-    case 4: return dispatch_ng<4, MODE>(st, ng_lane, grid, a);
+template <int MODE> int dispatch_r(hipStream_t st, int rw, int ng_lane, const DmvK &a) {
+    switch (rw) {
+    case 1: return dispatch_ng<1, MODE>(st, ng_lane, a);
+    case 2: return dispatch_ng<2, MODE>(st, ng_lane, a);
+    case 4: return dispatch_ng<4, MODE>(st, ng_lane, a);
+    case 8: return dispatch_ng<8, MODE>(st, ng_lane, a);
+    case 16: return dispatch_ng<16, MODE>(st, ng_lane, a);
     }
     return -1;
 }
 
-// rows per wave: enough workgroups to cover the chip several times over before rows are batched per wave
-int rows_per_wave(int n_rows) {
-    if (n_rows >= 16 * 4096) return 4;
-    if (n_rows >= 8 * 2048) return 2;
-    return 1;
+// Rows per wave: the largest that still gives every CU two workgroups or more (small decode matrices are latency
+// bound: all their loads go out at once), capped so a lane's quant registers stay ≤ 64 (+ x) for occupancy. The cap
+// RW·NG ≤ 16 also keeps a tile's scales within one 16-byte unit per thread (RT·nb/8 = RW·nb/2 ≤ 8·RW·NG ≤ 256 halves
+// … units), which scales_issue relies on.
+int rows_per_wave(int n_rows, int n_cu, int ng_lane, int nm) {
+    int rw = 16;
+    while (rw > 1 && (n_rows + WAVES * rw - 1) / (WAVES * rw) < 2 * n_cu) rw >>= 1;
+    while (rw > 1 && rw * ng_lane * nm > 16) rw >>= 1;
+    return rw;
 }
 
 }  // namespace
@@ -290,15 +417,15 @@ int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, in
     a.y = y;
     a.acc = acc;
     const int ng_lane = (k / 16 + 63) / 64;
-    const int r = rows_per_wave(rows);
+    const int rw = rows_per_wave(rows, dev->n_cu, ng_lane, mode == DMV_FFN ? 2 : 1);
     int rc = -1;
     switch (mode) {
-    case DMV_PLAIN: rc = dispatch_r<DMV_PLAIN>(st, r, ng_lane, a); break;
-    case DMV_NORM: rc = dispatch_r<DMV_NORM>(st, r, ng_lane, a); break;
-    case DMV_QKV: rc = dispatch_r<DMV_QKV>(st, r, ng_lane, a); break;
-    case DMV_FFN: rc = dispatch_r<DMV_FFN>(st, r, ng_lane, a); break;
+    case DMV_PLAIN: rc = dispatch_r<DMV_PLAIN>(st, rw, ng_lane, a); break;
+    case DMV_NORM: rc = dispatch_r<DMV_NORM>(st, rw, ng_lane, a); break;
+    case DMV_QKV: rc = dispatch_r<DMV_QKV>(st, rw, ng_lane, a); break;
+    case DMV_FFN: rc = dispatch_r<DMV_FFN>(st, rw, ng_lane, a); break;
     }
-    if (rc < 0) return htr_fail("matvec: no kernel for mode %d, R %d, K %d", mode, r, k);
+    if (rc < 0) return htr_fail("matvec: no kernel for mode %d, RW %d, K %d", mode, rw, k);
     return htr_launched(dev, "k_dmv");
 }
 
@@ -308,19 +435,30 @@ int launch_dmv_many(htr_device *dev, hipStream_t st, const DmvMat *mats, int n, 
         const int cnt = std::min(MAX_MANY, n - base);
         DmvManyK a{};
         for (int i = 0; i < cnt; i++) a.m[i] = mats[base + i];
+        a.rows = mats[0].rows;
+        a.n_rows = cnt * a.rows;
         a.k = k;
         a.x = x;
         a.y = y + (size_t)base * mats[0].rows;
-        const int rows = mats[0].rows;
         const int ng_lane = (k / 16 + 63) / 64;
-        const int r = 2;
-        dim3 grid((rows + 4 * r - 1) / (4 * r), cnt);
-        switch (ng_lane) {
-        case 1: hipLaunchKernelGGL((k_dmv_many<2, 1>), grid, dim3(WG), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((k_dmv_many<2, 2>), grid, dim3(WG), 0, st, a); break;
-        case 3: hipLaunchKernelGGL((k_dmv_many<2, 3>), grid, dim3(WG), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_dmv_many<2, 4>), grid, dim3(WG), 0, st, a); break;
+        int rw = rows_per_wave(a.n_rows, dev->n_cu, ng_lane, 1);
+        while (rw > 1 && WAVES * rw > a.rows) rw >>= 1;  // a tile spans at most two matrices
+        const dim3 grid((a.n_rows + WAVES * rw - 1) / (WAVES * rw));
+#define HTR_MANY(RW)                                                                                                   \
+    switch (ng_lane) {                                                                                                 \
+    case 1: hipLaunchKernelGGL((k_dmv_many<RW, 1>), grid, dim3(WG), 0, st, a); break;                                  \
+    case 2: hipLaunchKernelGGL((k_dmv_many<RW, 2>), grid, dim3(WG), 0, st, a); break;                                  \
+    case 3: hipLaunchKernelGGL((k_dmv_many<RW, 3>), grid, dim3(WG), 0, st, a); break;                                  \
+    default: hipLaunchKernelGGL((k_dmv_many<RW, 4>), grid, dim3(WG), 0, st, a); break;                                 \
+    }
+        switch (rw) {
+        case 1: HTR_MANY(1) break;
+        case 2: HTR_MANY(2) break;
+        case 4: HTR_MANY(4) break;
+        case 8: HTR_MANY(8) break;
+        default: HTR_MANY(16) break;
         }
+#undef HTR_MANY
         HTR_TRY(htr_launched(dev, "k_dmv_many"));
     }
     return 0;
@@ -358,6 +496,10 @@ extern "C" int htr_matvec_q8_0_many(htr_device *dev, const htr_weight *const *ws
                             ws[i]->cols, ws[0]->rows, ws[0]->cols);
         ms[i] = mat_of(ws[i]);
     }
+    if (ws[0]->rows < (size_t)WAVES)
+        return htr_fail("htr_matvec_q8_0_many: %zu rows per matrix (at least %d)", ws[0]->rows, WAVES);
+    if (ws[0]->rows * std::min<size_t>(n, MAX_MANY) > (size_t)INT32_MAX)
+        return htr_fail("htr_matvec_q8_0_many: %zu rows per launch", ws[0]->rows * std::min<size_t>(n, MAX_MANY));
     return launch_dmv_many(dev, dev->stream, ms.data(), (int)n, (int)ws[0]->cols, d_x, d_y);
 }
 

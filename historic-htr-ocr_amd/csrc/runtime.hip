@@ -69,6 +69,8 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
         return htr_fail("device %d is %s: this library is built for gfx950 (MI355X) only", ordinal, prop.gcnArchName);
     auto *dev = new htr_device;
     dev->ordinal = ordinal;
+    const char *graphs = getenv("HTR_GRAPHS");
+    dev->use_graphs = !(graphs && strcmp(graphs, "0") == 0);
     snprintf(dev->name, sizeof dev->name, "%s (%s)", prop.name, prop.gcnArchName);
     dev->n_cu = prop.multiProcessorCount;
     // default priority: one stream for every launch of this device
@@ -271,7 +273,8 @@ extern "C" int htr_weight_q8_0(htr_device *dev, const void *h_blocks, size_t row
     w->rows = rows;
     w->cols = cols;
     int rc = htr_dev_alloc(dev, q.size(), HTR_MEM_WEIGHTS, (void **)&w->q);
-    if (rc == 0) rc = htr_dev_alloc(dev, d.size() * 2, HTR_MEM_WEIGHTS, (void **)&w->d);
+    // the scale plane has 16 bytes of slack: the matvec's scale staging reads whole 16-byte units
+    if (rc == 0) rc = htr_dev_alloc(dev, d.size() * 2 + 16, HTR_MEM_WEIGHTS, (void **)&w->d);
     if (rc == 0) rc = htr_upload(dev, w->q, q.data(), q.size());
     if (rc == 0) rc = htr_upload(dev, w->d, d.data(), d.size() * 2);
     if (rc < 0) {

@@ -69,7 +69,8 @@ struct htr_choice {
     float rp = 1.0f, fp = 0.0f;
     size_t max_new = 0, chunk = 1, depth = 1;
     int n_vocab = 0;
-    uint32_t *hist = nullptr, *counts = nullptr, *part = nullptr, *counters = nullptr;
+    uint32_t *hist = nullptr, *counts = nullptr, *counters = nullptr;
+    uint64_t *best = nullptr;
     float *fpen = nullptr;
     uint32_t *h_ids = nullptr;  // pinned [depth][chunk]
     std::vector<hipEvent_t> events;
@@ -147,7 +148,7 @@ ChooseArgs choice_args(htr_choice *ch, bool advance) {
     a.fpen = ch->fpen;
     a.tok = s->tok;
     a.advance = advance ? s->state : nullptr;
-    a.part = ch->part;
+    a.best = ch->best;
     a.counters = ch->counters;
     a.rows = 1;
     return a;
@@ -173,6 +174,23 @@ int capture(htr_session *s, htr_choice *ch, int n, bool with_step, hipGraphExec_
     e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     return htr_hip(dev, e, "hipGraphInstantiate");
+}
+
+// `n` repetitions of [step? + choice]: the captured graph `*g` (captured on first use) replayed, or — with graphs
+// switched off on the device (HTR_GRAPHS=0: profilers that cannot follow stream capture) — the same kernels
+// launched one by one on the stream
+int run_steps(htr_session *s, htr_choice *ch, int n, bool with_step, hipGraphExec_t *g) {
+    htr_device *dev = s->dev;
+    hipStream_t st = dev->stream;
+    if (!dev->use_graphs) {
+        for (int i = 0; i < n; i++) {
+            if (with_step) HTR_TRY(record_step(s, st));
+            if (ch) HTR_TRY(launch_choose(dev, st, choice_args(ch, with_step)));
+        }
+        return 0;
+    }
+    if (!*g) HTR_TRY(capture(s, ch, n, with_step, g));
+    return htr_hip(dev, hipGraphLaunch(*g, st), "hipGraphLaunch");
 }
 
 int set_state(htr_session *s, int pos, int len) {
@@ -265,7 +283,7 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
                         c.n_kv);
     if (n_ctx < 1 || (c.n_ctx_train > 0 && n_ctx > (size_t)c.n_ctx_train))
         return htr_fail("%zu positions asked, the model was trained on %d", n_ctx, c.n_ctx_train);
-    if (n_ctx > (1u << 20)) return htr_fail("%zu positions: at most %u", n_ctx, 1u << 20);
+    if (n_ctx > 65536) return htr_fail("%zu positions: the decode attention takes at most 65536", n_ctx);
     auto *s = new htr_session;
     s->m = m;
     s->dev = dev;
@@ -287,8 +305,7 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->tok);
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->state);
     if (rc == 0)
-        rc = htr_dev_alloc(dev, (size_t)c.n_head * s->asc.max_chunk * (HEAD + 2) * 4, HTR_MEM_WORK,
-                           (void **)&s->asc.part);
+        rc = htr_dev_alloc(dev, attn_part_bytes(c.n_head, s->asc.max_chunk), HTR_MEM_WORK, (void **)&s->asc.part);
     if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_kv * 4, HTR_MEM_WORK, (void **)&s->asc.counters);
     if (rc == 0) rc = htr_sync(dev);
     if (rc < 0) {
@@ -399,8 +416,7 @@ extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
     uint32_t t = (uint32_t)token;
     HTR_TRY(htr_upload(dev, s->tok, &t, 4));
     HTR_TRY(set_state(s, s->n_past, 0));
-    if (!s->step_graph) HTR_TRY(capture(s, nullptr, 1, true, &s->step_graph));
-    HTR_TRY(htr_hip(dev, hipGraphLaunch(s->step_graph, dev->stream), "hipGraphLaunch"));
+    HTR_TRY(run_steps(s, nullptr, 1, true, &s->step_graph));
     HTR_TRY(htr_sync(dev));
     s->n_past += 1;
     if (h_logits) HTR_TRY(htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4));
@@ -415,7 +431,7 @@ extern "C" int htr_choice_free(htr_choice *ch) {
     for (hipGraphExec_t g : {ch->g_first, ch->g_one, ch->g_chunk})
         if (g) hipGraphExecDestroy(g);
     for (hipEvent_t e : ch->events) hipEventDestroy(e);
-    for (void *p : {(void *)ch->hist, (void *)ch->counts, (void *)ch->fpen, (void *)ch->part, (void *)ch->counters})
+    for (void *p : {(void *)ch->hist, (void *)ch->counts, (void *)ch->fpen, (void *)ch->best, (void *)ch->counters})
         if (p) htr_dev_free(dev, p);
     if (ch->h_ids) hipHostFree(ch->h_ids);
     delete ch;
@@ -460,7 +476,7 @@ extern "C" int htr_choice_create(htr_session *s, const htr_preset *p, const int3
     if (rc == 0) rc = htr_upload(dev, ch->hist, hist.data(), hist.size() * 4);
     if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->counts);
     if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->fpen);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)choose_groups(n_vocab) * 8, HTR_MEM_WORK, (void **)&ch->part);
+    if (rc == 0) rc = htr_dev_alloc(dev, 8, HTR_MEM_WORK, (void **)&ch->best);
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&ch->counters);
     if (rc == 0) rc = htr_hip(dev, hipHostMalloc((void **)&ch->h_ids, depth * chunk * 4, hipHostMallocDefault), "hipHostMalloc");
     for (size_t i = 0; i < depth && rc == 0; i++) {
@@ -488,9 +504,6 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
     if ((size_t)s->n_past + (max - 1) > (size_t)s->n_ctx)
         return htr_fail("%zu choices need %zu positions, the session holds %d", max, s->n_past + max - 1, s->n_ctx);
     hipStream_t st = dev->stream;
-    if (!ch->g_first) HTR_TRY(capture(s, ch, 1, false, &ch->g_first));
-    if (!ch->g_one) HTR_TRY(capture(s, ch, 1, true, &ch->g_one));
-    if (!ch->g_chunk && ch->chunk > 1) HTR_TRY(capture(s, ch, (int)ch->chunk, true, &ch->g_chunk));
     HTR_TRY(set_state(s, s->n_past, ch->seed_len));
 
     struct Pending {
@@ -508,17 +521,17 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
             free_slots.pop_back();
             size_t n_launched = 0;
             if (next == 0) {
-                rc = htr_hip(dev, hipGraphLaunch(ch->g_first, st), "hipGraphLaunch");
+                rc = run_steps(s, ch, 1, false, &ch->g_first);
                 n_launched = 1;
             }
             // fill the slot up to `chunk` choices: whole chunk graphs, else single steps
             while (rc == 0 && n_launched < ch->chunk && next + n_launched < max) {
                 const size_t left = std::min(ch->chunk - n_launched, max - next - n_launched);
-                if (left == ch->chunk && ch->g_chunk) {
-                    rc = htr_hip(dev, hipGraphLaunch(ch->g_chunk, st), "hipGraphLaunch");
+                if (left == ch->chunk && ch->chunk > 1) {
+                    rc = run_steps(s, ch, (int)ch->chunk, true, &ch->g_chunk);
                     n_launched += ch->chunk;
                 } else {
-                    rc = htr_hip(dev, hipGraphLaunch(ch->g_one, st), "hipGraphLaunch");
+                    rc = run_steps(s, ch, 1, true, &ch->g_one);
                     n_launched += 1;
                 }
             }

@@ -56,40 +56,10 @@ def tiny_prompt(n: int = 20) -> np.ndarray:
 
 
 def synth_text_model(n_layer=28, dim=1024, n_head=16, n_kv=8, n_ff=3072, n_vocab=151936, seed=1000):
-    """The Qwen3-0.6B-shaped random decoder: every linear q8_0 (quants uniform in [−127, 127], d = f16(|N(0,1)|·0.002)),
-    RMSNorm weights 1 + N(0, 0.02); tied LM head."""
-    import htr
+    """The Qwen3-0.6B-shaped random decoder (htr.synth.text_model)."""
+    from htr import synth
 
-    d_head = 128
-    qd, kvd = n_head * d_head, n_kv * d_head
-    s = seed
-    layers = []
-
-    def nxt():
-        nonlocal s
-        s += 1
-        return s
-
-    for _ in range(n_layer):
-        ly = {
-            "attn_norm": htr.synth_normal(nxt(), dim, 1.0, 0.02),
-            "q": htr.synth_q8_0(nxt(), qd, dim),
-            "k": htr.synth_q8_0(nxt(), kvd, dim),
-            "v": htr.synth_q8_0(nxt(), kvd, dim),
-            "o": htr.synth_q8_0(nxt(), dim, qd),
-            "q_norm": htr.synth_normal(nxt(), d_head, 1.0, 0.02),
-            "k_norm": htr.synth_normal(nxt(), d_head, 1.0, 0.02),
-            "ffn_norm": htr.synth_normal(nxt(), dim, 1.0, 0.02),
-            "gate": htr.synth_q8_0(nxt(), n_ff, dim),
-            "up": htr.synth_q8_0(nxt(), n_ff, dim),
-            "down": htr.synth_q8_0(nxt(), dim, n_ff),
-        }
-        layers.append(ly)
-    tok_embd = htr.synth_q8_0(nxt(), n_vocab, dim)
-    output_norm = htr.synth_normal(nxt(), dim, 1.0, 0.02)
-    cfg = dict(n_layer=n_layer, dim=dim, n_head=n_head, n_kv=n_kv, d_head=d_head, n_ff=n_ff, n_vocab=n_vocab,
-               n_ctx_train=40960, eps=1e-6, rope_base=1e6)
-    return cfg, tok_embd, output_norm, layers
+    return synth.text_model(n_layer, dim, n_head, n_kv, n_ff, n_vocab, seed)
 
 
 def to_htr_cfg(cfg: dict):

@@ -37,21 +37,32 @@ def teacher_forced(o: orc.Session, first_logits, prompt, toks, rp, window, tie_l
 
 
 def test_tiny_prefill_and_steps_match_oracle(dev, tiny):
-    """the reference's tiny model (text.rs:1297-1323) and prompt (text.rs:1333): prefill logits, then 40 greedy
-    CPU-choice steps (TextModel::step), every logits row against the oracle's"""
+    """the reference's tiny model (text.rs:1297-1323) and prompt (text.rs:1333): prefill logits against the fp64
+    forward (rel-L2 ≤ 1e-3) and the oracle, then 40 greedy CPU-choice steps (TextModel::step), every logits row against
+    the oracle's.
+
+    Bar against the oracle: 2e-4. Both are f32 computations of the same graph in different summation orders (the
+    prefill GEMMs and attention tile differently); the oracle's own rel-L2 to the fp64 forward is 3.0e-5 on this
+    prompt, and the two f32 results sit on either side of it."""
+    from test_oracle import np_forward
+
     cfg, te, on, layers, m = tiny
     prompt = tiny_prompt()
     s = m.session(prompt.size + 150)
     o = orc.Session(cfg, te, on, layers, prompt.size + 150)
     lg, lo = s.prefill(prompt), o.prefill(prompt)
-    assert rel_l2(lg, lo) < 1e-5
+    want = np_forward(cfg, te, on, layers, list(prompt))[-1]
+    e64, eo = rel_l2(lg, want), rel_l2(lg, lo)
+    print(f"\n[tiny prefill] rel-L2 vs fp64 {e64:.2e} (oracle vs fp64 {rel_l2(lo, want):.2e}), vs oracle {eo:.2e}")
+    assert e64 < 1e-3
+    assert eo < 2e-4
     assert s.n_past == prompt.size
     for i in range(40):
         t = int(np.argmax(lg))
         lo_t = int(np.argmax(lo))
         assert t == lo_t or near_tie(lo, lo_t, t), i
         lg, lo = s.step(t), o.step(t)
-        assert rel_l2(lg, lo) < 1e-5, i
+        assert rel_l2(lg, lo) < 2e-4, i
     assert s.n_past == prompt.size + 40
     s.free()
 
