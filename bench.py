@@ -202,10 +202,36 @@ def bench_attention(dev, n_head=16, n_kv=8):
     return res
 
 
-def cpu_baseline(model_inputs, budget_s=12.0):
+def bench_copy(dev, mib=512, reps=5):
+    """a plain device copy of known size (htr_copy): the HBM reference point of the byte counters"""
+    n = mib << 20
+    src, dst = dev.alloc(n), dev.alloc(n)
+    dst.copy_from(src)
+    dev.timer_begin()
+    for _ in range(reps):
+        dst.copy_from(src)
+    ms = dev.timer_end() / reps
+    src.free()
+    dst.free()
+    res = {"bytes": n, "us": ms * 1e3, "GBs_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}
+    log(f"copy {mib} MiB: {res['us']:.1f} us, {res['GBs_read_plus_write']:.0f} GB/s (read + write)")
+    return res
+
+
+def load_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE
+    per dispatch, scaled by what the same counters read for a copy of known size), or None"""
+    f = os.path.join(ROOT, "profiles", "k_dmv_many_cfg0_traffic.json")
+    if not os.path.exists(f):
+        return None
+    with open(f) as fh:
+        t = json.load(fh)
+    return t.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
     """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores"""
     # the oracle is the checker: imported here, for the CPU baseline leg only
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import importlib.util
 
     spec = importlib.util.spec_from_file_location("htr_oracle_py", os.path.join(ROOT, "oracle", "oracle.py"))
@@ -214,12 +240,12 @@ def cpu_baseline(model_inputs, budget_s=12.0):
 
     cfg, te, on, layers, prompt = model_inputs
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    o = orc.Session(cfg, te, on, layers, 32 + 48 + 1)
-    lo = o.prefill(prompt[:32])
-    hist = [int(t) for t in prompt[:32]]
+    o = orc.Session(cfg, te, on, layers, prompt_n + max_new + 1)
+    lo = o.prefill(prompt[:prompt_n])
+    hist = [int(t) for t in prompt[:prompt_n]]
     t0 = time.perf_counter()
     n = 0
-    while n < 48 and (n < 3 or time.perf_counter() - t0 < budget_s):
+    while n < max_new and (n < 3 or time.perf_counter() - t0 < budget_s):
         t = orc.choose(lo, 1.1, 64, 0.0, hist)
         hist.append(t)
         lo = o.step(t)
@@ -227,8 +253,9 @@ def cpu_baseline(model_inputs, budget_s=12.0):
     dt = time.perf_counter() - t0
     log(f"cpu baseline: {n} tokens in {dt:.1f} s on {threads} threads")
     return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle decode of {n} greedy tokens (rp 1.1 / 64) of the same 28-layer q8_0 model after a 32-token "
-                      f"prompt (shorter attention context than the workload's 1024-1536; the weights dominate)"}
+            "sample": f"oracle (C restatement, OpenMP) greedy decode of {n} tokens (rp 1.1 / 64) of the same 28-layer q8_0 "
+                      f"model after a {prompt_n}-token prompt: attention context {prompt_n}-{prompt_n + n} keys, shorter "
+                      f"than the workload's 1024-1536 (the 633 MB of weights per token dominate either way)"}
 
 
 def main():
@@ -237,7 +264,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention")
+    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this path has no multi-GPU sharding (asked for {args.gpus})", file=sys.stderr)
@@ -278,12 +305,18 @@ def main():
         result["matvec"] = mv
         ach = mv["batched_launch_GBs"]
         result["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": ach / HBM_PEAK_GBS, "traffic": None,
-                              "kernel": "k_dmv_many (q8_0 matvec), 128 x W[3072x1024] per launch"}
+                              "frac": ach / HBM_PEAK_GBS, "traffic": load_traffic(),
+                              "kernel": "k_dmv_many: q8_0 matvec W[3072x1024] f32 x[1024] -> y[3072], 128 distinct W "
+                                        "copies per launch (430 MB, past the 256 MB Infinity Cache); algorithmic "
+                                        "bytes 3,358,720 per matvec",
+                              "algorithmic_bytes_per_launch": mv["batched_bytes_per_launch"],
+                              "avg_launch_us": mv["batched_launch_us"]}
     if want("choose"):
         result["choose"] = bench_choose(dev)
     if want("attention"):
         result["attention"] = bench_attention(dev)
+    if want("copy"):
+        result["copy"] = bench_copy(dev)
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)
     dev.close()

@@ -237,6 +237,31 @@ extern "C" int htr_download(htr_device *dev, void *h_dst, const void *d_src, siz
     return htr_hip(dev, hipStreamSynchronize(dev->stream), "download sync");
 }
 
+// ---- device copy (gpu.rs:2102-2110 Batch::copy → copy_words.wgsl) ---------------------------------------------------
+
+// dst[i] = src[i] over n 16-byte units (grid-stride), then the tail of < 16 bytes
+__global__ __launch_bounds__(256) void k_copy16(const int4 *src, int4 *dst, size_t n16, const uint8_t *src_tail,
+                                                uint8_t *dst_tail, int tail) {
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+    if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
+extern "C" int htr_copy(htr_device *dev, void *d_dst, const void *d_src, size_t bytes) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!bytes) return 0;
+    if (!d_dst || !d_src) return htr_fail("htr_copy: null pointer");
+    if (((uintptr_t)d_dst | (uintptr_t)d_src) & 15) return htr_fail("htr_copy: pointers must be 16-byte aligned");
+    const char *s = (const char *)d_src;
+    char *d = (char *)d_dst;
+    if ((s < d + bytes) && (d < s + bytes)) return htr_fail("htr_copy: %zu bytes from %p to %p overlap", bytes, d_src, d_dst);
+    const size_t n16 = bytes / 16;
+    const int tail = (int)(bytes % 16);
+    const int grid = (int)std::max<size_t>(1, std::min<size_t>((n16 + 255) / 256, (size_t)dev->n_cu * 8));
+    hipLaunchKernelGGL(k_copy16, dim3(grid), dim3(256), 0, dev->stream, (const int4 *)d_src, (int4 *)d_dst, n16,
+                       (const uint8_t *)(s + 16 * n16), (uint8_t *)(d + 16 * n16), tail);
+    return htr_launched(dev, "k_copy16");
+}
+
 // ---- weights --------------------------------------------------------------------------------------------------------
 
 static inline uint16_t f16_bits_rne(float v);  // below

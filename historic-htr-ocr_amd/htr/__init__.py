@@ -23,7 +23,8 @@ MEM_WEIGHTS, MEM_KV_CACHE, MEM_WORK, MEM_READBACK = 0, 1, 2, 3
 # every symbol include/htr.h declares
 SYMBOLS = [
     "htr_last_error", "htr_device_open", "htr_device_close", "htr_alive", "htr_set_fatal_hook", "htr_debug_mark_lost",
-    "htr_sync", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free", "htr_upload", "htr_download", "htr_phase",
+    "htr_sync", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free",
+    "htr_upload", "htr_download", "htr_copy", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
     "htr_choose_many", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
@@ -88,6 +89,7 @@ def lib() -> C.CDLL:
             "htr_free": (i32, [vp, vp]),
             "htr_upload": (i32, [vp, vp, vp, sz]),
             "htr_download": (i32, [vp, vp, vp, sz]),
+            "htr_copy": (i32, [vp, vp, vp, sz]),
             "htr_phase": (i32, [vp, C.c_char_p]),
             "htr_weight_q8_0": (i32, [vp, vp, sz, sz, pp]),
             "htr_weight_q8_0_f16": (i32, [vp, vp, sz, sz, f32, pp]),
@@ -178,6 +180,12 @@ class Buffer:
         out = np.empty(n, dtype=dt)
         _check(lib().htr_download(self.dev.h, _ptr(out), self.ptr, out.nbytes))
         return out
+
+    def copy_from(self, src: "Buffer", nbytes: int | None = None) -> "Buffer":
+        """device → device copy (gpu.rs Batch::copy)"""
+        n = min(self.nbytes, src.nbytes) if nbytes is None else nbytes
+        _check(lib().htr_copy(self.dev.h, self.ptr, src.ptr, n))
+        return self
 
     def free(self) -> None:
         if self.ptr:

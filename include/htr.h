@@ -70,6 +70,9 @@ int htr_free(htr_device *dev, void *d_ptr);
 /* host ↔ device copies on the device's stream; htr_download waits for it */
 int htr_upload(htr_device *dev, void *d_dst, const void *h_src, size_t bytes);
 int htr_download(htr_device *dev, void *h_dst, const void *d_src, size_t bytes);
+/* d_dst[0 … bytes) = d_src[0 … bytes) on the device's stream, both 16-byte aligned, not overlapping (gpu.rs:2102-2110
+ * Batch::copy). Also the plain copy of known size that calibrates the HBM byte counters. */
+int htr_copy(htr_device *dev, void *d_dst, const void *d_src, size_t bytes);
 /* a phase label for the profiler ranges (gpu.rs:1349-1358 Gpu::phase) */
 int htr_phase(htr_device *dev, const char *name);
 
