@@ -7,26 +7,16 @@
 // KV cache layout (this library's): f16, head-major per layer, [n_kv][n_ctx][128] — one KV head's keys are
 // contiguous, so a workgroup working on (kv head, key chunk) reads one contiguous range (256 bytes per key).
 #include "htr_internal.h"
+#include "wave.h"
 
 namespace {
 
 constexpr int D = 128;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
 // one head's 128 values held as (lane, lane + 64) by a 64-lane wave: RMS norm with w, then RoPE NEOX with (c, s)
 __device__ __forceinline__ void norm_rope(float &x0, float &x1, const float *w, const float *rope_row, int lane,
                                           float eps) {
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float ss = wave_sum(x0 * x0 + x1 * x1, lane);
     const float scale = 1.0f / sqrtf(ss / (float)D + eps);
     const float y0 = (x0 * scale) * w[lane], y1 = (x1 * scale) * w[lane + 64];
     const float c = rope_row[2 * lane], s = rope_row[2 * lane + 1];
@@ -97,16 +87,22 @@ __global__ __launch_bounds__(64) void k_qk_rows(float *q, float *k, const float 
 // kk + 16·i (kk = t >> 4, i < NI): one wave-wide load reads 4 keys (1 KiB), and every K and V load of the chunk is
 // issued before the first use.
 //   1. scores s[h][key] = (q_h·scale)·k: 8 products per slice, summed over the 16 slices of a key by an
-//      exchange-and-halve butterfly over all 2·NI (key, head) values at once → LDS
-//   2. per head (one wave each): m = max s, p = exp(s − m), l = Σ p → LDS
-//   3. o[h][·] = Σ p·v from the V registers, summed over the 16 key positions (lanes, then the 4 waves in LDS)
+//      exchange-and-halve butterfly over all 2·NI (key, head) values at once → LDS (barrier)
+//   2. every wave: m = max s, p = exp(s − m), l = Σ p for both heads → its own LDS copy of p (no barrier)
+//   3. o[h][·] = Σ p·v from the V registers, summed over the 16 key positions (lane bits 5, 4, then the 4 waves in
+//      LDS: barrier)
 //   4. the chunk's (m, l, o) → partials [h][c][130]; the last workgroup of the KV head (atomic ticket) merges:
-//      M = max m_c, w_c = e^(m_c − M), O = Σ o_c·w_c / Σ l_c·w_c, every thread issuing its loads of all chunks at
-//      once. A single-chunk call writes O = o / l directly.
+//      M = max m_c, w_c = e^(m_c − M), O = Σ o_c·w_c / Σ l_c·w_c — each wave one (head, 64 dims), its loads of all
+//      chunks issued at once, no workgroup barrier. A single-chunk call writes O = o / l directly.
+// Cross-lane moves are DPP / permlane VALU moves (wave.h). Cross-workgroup traffic is device-scope (sc1) stores and
+// loads plus the ticket atomic (one 128-byte line per KV head): a release fence per workgroup would write back the
+// L2 each time.
 constexpr int AW = 256;
 constexpr int MAX_CHUNK_KEYS = 256;  // C ≤ 256 (NI ≤ 16)
 constexpr int MAX_CHUNKS = 256;      // chunks per KV head: n_ctx ≤ 65536
-constexpr int MERGE_PREFETCH = 64;   // chunk partials each merging thread holds in registers before the loop
+constexpr int MERGE_PREFETCH = 64;   // chunk partials each merging thread holds in registers (= the wave size: their
+                                     // weights are read from the lanes that hold them)
+constexpr int CNT_STRIDE = 32;       // ticket counters 128 bytes apart: the KV heads' atomics do not share a line
 
 __device__ __forceinline__ int4 aload16(const void *p) { return *reinterpret_cast<const int4 *>(p); }
 
@@ -123,21 +119,11 @@ __device__ __forceinline__ void unpack8(const int4 w, float (&f)[8]) {
     }
 }
 
-// exchange-and-halve over the lane bits of `masks` (high to low): v[0 … N) of every lane → each lane keeps N / 2^S
-// sums over the 2^S lanes that differ in those bits; lane bit (mask) set keeps the upper half at each step.
-template <int N, int M0, int S> __device__ __forceinline__ void halve(float (&v)[N], int lane) {
-#pragma unroll
-    for (int s = 0, n = N / 2, m = M0; s < S; s++, n >>= 1, m >>= 1) {
-        const bool hi = (lane & m) != 0;
-#pragma unroll
-        for (int i = 0; i < N / 2; i++) {
-            if (i < n) {
-                const float send = hi ? v[i] : v[i + n];
-                const float keep = hi ? v[i + n] : v[i];
-                v[i] = keep + __shfl_xor(send, m, 64);
-            }
-        }
-    }
+__device__ __forceinline__ float ld_dev(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int NI>
@@ -145,15 +131,16 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
                                                     int n_ctx, const int *pos_dev, int n_keys_arg, int max_chunk,
                                                     float scale, float *part, uint32_t *counters, float *out) {
     constexpr int C = 16 * NI;
-    constexpr int N = 2 * NI;  // (key, head) values per thread
-    __shared__ float s_p[2][C];
-    __shared__ float s_ml[2][2];
+    constexpr int N = 2 * NI;              // (key, head) values per thread
+    constexpr int KL = C >= 64 ? C / 64 : 1;  // keys per lane in the softmax
+    __shared__ float s_sc[2][C];
+    __shared__ float s_pw[4][2][C];  // each wave's copy of p
+    __shared__ float s_lw[2];
     __shared__ float s_o[4][2][D];
-    __shared__ float s_w[2][MAX_CHUNKS];
-    __shared__ float s_red[2][4];
+    __shared__ float s_w[4][MAX_CHUNKS];
     __shared__ int s_last;
     const int c = blockIdx.x, kvh = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = tid & 15, kk = tid >> 4;
     // keys beyond the cache are never read (the host checks positions first; a bad one yields no output)
     const int n_keys = min(pos_dev ? *pos_dev + 1 : n_keys_arg, n_ctx);
@@ -197,53 +184,51 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         v[2 * i] = da;
         v[2 * i + 1] = db;
     }
-    if (N >= 16) {
+    if constexpr (N >= 16) {
         halve<N, 8, 4>(v, lane);  // lane j keeps values (N/16)·j + r
 #pragma unroll
-        for (int r = 0; r < (N >= 16 ? N / 16 : 1); r++) {
+        for (int r = 0; r < N / 16; r++) {
             const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
             const int key = kk + 16 * i;
-            s_p[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
+            s_sc[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
         }
     } else {
         constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;  // log2 N
         halve<N, 8, S>(v, lane);                         // lane j keeps value j >> (4 − S)
-        float t = v[0];
-#pragma unroll
-        for (int m = 8 >> S; m > 0; m >>= 1) t += __shfl_xor(t, m, 64);
+        const float t = group_sum<(8 >> S)>(v[0], lane);
         if ((j & ((16 >> S) - 1)) == 0) {
             const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
             const int key = kk + 16 * i;
-            s_p[h][key] = k0 + key < n_keys ? t : -INFINITY;
+            s_sc[h][key] = k0 + key < n_keys ? t : -INFINITY;
         }
     }
     __syncthreads();
 
-    // 2. softmax statistics, one wave per head
-    if (wave < 2) {
-        float sv[(C + 63) / 64], mx = -INFINITY;
+    // 2. softmax statistics, every wave for both heads into its own copy of p
+    float l_h[2];
 #pragma unroll
-        for (int i = 0; i < (C + 63) / 64; i++) {
+    for (int h = 0; h < 2; h++) {
+        float sv[KL], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < KL; i++) {
             const int key = lane + 64 * i;
-            sv[i] = key < C ? s_p[wave][key] : -INFINITY;
+            sv[i] = key < C ? s_sc[h][key] : -INFINITY;
             mx = fmaxf(mx, sv[i]);
         }
-        mx = wave_max(mx);
+        mx = wave_max(mx, lane);
         float l = 0.0f;
 #pragma unroll
-        for (int i = 0; i < (C + 63) / 64; i++) {
+        for (int i = 0; i < KL; i++) {
             const int key = lane + 64 * i;
             const float p = expf(sv[i] - mx);  // masked keys: exp(−inf) = 0
-            if (key < C) s_p[wave][key] = p;
+            if (key < C) s_pw[wave][h][key] = p;
             l += p;
         }
-        l = wave_sum(l);
-        if (lane == 0) {
-            s_ml[wave][0] = mx;
-            s_ml[wave][1] = l;
-        }
+        l_h[h] = wave_sum(l, lane);
+        if (h == 0 && wave == 0 && lane == 0) s_lw[0] = mx;
+        if (h == 1 && wave == 0 && lane == 0) s_lw[1] = mx;
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
 
     // 3. values
     float o[16];  // [h][e]
@@ -253,7 +238,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
     for (int i = 0; i < NI; i++) {
         float vf[8];
         unpack8(vr[i], vf);
-        const float pa = s_p[0][kk + 16 * i], pb = s_p[1][kk + 16 * i];
+        const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             o[e] = fmaf(pa, vf[e], o[e]);
@@ -272,64 +257,64 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
     __syncthreads();
     const int hh = tid >> 7, d = tid & 127;  // 256 threads = 2 heads × 128 dims
     const float oc = (s_o[0][hh][d] + s_o[1][hh][d]) + (s_o[2][hh][d] + s_o[3][hh][d]);
+    const float lc = l_h[hh];  // every wave holds both heads' sums
     const int h = h0 + hh;
     if (n_chunk == 1) {
-        out[h * D + d] = oc / s_ml[hh][1];
+        out[h * D + d] = oc / lc;
         return;
     }
 
-    // 4. partials, then the last workgroup of the KV head merges. Cross-workgroup traffic is device-scope (sc1)
-    // stores and loads plus the ticket atomic: a release fence per workgroup would write back the L2 each time.
+    // 4. partials, then the last workgroup of the KV head merges
     float *pc = part + ((size_t)h * max_chunk + c) * (D + 2);  // [h][c][m, l, o[128]]
-    __hip_atomic_store(pc + 2 + d, oc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d < 2) __hip_atomic_store(pc + d, s_ml[hh][d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    st_dev(pc + 2 + d, oc);
+    if (d == 0) st_dev(pc, s_lw[hh]);
+    if (d == 1) st_dev(pc + 1, lc);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are performed
     __syncthreads();
+    uint32_t *ticket = counters + (size_t)kvh * CNT_STRIDE;
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(&counters[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (uint32_t)(n_chunk - 1);
     __syncthreads();
     if (!s_last) return;
-    // this thread's o partials (the first MERGE_PREFETCH chunks) go out now, with m and l
-    const float *ph = part + (size_t)h * max_chunk * (D + 2);
+    // the merge: wave w → head h0 + (w >> 1), dims (w & 1)·64 + lane. The m and l of the chunks lane, lane + 64, … go
+    // out first, then the o partials: the weights are computed while the o loads are in flight
+    const int mh = h0 + (wave >> 1), md = (wave & 1) * 64 + lane;
+    const float *ph = part + (size_t)mh * max_chunk * (D + 2);
+    float mv[MAX_CHUNKS / 64], lv[MAX_CHUNKS / 64];
+#pragma unroll
+    for (int k = 0; k < MAX_CHUNKS / 64; k++) {
+        const int cc = lane + 64 * k;
+        mv[k] = cc < n_chunk ? ld_dev(ph + (size_t)cc * (D + 2)) : -INFINITY;
+        lv[k] = cc < n_chunk ? ld_dev(ph + (size_t)cc * (D + 2) + 1) : 0.0f;
+    }
     float ov[MERGE_PREFETCH];
 #pragma unroll
-    for (int i = 0; i < MERGE_PREFETCH; i++)
-        ov[i] = i < n_chunk ? __hip_atomic_load(ph + (size_t)i * (D + 2) + 2 + d, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT)
-                            : 0.0f;
-    // M and the weights w_c = e^(m_c − M) of each head: 128 threads per head, chunks c = i, i + 128
-    const int i0 = tid & 127;
-    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
-    if (i0 < n_chunk) {
-        m0 = __hip_atomic_load(ph + (size_t)i0 * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        l0 = __hip_atomic_load(ph + (size_t)i0 * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < MERGE_PREFETCH; i++) ov[i] = i < n_chunk ? ld_dev(ph + (size_t)i * (D + 2) + 2 + md) : 0.0f;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < MAX_CHUNKS / 64; k++) mx = fmaxf(mx, mv[k]);
+    mx = wave_max(mx, lane);
+    float L = 0.0f, w0 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_CHUNKS / 64; k++) {
+        const int cc = lane + 64 * k;
+        const float w = expf(mv[k] - mx);  // chunks past the end: e^(−inf) = 0
+        if (k == 0) w0 = w;
+        else if (cc < n_chunk) s_w[wave][cc] = w;  // chunks ≥ 64 (long contexts): through LDS
+        L = fmaf(lv[k], w, L);
     }
-    if (i0 + 128 < n_chunk) {
-        m1 = __hip_atomic_load(ph + (size_t)(i0 + 128) * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        l1 = __hip_atomic_load(ph + (size_t)(i0 + 128) * (D + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    float mx = wave_max(fmaxf(m0, m1));
-    if (lane == 0) s_red[hh][wave & 1] = mx;
-    __syncthreads();
-    mx = fmaxf(s_red[hh][0], s_red[hh][1]);
-    const float w0 = expf(m0 - mx), w1 = expf(m1 - mx);  // chunks past the end: e^(−inf) = 0
-    if (i0 < n_chunk) s_w[hh][i0] = w0;
-    if (i0 + 128 < n_chunk) s_w[hh][i0 + 128] = w1;
-    float L = wave_sum(fmaf(l0, w0, l1 * w1));
-    __syncthreads();  // s_red reused below
-    if (lane == 0) s_red[hh][wave & 1] = L;
-    __syncthreads();
-    L = s_red[hh][0] + s_red[hh][1];
+    L = wave_sum(L, lane);
+    // the first 64 chunks' weights straight from the lane that holds them (a scalar operand of the fma; LDS reads
+    // would put one LDS round trip per chunk on this dependent chain)
     float O = 0.0f;
 #pragma unroll
     for (int i = 0; i < MERGE_PREFETCH; i++)
-        if (i < n_chunk) O = fmaf(ov[i], s_w[hh][i], O);
-    for (int cc = MERGE_PREFETCH; cc < n_chunk; cc++)
-        O = fmaf(__hip_atomic_load(ph + (size_t)cc * (D + 2) + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 s_w[hh][cc], O);
-    out[h * D + d] = O / L;
-    if (tid == 0) counters[kvh] = 0;  // ready for the next launch
+        if (i < n_chunk) O = fmaf(ov[i], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w0), i)), O);
+    __builtin_amdgcn_wave_barrier();
+    for (int cc = MERGE_PREFETCH; cc < n_chunk; cc++) O = fmaf(ld_dev(ph + (size_t)cc * (D + 2) + 2 + md), s_w[wave][cc], O);
+    out[mh * D + md] = O / L;
+    if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
 }
 
 // ---- prefill causal attention --------------------------------------------------------------------------------------
@@ -393,14 +378,18 @@ __global__ __launch_bounds__(128) void k_attn_causal(const float *q, const _Floa
 }  // namespace
 
 int attn_chunk_for(int n_ctx) {
-    // 16 keys per workgroup, doubled while a KV head would need more than 64 chunks (so at most 64 partials per head
-    // are merged for n_ctx ≤ 16384), up to 256 keys
+    // 16 keys per workgroup, doubled while a KV head would need more than 32 chunks (at most 32 partials per head are
+    // merged for n_ctx ≤ 8192), up to 256 keys. Measured on one MI355X at 1536 keys: 24 chunks of 64 keys 6.95 µs a
+    // launch, 48 of 32 8.2 µs, 96 of 16 12.3 µs, 12 of 128 7.15 µs (the merge and the ticket grow with the chunk
+    // count, the workgroup's own load phase with its keys)
     int chunk = 16;
-    while ((n_ctx + chunk - 1) / chunk > 64 && chunk < MAX_CHUNK_KEYS) chunk *= 2;
+    while ((n_ctx + chunk - 1) / chunk > 32 && chunk < MAX_CHUNK_KEYS) chunk *= 2;
     return chunk;
 }
 
 size_t attn_part_bytes(int n_head, int max_chunk) { return (size_t)n_head * max_chunk * (D + 2) * 4; }
+
+size_t attn_counter_bytes(int n_kv) { return (size_t)n_kv * CNT_STRIDE * 4; }
 
 int launch_qkv_post(htr_device *dev, hipStream_t st, float *qkv, const float *qn, const float *kn, const float *rope,
                     int n_head, int n_kv, const int *pos_dev, int pos, int n_ctx, float eps, uint16_t *kc,
@@ -473,6 +462,6 @@ extern "C" int htr_decode_attention(htr_device *dev, const float *d_q, const uin
     sc.chunk = attn_chunk_for(n_ctx);
     sc.max_chunk = (n_ctx + sc.chunk - 1) / sc.chunk;
     HTR_TRY(htr_scratch(dev, SCR_ATTN_PART, attn_part_bytes(n_head, sc.max_chunk), (void **)&sc.part));
-    HTR_TRY(htr_scratch(dev, SCR_ATTN_CNT, (size_t)n_kv * 4, (void **)&sc.counters));
+    HTR_TRY(htr_scratch(dev, SCR_ATTN_CNT, attn_counter_bytes(n_kv), (void **)&sc.counters));
     return launch_attn_decode(dev, dev->stream, d_q, d_k, d_v, n_head, n_kv, n_ctx, nullptr, n_keys, scale, sc, d_out);
 }

@@ -21,11 +21,14 @@
 #include <cmath>
 
 #include "htr_internal.h"
+#include "wave.h"
 
 namespace {
 
 constexpr int CW = 256;
-constexpr int SPAN = 1024;
+constexpr int SPAN = 4096;          // logits per workgroup (16 per thread): 38 workgroups over 151,936
+constexpr int PER = SPAN / CW;
+constexpr int LINE = 16;            // u64 words between rows' best keys / u32 between tickets: one 128-byte line each
 constexpr int WIN_LDS = CW;  // windows up to this many ids are staged in LDS (longer ones are read from memory)
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float w, uint32_t j) { return v > w || (v == w && i < j); }
@@ -39,16 +42,20 @@ __device__ __forceinline__ uint64_t choose_key(float v, uint32_t i) {
     return ((uint64_t)b << 32) | (uint64_t)(~i);
 }
 
-__device__ __forceinline__ void wave_best(float &v, uint32_t &i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const uint32_t oi = __shfl_xor(i, off, 64);
-        if (better(ov, oi, v, i)) {
-            v = ov;
-            i = oi;
-        }
+__device__ __forceinline__ void wave_best(float &v, uint32_t &i, int lane) {
+    // the partner moves of wave.h (for bits 4 and 8 the partner also differs in lower bits: `better` is a total order
+    // on (value, index) pairs without NaN, so the order in which lanes meet does not matter)
+#define HTR_BEST_STEP(M)                                                                                               \
+    {                                                                                                                  \
+        const float ov = lane_swap<M>(v, lane);                                                                        \
+        const uint32_t oi = lane_swap_u32<M>(i, lane);                                                                 \
+        if (better(ov, oi, v, i)) {                                                                                    \
+            v = ov;                                                                                                    \
+            i = oi;                                                                                                    \
+        }                                                                                                              \
     }
+    HTR_BEST_STEP(32) HTR_BEST_STEP(16) HTR_BEST_STEP(8) HTR_BEST_STEP(4) HTR_BEST_STEP(2) HTR_BEST_STEP(1)
+#undef HTR_BEST_STEP
 }
 
 // block-wide best of (v, i) → returned to every thread
@@ -56,7 +63,7 @@ __device__ __forceinline__ void block_best(float &v, uint32_t &i) {
     __shared__ float s_v[CW / 64];
     __shared__ uint32_t s_i[CW / 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    wave_best(v, i);
+    wave_best(v, i, lane);
     __syncthreads();
     if (lane == 0) {
         s_v[wave] = v;
@@ -88,7 +95,29 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
     const int n_win = a.rp != 1.0f ? len - start : 0;
     const bool win_lds = n_win <= WIN_LDS;
     if (win_lds && tid < n_win) s_win[tid] = hist[start + tid];
-    for (int i = tid; i < hi - lo; i += CW) s_l[i] = logits[lo + i];
+    // the span's logits → LDS: every load issued before the first store (16-byte loads when the row is aligned)
+    if ((((uintptr_t)(logits + lo)) & 15) == 0) {
+        float4 lv[PER / 4];
+#pragma unroll
+        for (int i = 0; i < PER / 4; i++) {
+            const int e = 4 * tid + SPAN / 4 * i;
+            lv[i] = lo + e + 3 < hi ? *reinterpret_cast<const float4 *>(logits + lo + e) : make_float4(0, 0, 0, 0);
+            if (lo + e + 3 >= hi) {  // the row's ragged end
+                float t[4] = {0, 0, 0, 0};
+                for (int u = 0; u < 4; u++)
+                    if (lo + e + u < hi) t[u] = logits[lo + e + u];
+                lv[i] = make_float4(t[0], t[1], t[2], t[3]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER / 4; i++) *reinterpret_cast<float4 *>(s_l + 4 * tid + SPAN / 4 * i) = lv[i];
+    } else {
+        float lv[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) lv[i] = lo + tid + CW * i < hi ? logits[lo + tid + CW * i] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; i++) s_l[tid + CW * i] = lv[i];
+    }
     __syncthreads();
     // the window's distinct ids in [lo, hi): the first occurrence of each applies the penalty
     if (n_win > 0) {
@@ -110,19 +139,28 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
         __syncthreads();
     }
     // pass 1: this workgroup's best (NaN never wins: `better` is false for it)
+    // (a fixed count of LDS reads, all issued before the first compare)
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
-    for (int i = tid; i < hi - lo; i += CW) {
-        float x = s_l[i];
-        const uint32_t k = (uint32_t)(lo + i);
-        if (a.fp != 0.0f && a.counts[k] != 0u) x = x - a.fpen[k];
-        if (better(x, k, bv, bi)) {
-            bv = x;
-            bi = k;
+    float xs[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) xs[i] = s_l[tid + CW * i];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int e = tid + CW * i;
+        if (lo + e < hi) {
+            float x = xs[i];
+            const uint32_t k = (uint32_t)(lo + e);
+            if (a.fp != 0.0f && a.counts[k] != 0u) x = x - a.fpen[k];
+            if (better(x, k, bv, bi)) {
+                bv = x;
+                bi = k;
+            }
         }
     }
     block_best(bv, bi);
-    uint64_t *best = a.best + row;
+    uint64_t *best = a.best + (size_t)row * LINE;
+    uint32_t *ticket = a.counters + (size_t)row * LINE;
     if (tid == 0) {
         // a NaN at index 0 after the penalty decides token 0 (the CPU loop never finds a greater value): top key
         const bool nan0 = lo == 0 && s_l[0] != s_l[0];
@@ -130,7 +168,7 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
         __hip_atomic_fetch_max(best, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // the max is performed before the ticket: wait for its return
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        s_last = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  gridDim.x - 1;
     }
     __syncthreads();
@@ -149,13 +187,16 @@ __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
     if (a.len_dev) *(int *)a.len_dev = len + 1;
     if (a.advance) a.advance[0] += 1;
     // ready for the next launch (seen by it: a kernel boundary)
-    *best = 0ull;
-    a.counters[row] = 0u;
+    __hip_atomic_store(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
 int choose_groups(int n_vocab) { return (n_vocab + SPAN - 1) / SPAN; }
+
+size_t choose_best_bytes(int rows) { return (size_t)rows * LINE * 8; }
+size_t choose_ticket_bytes(int rows) { return (size_t)rows * LINE * 4; }
 
 int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a) {
     if (a.n_vocab <= 0 || a.rows <= 0) return htr_fail("choose: %d logits, %d rows", a.n_vocab, a.rows);
@@ -171,8 +212,8 @@ static int check_rp(float rp) {
 }
 
 static int choose_scratch(htr_device *dev, int rows, uint64_t **best, uint32_t **counters) {
-    HTR_TRY(htr_scratch(dev, SCR_CHOOSE_PART, (size_t)rows * 8, (void **)best));
-    return htr_scratch(dev, SCR_CHOOSE_CNT, (size_t)rows * 4, (void **)counters);
+    HTR_TRY(htr_scratch(dev, SCR_CHOOSE_PART, choose_best_bytes(rows), (void **)best));
+    return htr_scratch(dev, SCR_CHOOSE_CNT, choose_ticket_bytes(rows), (void **)counters);
 }
 
 extern "C" int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_t *d_hist, int len, int window, float rp,

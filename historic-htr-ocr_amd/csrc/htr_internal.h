@@ -103,6 +103,8 @@ struct AttnScratch {
 int attn_chunk_for(int n_ctx);
 // bytes of the split-K partials for n_head q heads and max_chunk chunks ([h][c][m, l, o[128]] f32)
 size_t attn_part_bytes(int n_head, int max_chunk);
+// bytes of the split-K ticket counters (one 128-byte line per KV head; zero, self-resetting)
+size_t attn_counter_bytes(int n_kv);
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
                        const AttnScratch &sc, float *out);
@@ -128,11 +130,14 @@ struct ChooseArgs {
     float *fpen;
     uint32_t *tok;
     int *advance;  // NULL, or { pos, len } incremented by the pick (the decode loop's device-resident counters)
-    uint64_t *best;      // [rows], zero, self-resetting: the row's best key
-    uint32_t *counters;  // [rows], zero, self-resetting
+    uint64_t *best;      // [rows] × 128 B, zero, self-resetting: the row's best key
+    uint32_t *counters;  // [rows] × 128 B, zero, self-resetting: the row's ticket
     int rows;
 };
 int choose_groups(int n_vocab);
+// bytes of the choice's per-row best keys and tickets (one 128-byte line per row; zero, self-resetting)
+size_t choose_best_bytes(int rows);
+size_t choose_ticket_bytes(int rows);
 int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a);
 
 // dense kernels (gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ with W q8_0 (exact dequant), f32; rms_norm rows; swiglu

@@ -11,14 +11,16 @@
 //             the wave's rows is issued before the first use; the tile's f16 scales (contiguous: rows are back to
 //             back) are copied into LDS by the whole workgroup while those loads are in flight;
 //   reduce    the RW per-lane partials of a wave are summed across the 64 lanes by one transposing butterfly:
-//             exchange-and-halve steps (masks 32, 16, …) leave one row per lane group, then a plain butterfly over
-//             the rest — RW−1 + log2(64/RW) cross-lane moves instead of 6·RW;
+//             exchange-and-halve steps (lane bits 32, 16, …) leave one row per lane group, then a plain butterfly over
+//             the rest — RW−1 + log2(64/RW) cross-lane moves instead of 6·RW, each a DPP / permlane VALU move
+//             (wave.h);
 //   norm      the fused RMS norm is computed on the registers: the wave's lanes hold all K inputs, so Σx² is one
 //             wave sum (no workgroup barrier, no second read of x);
 //   math      f32 (the reference's numbers: exact int8·f16-scale dequant, f32 products and sums): the 16 products
 //             of a group are an fma chain, times the block's scale into the row's accumulator. The int8 → f32
 //             conversion is one v_cvt_f32_i32 with a sign-extended byte select per quant.
 #include "htr_internal.h"
+#include "wave.h"
 
 namespace {
 
@@ -78,12 +80,6 @@ __device__ __forceinline__ DmvMat uniform_mat(const DmvMat &m) {
     return DmvMat{uniform_ptr(m.q), uniform_ptr(m.d), __builtin_amdgcn_readfirstlane(m.rows)};
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // Σ_j q_j · x_j over the 16 quants of one group (fma chain)
 __device__ __forceinline__ float dot16(const int4 q, const float *x) {
     const int w[4] = {q.x, q.y, q.z, q.w};
@@ -93,28 +89,6 @@ __device__ __forceinline__ float dot16(const int4 q, const float *x) {
 #pragma unroll
         for (int b = 0; b < 4; b++) s = fmaf((float)(int8_t)(w[i] >> (8 * b)), x[4 * i + b], s);
     }
-    return s;
-}
-
-// Sums v[r] over the wave for every r < N (a power of two ≤ 64). On return the lanes whose low log2(64/N) bits are
-// zero hold a total: lane ℓ holds row ℓ / (64/N). Exchange-and-halve: at mask m the lane keeps the half of its values
-// its bit m selects and adds the partner's copy of that half.
-template <int N> __device__ __forceinline__ float wave_sum_rows(float (&v)[N], int lane) {
-#pragma unroll
-    for (int n = N / 2, m = 32; n >= 1; n >>= 1, m >>= 1) {
-        const bool hi = (lane & m) != 0;
-#pragma unroll
-        for (int i = 0; i < (N > 1 ? N / 2 : 1); i++) {
-            if (i < n) {
-                const float send = hi ? v[i] : v[i + n];
-                const float keep = hi ? v[i + n] : v[i];
-                v[i] = keep + __shfl_xor(send, m, 64);
-            }
-        }
-    }
-    float s = v[0];
-#pragma unroll
-    for (int m = 32 / N; m > 0; m >>= 1) s += __shfl_xor(s, m, 64);
     return s;
 }
 
@@ -150,13 +124,13 @@ __device__ __forceinline__ void load_x(float (&xv)[NG][16], float (&wv)[NG][16],
 // the fused RMS norm (dmv_common.wgsl:23-30) on the registers: x · 1/sqrt(Σx²/K + eps) · nw. Σx² is a wave sum: the
 // wave holds all of x, so no workgroup barrier.
 template <int NG>
-__device__ __forceinline__ void norm_x(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k) {
+__device__ __forceinline__ void norm_x(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k, int lane) {
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < NG; i++)
 #pragma unroll
         for (int j = 0; j < 16; j++) s = fmaf(xv[i][j], xv[i][j], s);
-    const float scale = 1.0f / sqrtf(wave_sum(s) / (float)k + eps);
+    const float scale = 1.0f / sqrtf(wave_sum(s, lane) / (float)k + eps);
 #pragma unroll
     for (int i = 0; i < NG; i++)
 #pragma unroll
@@ -279,7 +253,7 @@ template <int RW, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv(
         load_row<NG>(qv[0][r], m, lr, k, lane, ng);
         if (NM == 2) load_row<NG>(qv[NM - 1][r], a.m[1], lr, k, lane, ng);
     }
-    if (MODE != DMV_PLAIN) norm_x<NG>(xv, wv, a.eps, k);
+    if (MODE != DMV_PLAIN) norm_x<NG>(xv, wv, a.eps, k, lane);
     scales_store(s_d[0], ss[0], row0, RT, a.n_rows, nb, mat_of);
     if (NM == 2) scales_store(s_d[NM - 1], ss[NM - 1], row0, RT, a.n_rows, nb, up_of);
     __syncthreads();

@@ -306,7 +306,7 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->state);
     if (rc == 0)
         rc = htr_dev_alloc(dev, attn_part_bytes(c.n_head, s->asc.max_chunk), HTR_MEM_WORK, (void **)&s->asc.part);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_kv * 4, HTR_MEM_WORK, (void **)&s->asc.counters);
+    if (rc == 0) rc = htr_dev_alloc(dev, attn_counter_bytes(c.n_kv), HTR_MEM_WORK, (void **)&s->asc.counters);
     if (rc == 0) rc = htr_sync(dev);
     if (rc < 0) {
         std::string keep = htr_last_error();
@@ -476,8 +476,8 @@ extern "C" int htr_choice_create(htr_session *s, const htr_preset *p, const int3
     if (rc == 0) rc = htr_upload(dev, ch->hist, hist.data(), hist.size() * 4);
     if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->counts);
     if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->fpen);
-    if (rc == 0) rc = htr_dev_alloc(dev, 8, HTR_MEM_WORK, (void **)&ch->best);
-    if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&ch->counters);
+    if (rc == 0) rc = htr_dev_alloc(dev, choose_best_bytes(1), HTR_MEM_WORK, (void **)&ch->best);
+    if (rc == 0) rc = htr_dev_alloc(dev, choose_ticket_bytes(1), HTR_MEM_WORK, (void **)&ch->counters);
     if (rc == 0) rc = htr_hip(dev, hipHostMalloc((void **)&ch->h_ids, depth * chunk * 4, hipHostMallocDefault), "hipHostMalloc");
     for (size_t i = 0; i < depth && rc == 0; i++) {
         hipEvent_t e;
