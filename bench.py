@@ -202,6 +202,53 @@ def bench_attention(dev, n_head=16, n_kv=8):
     return res
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
+    """config 4's encoder-layer GEMMs on the matrix cores at one page's 12100 patch rows: q, k, v, o [1024 x 1024],
+    gate + up fused with SwiGLU [4096 x 1024] x 2, down [1024 x 4096] (q8_0 weights dequantised to f16 at load)"""
+    x16 = dev.upload(synth_normal_f16(71, m * ff))
+    y = dev.alloc(m * dim * 4)
+    g16 = dev.alloc(m * ff * 2)
+    ws = {name: htr.Weight(dev, htr.synth_q8_0(600 + i, rows, cols), rows, cols, f16=True,
+                           scale=64.0 if name == "down" else 1.0)
+          for i, (name, rows, cols) in enumerate([("q", dim, dim), ("k", dim, dim), ("v", dim, dim), ("o", dim, dim),
+                                                  ("gate", ff, dim), ("up", ff, dim), ("down", dim, ff)])}
+
+    def layer():
+        for name in ("q", "k", "v"):
+            htr.gemm_f16(dev, x16, m, ws[name], y)
+        htr.gemm_f16(dev, x16, m, ws["o"], y, acc=True)
+        htr.gemm_ffn_f16(dev, x16, m, ws["gate"], ws["up"], 1.0 / 64, g16)
+        htr.gemm_f16(dev, g16, m, ws["down"], y, acc=True)
+
+    layer()
+    dev.timer_begin()
+    for _ in range(reps):
+        layer()
+    ms = dev.timer_end() / reps
+    flop = 2.0 * m * (4 * dim * dim + 2 * ff * dim + dim * ff)
+    # the single largest GEMM alone (gate + up, 2 x 101.5 GFLOP)
+    dev.timer_begin()
+    for _ in range(reps):
+        htr.gemm_ffn_f16(dev, x16, m, ws["gate"], ws["up"], 1.0 / 64, g16)
+    ms_ffn = dev.timer_end() / reps
+    for w in ws.values():
+        w.free()
+    res = {"rows": m, "layer_gemm_ms": ms, "layer_gemm_flop": flop, "tflops": flop / (ms * 1e-3) / 1e12,
+           "ffn_ms": ms_ffn, "ffn_tflops": 2.0 * m * 2 * ff * dim / (ms_ffn * 1e-3) / 1e12}
+    res["frac_mfma_peak"] = res["tflops"] / MFMA_F16_PEAK_TFLOPS
+    res["encoder_gemm_ms_24_layers"] = 24 * ms
+    log(f"vision GEMMs: {ms:.3f} ms per layer ({res['tflops']:.0f} TFLOP/s, {100 * res['frac_mfma_peak']:.1f} % of "
+        f"the f16 MFMA peak); FFN gate/up {res['ffn_tflops']:.0f} TFLOP/s")
+    return res
+
+
+def synth_normal_f16(seed, n):
+    return htr.synth_normal(seed, n).astype(np.float16)
+
+
 def bench_copy(dev, mib=512, reps=5):
     """a plain device copy of known size (htr_copy): the HBM reference point of the byte counters"""
     n = mib << 20
@@ -264,7 +311,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy")
+    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, vision")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this path has no multi-GPU sharding (asked for {args.gpus})", file=sys.stderr)
@@ -317,6 +364,8 @@ def main():
         result["attention"] = bench_attention(dev)
     if want("copy"):
         result["copy"] = bench_copy(dev)
+    if want("vision"):
+        result["vision_gemm"] = bench_vision_gemm(dev)
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)
     dev.close()

@@ -146,3 +146,9 @@ int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const 
 int launch_rms_norm(htr_device *dev, hipStream_t st, const float *x, const float *w, float *y, int rows, int dim,
                     float eps);
 int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, size_t n);
+
+// MFMA GEMM (mfma_gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ, X and W f16, f32 accumulation. GEMM_FFN: w = gate, w2 = up,
+// y16 = f16(silu(X·Wgᵀ)·(X·Wuᵀ)·scale). W rows a multiple of 128, K a multiple of 32.
+enum { GEMM_F32 = 0, GEMM_ACC = 1, GEMM_FFN = 2 };
+int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x, int m, const htr_weight *w,
+                    const htr_weight *w2, float *y, _Float16 *y16, float scale);

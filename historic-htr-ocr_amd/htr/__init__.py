@@ -27,7 +27,7 @@ SYMBOLS = [
     "htr_upload", "htr_download", "htr_copy", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
-    "htr_choose_many", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
+    "htr_choose_many", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
 ]
@@ -103,6 +103,8 @@ def lib() -> C.CDLL:
             "htr_decode_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
             "htr_choose": (i32, [vp, vp, i32, vp, i32, i32, f32, f32, vp, vp, vp]),
             "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),
+            "htr_gemm_f16": (i32, [vp, vp, sz, vp, vp, i32]),
+            "htr_gemm_ffn_f16": (i32, [vp, vp, sz, vp, vp, f32, vp]),
             "htr_text_model_create": (i32, [vp, C.POINTER(TextConfigC), vp, vp, C.POINTER(LayerTensorsC), pp]),
             "htr_text_model_free": (i32, [vp]),
             "htr_session_create": (i32, [vp, sz, pp]),
@@ -319,6 +321,16 @@ def choose(dev: Device, logits: Buffer, n_vocab: int, hist: Buffer, length: int,
 def choose_many(dev: Device, logits: Buffer, n_vocab: int, n: int, hist: Buffer, hist_stride: int, length: int,
                 window: int, rp: float, tok: Buffer) -> None:
     _check(lib().htr_choose_many(dev.h, logits.ptr, n_vocab, n, hist.ptr, hist_stride, length, window, rp, tok.ptr))
+
+
+def gemm_f16(dev: Device, x16: Buffer, m: int, w: Weight, y: Buffer, acc: bool = False) -> None:
+    """y[m][N] (+)= x16·Wᵀ on the matrix cores (x16: f16 [m][K]; w: an f16 weight)"""
+    _check(lib().htr_gemm_f16(dev.h, x16.ptr, m, w.h, y.ptr, int(acc)))
+
+
+def gemm_ffn_f16(dev: Device, x16: Buffer, m: int, w_gate: Weight, w_up: Weight, scale: float, g16: Buffer) -> None:
+    """g16[m][N] = f16(silu(x16·Wgᵀ)·(x16·Wuᵀ)·scale)"""
+    _check(lib().htr_gemm_ffn_f16(dev.h, x16.ptr, m, w_gate.h, w_up.h, scale, g16.ptr))
 
 
 # ---- the text decoder ----------------------------------------------------------------------------------------------

@@ -124,6 +124,15 @@ int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_t *d_hist, 
 int htr_choose_many(htr_device *dev, float *d_logits, int n_vocab, int n, uint32_t *d_hist, int hist_stride, int len,
                     int window, float rp, uint32_t *d_tok);
 
+/* ---- the vision encoder's GEMMs on the matrix cores (gpu.rs:2019-2042 Batch::matmul_f16x → matmul_coopd.wgsl,
+ *      gpu.rs:2048-2086 Batch::ffn_f16 → ffn_coopd.wgsl) ------------------------------------------------------- */
+/* d_y[m][N] (+= with acc) X·Wᵀ: d_x f16 [m][K] (IEEE binary16 bits), w an f16 weight (htr_weight_q8_0_f16) [N][K]
+ * with N a multiple of 128 and K a multiple of 32; f32 accumulation */
+int htr_gemm_f16(htr_device *dev, const uint16_t *d_x, size_t m, const htr_weight *w, float *d_y, int acc);
+/* d_g[m][N] = f16(silu(X·Wgᵀ) · (X·Wuᵀ) · scale): the vision FFN's first half (the reference stores it × 1/64) */
+int htr_gemm_ffn_f16(htr_device *dev, const uint16_t *d_x, size_t m, const htr_weight *w_gate, const htr_weight *w_up,
+                     float scale, uint16_t *d_g);
+
 /* ---- the text decoder (text.rs:30-130 TextConfig / TextModel, text.rs:332-375 load) ------------------------------ */
 typedef struct {
     int n_layer, dim, n_head, n_kv, d_head, n_ff, n_vocab, n_ctx_train;
