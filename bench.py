@@ -245,6 +245,31 @@ def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
     return res
 
 
+def bench_vision_encode(dev, reps=2):
+    """config 4 end to end: one 1540 x 1540 page (12100 patches) through the 24-layer encoder and the projector
+    (3025 x 1024 embeddings left on the device), random-init q8_0 weights"""
+    from htr import synth
+
+    cfg, t = synth.vision_model()
+    v = htr.Vision(dev, cfg, t)
+    rgb = synth.page(99, 1540, 1540)
+    out, n, d = v.encode_gpu(rgb)
+    dev.timer_begin()
+    for _ in range(reps):
+        v.encode_gpu(rgb, out=out)
+    ms = dev.timer_end() / reps
+    emb = out.download(np.float32, n * d)
+    out.free()
+    v.free()
+    m = 12100
+    gemm = 24 * 2.0 * m * (4 * 1024 * 1024 + 3 * 4096 * 1024)
+    attn = 24 * 16 * 2 * (2.0 * m * m * 64)
+    res = {"page": "1540x1540", "patches": m, "out_tokens": n, "encode_ms": ms, "gemm_flop": gemm,
+           "attention_flop": attn, "finite": bool(np.all(np.isfinite(emb)))}
+    log(f"vision encode 1540x1540: {ms:.1f} ms per page ({n} x {d} embeddings)")
+    return res
+
+
 def synth_normal_f16(seed, n):
     return htr.synth_normal(seed, n).astype(np.float16)
 
@@ -366,6 +391,7 @@ def main():
         result["copy"] = bench_copy(dev)
     if want("vision"):
         result["vision_gemm"] = bench_vision_gemm(dev)
+        result["vision_encode"] = bench_vision_encode(dev)
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)
     dev.close()

@@ -152,3 +152,20 @@ int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, siz
 enum { GEMM_F32 = 0, GEMM_ACC = 1, GEMM_FFN = 2 };
 int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x, int m, const htr_weight *w,
                     const htr_weight *w2, float *y, _Float16 *y16, float scale);
+
+// the vision encoder's other kernels (vision.hip)
+int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const float *lut, int w, int px, int n,
+                    int side, float *P);
+int launch_rms_norm_f16(htr_device *dev, hipStream_t st, const float *x, const float *w, _Float16 *y, int rows, int dim,
+                        float eps);
+int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, int n_tok, int n_head, int d_head, int px,
+                  int max_pos);
+int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kh, _Float16 *vh,
+                     int n_tok, int n_head, int n_pad);
+int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kh, const _Float16 *vh,
+                       _Float16 *o, int n_tok, int n_head, int n_pad, float scale);
+int launch_unfold2x2(htr_device *dev, hipStream_t st, const float *x, float *z, int px, int py, int dim);
+int launch_gelu(htr_device *dev, hipStream_t st, float *x, size_t n);
+// Y[M,N] (+)= X[M,K]·Wᵀ, f32 X, W f32 or f16 (w_f16), any K
+int launch_gemm_f32w(htr_device *dev, hipStream_t st, const float *x, const void *w, bool w_f16, float *y, int m, int n,
+                     int k, int acc);

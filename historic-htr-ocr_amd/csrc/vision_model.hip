@@ -1,0 +1,251 @@
+// The vision encoder's host side: Vision (vision.rs:87-263) — weights at load (q8_0 → f16 for the matrix-core GEMMs,
+// the down projection × 64), the patch grid checks, and the f16 compute path's graph (vision.rs:328-423 run_f16 +
+// project) on the kernels of mfma_gemm.hip / vision.hip / gemm.hip.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "htr_internal.h"
+
+namespace {
+
+constexpr float FFN_DOWN_SCALE = 64.0f;  // vision.rs:31-35: the SwiGLU product stored ÷ 64, the down weights × 64
+
+struct VLayer {
+    float *ln1 = nullptr, *ln2 = nullptr;
+    htr_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr;
+};
+
+// vision.rs:159-175: [half][pos][k] × (cos, sin), the angle multiplied up step by step in f32
+std::vector<float> rope2d_table(float theta, int d_head, int max_pos) {
+    const int n_dims = d_head / 2;
+    const float theta_scale = powf(theta, -2.0f / (float)n_dims);
+    std::vector<float> out;
+    out.reserve((size_t)2 * max_pos * (n_dims / 2) * 2);
+    for (int half = 0; half < 2; half++) {
+        const float freq_scale = half == 0 ? 1.0f : powf(theta, -2.0f / (float)d_head);
+        for (int pos = 0; pos < max_pos; pos++) {
+            float t = (float)pos;
+            for (int k = 0; k < n_dims / 2; k++) {
+                const float a = freq_scale * t;
+                out.push_back(cosf(a));
+                out.push_back(sinf(a));
+                t *= theta_scale;
+            }
+        }
+    }
+    return out;
+}
+
+}  // namespace
+
+struct htr_vision {
+    htr_device *dev = nullptr;
+    htr_vision_config cfg{};
+    float *lut = nullptr, *patch_embd = nullptr, *pre_ln = nullptr, *input_norm = nullptr;
+    std::vector<VLayer> layers;
+    htr_weight *merger = nullptr, *mm1 = nullptr, *mm2 = nullptr;
+    // the encode's buffers, sized for the largest page seen (rows n_cap)
+    int n_cap = 0, pos_cap = 0;
+    uint8_t *rgb = nullptr;
+    size_t rgb_cap = 0;
+    float *P = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *tmp = nullptr, *cs = nullptr;
+    _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kh = nullptr, *vh = nullptr;
+};
+
+namespace {
+
+int up_vec(htr_device *dev, const float *h, size_t n, const char *what, float **out) {
+    if (!h) return htr_fail("missing f32 tensor %s [%zu]", what, n);
+    HTR_TRY(htr_dev_alloc(dev, n * 4, HTR_MEM_WEIGHTS, (void **)out));
+    return htr_upload(dev, *out, h, n * 4);
+}
+
+int up_w16(htr_device *dev, const void *h, size_t rows, size_t cols, float scale, const char *what, htr_weight **out) {
+    if (!h) return htr_fail("missing q8_0 tensor %s [%zu x %zu]", what, rows, cols);
+    if (htr_weight_q8_0_f16(dev, h, rows, cols, scale, out) < 0) return htr_fail("%s: %s", what, htr_last_error());
+    return 0;
+}
+
+void free_bufs(htr_vision *v) {
+    for (void *p : {(void *)v->rgb, (void *)v->P, (void *)v->x, (void *)v->q, (void *)v->k, (void *)v->v, (void *)v->tmp,
+                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kh, (void *)v->vh})
+        if (p) htr_dev_free(v->dev, p);
+    v->rgb = nullptr;
+    v->P = v->x = v->q = v->k = v->v = v->tmp = v->cs = nullptr;
+    v->h16 = v->a16 = v->g16 = v->kh = v->vh = nullptr;
+    v->n_cap = v->pos_cap = 0;
+    v->rgb_cap = 0;
+}
+
+// buffers for n patches (and the projector: unfold n·dim, merged n/4·dim, mm.1 n/4·proj_dim fit in q / k / v)
+int ensure_bufs(htr_vision *v, int n, int max_pos, size_t rgb_bytes) {
+    const htr_vision_config &c = v->cfg;
+    htr_device *dev = v->dev;
+    if (n > v->n_cap || max_pos > v->pos_cap || rgb_bytes > v->rgb_cap) {
+        free_bufs(v);
+        const size_t d = c.dim, f = c.n_ff, pp = 3 * (size_t)c.patch * c.patch, n_pad = (size_t)(n + 31) / 32 * 32;
+        const size_t qkv = (size_t)n * std::max<size_t>(d, (size_t)c.proj_dim);
+        int rc = htr_dev_alloc(dev, rgb_bytes, HTR_MEM_WORK, (void **)&v->rgb);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * pp * 4, HTR_MEM_WORK, (void **)&v->P);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 4, HTR_MEM_WORK, (void **)&v->x);
+        if (rc == 0) rc = htr_dev_alloc(dev, qkv * 4, HTR_MEM_WORK, (void **)&v->q);
+        if (rc == 0) rc = htr_dev_alloc(dev, qkv * 4, HTR_MEM_WORK, (void **)&v->k);
+        if (rc == 0) rc = htr_dev_alloc(dev, qkv * 4, HTR_MEM_WORK, (void **)&v->v);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 4, HTR_MEM_WORK, (void **)&v->tmp);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)2 * max_pos * (c.d_head / 4) * 2 * 4, HTR_MEM_WORK, (void **)&v->cs);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->h16);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->a16);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * f * 2, HTR_MEM_WORK, (void **)&v->g16);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->kh);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->vh);
+        if (rc < 0) {
+            std::string keep = htr_last_error();
+            free_bufs(v);
+            return htr_fail("%s", keep.c_str());
+        }
+        v->n_cap = n;
+        v->pos_cap = max_pos;
+        v->rgb_cap = rgb_bytes;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int htr_vision_free(htr_vision *v) {
+    if (!v) return 0;
+    htr_device *dev = v->dev;
+    free_bufs(v);
+    for (VLayer &l : v->layers) {
+        for (htr_weight *w : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) htr_weight_free(w);
+        for (float *p : {l.ln1, l.ln2})
+            if (p) htr_dev_free(dev, p);
+    }
+    for (htr_weight *w : {v->merger, v->mm1, v->mm2}) htr_weight_free(w);
+    for (float *p : {v->lut, v->patch_embd, v->pre_ln, v->input_norm})
+        if (p) htr_dev_free(dev, p);
+    delete v;
+    return 0;
+}
+
+// Vision::from_gguf (vision.rs:177-233) from host tensors
+extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, const float *patch_embd,
+                                 const float *pre_ln, const htr_vision_layer *layers, const float *input_norm,
+                                 const void *merger, const void *mm1, const void *mm2, htr_vision **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!cfg || !layers || !out) return htr_fail("htr_vision_create: null argument");
+    const htr_vision_config &c = *cfg;
+    if (c.n_layer < 1 || c.dim < 64 || c.n_head < 1 || c.patch < 1 || c.proj_dim < 1 || c.n_ff < 1)
+        return htr_fail("vision config: %d layers, dim %d, %d heads, patch %d, projection %d, ffn %d", c.n_layer, c.dim,
+                        c.n_head, c.patch, c.proj_dim, c.n_ff);
+    if (c.d_head != 64 || c.dim != c.n_head * 64)
+        return htr_fail("head dim %d (dim %d / %d heads): the attention kernel is written for 64", c.d_head, c.dim,
+                        c.n_head);
+    if (c.merge != 2 || c.n_ff < 4 * c.dim) return htr_fail("merge %d / n_ff %d: the unfold kernel is 2×2", c.merge, c.n_ff);
+    if (c.dim % 128 || c.n_ff % 128 || c.proj_dim % 32)
+        return htr_fail("dims %d / %d: the matrix-core GEMMs take widths that are multiples of 128", c.dim, c.n_ff);
+    auto *v = new htr_vision;
+    v->dev = dev;
+    v->cfg = c;
+    v->layers.resize(c.n_layer);
+    const size_t d = c.dim, f = c.n_ff, pp = 3 * (size_t)c.patch * c.patch;
+    // vision.rs:143-146 pixel_lut
+    std::vector<float> lut(768);
+    for (int ch = 0; ch < 3; ch++)
+        for (int i = 0; i < 256; i++) lut[ch * 256 + i] = ((float)i / 255.0f - c.mean[ch]) / c.std[ch];
+    int rc = up_vec(dev, lut.data(), 768, "pixel lut", &v->lut);
+    if (rc == 0) rc = up_vec(dev, patch_embd, d * pp, "v.patch_embd.weight", &v->patch_embd);
+    if (rc == 0) rc = up_vec(dev, pre_ln, d, "v.pre_ln.weight", &v->pre_ln);
+    for (int i = 0; i < c.n_layer && rc == 0; i++) {
+        const htr_vision_layer &t = layers[i];
+        VLayer &l = v->layers[i];
+        rc = up_vec(dev, t.ln1, d, "ln1", &l.ln1);
+        if (rc == 0) rc = up_vec(dev, t.ln2, d, "ln2", &l.ln2);
+        if (rc == 0) rc = up_w16(dev, t.q, d, d, 1.0f, "attn_q", &l.q);
+        if (rc == 0) rc = up_w16(dev, t.k, d, d, 1.0f, "attn_k", &l.k);
+        if (rc == 0) rc = up_w16(dev, t.v, d, d, 1.0f, "attn_v", &l.v);
+        if (rc == 0) rc = up_w16(dev, t.o, d, d, 1.0f, "attn_out", &l.o);
+        if (rc == 0) rc = up_w16(dev, t.gate, f, d, 1.0f, "ffn_gate", &l.gate);
+        if (rc == 0) rc = up_w16(dev, t.up, f, d, 1.0f, "ffn_up", &l.up);
+        if (rc == 0) rc = up_w16(dev, t.down, d, f, FFN_DOWN_SCALE, "ffn_down", &l.down);
+        if (rc < 0) rc = htr_fail("v.blk.%d: %s", i, std::string(htr_last_error()).c_str());
+    }
+    if (rc == 0) rc = up_vec(dev, input_norm, d, "mm.input_norm.weight", &v->input_norm);
+    if (rc == 0) rc = up_w16(dev, merger, d, 4 * d, 1.0f, "mm.patch_merger.weight", &v->merger);
+    if (rc == 0) rc = up_w16(dev, mm1, c.proj_dim, d, 1.0f, "mm.1.weight", &v->mm1);
+    if (rc == 0) rc = up_w16(dev, mm2, c.proj_dim, c.proj_dim, 1.0f, "mm.2.weight", &v->mm2);
+    if (rc < 0) {
+        std::string keep = htr_last_error();
+        htr_vision_free(v);
+        return htr_fail("%s", keep.c_str());
+    }
+    *out = v;
+    return 0;
+}
+
+// vision.rs:236-244 grid + the output shape of an encode
+extern "C" int htr_vision_out_shape(htr_vision *v, int width, int height, int n_layers, size_t *n_tokens, size_t *dim) {
+    if (!v) return htr_fail("htr_vision_out_shape: null vision");
+    const htr_vision_config &c = v->cfg;
+    const int grid = c.patch * c.merge;
+    if (width <= 0 || height <= 0 || width % grid || height % grid || std::max(width, height) > c.image_size)
+        return htr_fail("image %dx%d is not baked (both sides on the %d px grid, longest ≤ %d)", width, height, grid,
+                        c.image_size);
+    if (n_layers > c.n_layer) return htr_fail("%d layers asked, the encoder has %d", n_layers, c.n_layer);
+    const size_t n = (size_t)(width / c.patch) * (height / c.patch);
+    if (n_tokens) *n_tokens = n_layers < 0 ? n / 4 : n;
+    if (dim) *dim = n_layers < 0 ? (size_t)c.proj_dim : (size_t)c.dim;
+    return 0;
+}
+
+// Vision::encode_gpu / encode (vision.rs:248-263, 328-423)
+extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width, int height, int n_layers,
+                                 float *d_out) {
+    if (!v || !h_rgb || !d_out) return htr_fail("htr_vision_encode: null argument");
+    htr_device *dev = v->dev;
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_vision_out_shape(v, width, height, n_layers, nullptr, nullptr));
+    const htr_vision_config &c = v->cfg;
+    const int px = width / c.patch, py = height / c.patch, n = px * py, d = c.dim, pp = 3 * c.patch * c.patch;
+    const int n_pad = (n + 31) / 32 * 32, max_pos = std::max(px, py);
+    const size_t rgb_bytes = (size_t)width * height * 3;
+    HTR_TRY(ensure_bufs(v, n, max_pos, rgb_bytes));
+    hipStream_t st = dev->stream;
+    HTR_TRY(htr_upload(dev, v->rgb, h_rgb, rgb_bytes));
+    const std::vector<float> cs = rope2d_table(c.rope_theta, c.d_head, max_pos);
+    HTR_TRY(htr_upload(dev, v->cs, cs.data(), cs.size() * 4));
+    const float scale = 1.0f / sqrtf((float)c.d_head);
+    const int nl = n_layers < 0 ? c.n_layer : n_layers;
+    HTR_TRY(launch_patchify(dev, st, v->rgb, v->lut, width, px, n, c.patch, v->P));
+    HTR_TRY(launch_gemm_f32w(dev, st, v->P, v->patch_embd, false, v->tmp, n, d, pp, 0));
+    HTR_TRY(launch_rms_norm(dev, st, v->tmp, v->pre_ln, v->x, n, d, c.eps));
+    for (int li = 0; li < nl; li++) {
+        const VLayer &l = v->layers[li];
+        HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln1, v->h16, n, d, c.eps));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.q, nullptr, v->q, nullptr, 1.0f));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.k, nullptr, v->k, nullptr, 1.0f));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
+        HTR_TRY(launch_rope2d(dev, st, v->q, v->cs, n, c.n_head, c.d_head, px, max_pos));
+        HTR_TRY(launch_rope2d(dev, st, v->k, v->cs, n, c.n_head, c.d_head, px, max_pos));
+        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kh, v->vh, n, c.n_head, n_pad));
+        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kh, v->vh, v->a16, n, c.n_head, n_pad, scale));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_ACC, v->a16, n, l.o, nullptr, v->x, nullptr, 1.0f));
+        HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln2, v->h16, n, d, c.eps));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_FFN, v->h16, n, l.gate, l.up, nullptr, v->g16, 1.0f / FFN_DOWN_SCALE));
+        HTR_TRY(launch_gemm_f16(dev, st, GEMM_ACC, v->g16, n, l.down, nullptr, v->x, nullptr, 1.0f));
+    }
+    if (n_layers >= 0) {
+        HTR_TRY(htr_hip(dev, hipMemcpyAsync(d_out, v->x, (size_t)n * d * 4, hipMemcpyDeviceToDevice, st), "copy"));
+        return htr_sync(dev);
+    }
+    // project (vision.rs:405-423): input_norm → unfold 2×2 → merger → mm.1 → gelu → mm.2
+    const int n_out = n / 4;
+    HTR_TRY(launch_rms_norm(dev, st, v->x, v->input_norm, v->tmp, n, d, c.eps));
+    HTR_TRY(launch_unfold2x2(dev, st, v->tmp, v->q, px, py, d));
+    HTR_TRY(launch_gemm_f32w(dev, st, v->q, v->merger->h, true, v->k, n_out, d, 4 * d, 0));
+    HTR_TRY(launch_gemm_f32w(dev, st, v->k, v->mm1->h, true, v->v, n_out, c.proj_dim, d, 0));
+    HTR_TRY(launch_gelu(dev, st, v->v, (size_t)n_out * c.proj_dim));
+    HTR_TRY(launch_gemm_f32w(dev, st, v->v, v->mm2->h, true, d_out, n_out, c.proj_dim, c.proj_dim, 0));
+    return htr_sync(dev);
+}

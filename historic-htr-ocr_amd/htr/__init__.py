@@ -27,7 +27,8 @@ SYMBOLS = [
     "htr_upload", "htr_download", "htr_copy", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
-    "htr_choose_many", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
+    "htr_choose_many", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
+    "htr_vision_out_shape", "htr_vision_encode", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
 ]
@@ -56,6 +57,16 @@ class PresetC(C.Structure):
     _fields_ = [("temperature", C.c_double), ("top_p", C.c_double), ("repetition_penalty", C.c_double),
                 ("frequency_penalty", C.c_double), ("repetition_window", C.c_size_t),
                 ("max_new_tokens", C.c_size_t)]
+
+
+class VisionConfigC(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("dim", C.c_int), ("n_head", C.c_int), ("d_head", C.c_int), ("n_ff", C.c_int),
+                ("patch", C.c_int), ("merge", C.c_int), ("image_size", C.c_int), ("proj_dim", C.c_int),
+                ("eps", C.c_float), ("rope_theta", C.c_float), ("mean", C.c_float * 3), ("std", C.c_float * 3)]
+
+
+class VisionLayerC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")]
 
 
 FATAL_HOOK = C.CFUNCTYPE(None, C.c_char_p, C.c_char_p, C.c_void_p)
@@ -105,6 +116,11 @@ def lib() -> C.CDLL:
             "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),
             "htr_gemm_f16": (i32, [vp, vp, sz, vp, vp, i32]),
             "htr_gemm_ffn_f16": (i32, [vp, vp, sz, vp, vp, f32, vp]),
+            "htr_vision_create": (i32, [vp, C.POINTER(VisionConfigC), vp, vp, C.POINTER(VisionLayerC), vp, vp, vp, vp,
+                                        pp]),
+            "htr_vision_free": (i32, [vp]),
+            "htr_vision_out_shape": (i32, [vp, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)]),
+            "htr_vision_encode": (i32, [vp, vp, i32, i32, i32, vp]),
             "htr_text_model_create": (i32, [vp, C.POINTER(TextConfigC), vp, vp, C.POINTER(LayerTensorsC), pp]),
             "htr_text_model_free": (i32, [vp]),
             "htr_session_create": (i32, [vp, sz, pp]),
@@ -473,3 +489,63 @@ class Choice:
         if self.h:
             lib().htr_choice_free(self.h)
             self.h = None
+
+
+# ---- the vision encoder --------------------------------------------------------------------------------------------
+
+class Vision:
+    """Vision::from_gguf (vision.rs:177-233) from host tensors. ``cfg``: n_layer, dim, n_head, n_ff, patch,
+    image_size, proj_dim, eps, rope_theta, mean, std; ``t``: patch_embd (f32), pre_ln, input_norm (f32), merger, mm1,
+    mm2 (q8_0 blocks) and ``layers`` (dicts with ln1, ln2 f32 and q, k, v, o, gate, up, down q8_0 blocks)."""
+
+    def __init__(self, dev: Device, cfg: dict, t: dict):
+        self.dev, self.cfg = dev, cfg
+        keep = []
+
+        def f32(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            keep.append(a)
+            return _ptr(a)
+
+        def u8(a):
+            a = np.ascontiguousarray(a, dtype=np.uint8)
+            keep.append(a)
+            return _ptr(a)
+
+        arr = (VisionLayerC * cfg["n_layer"])()
+        for i, ly in enumerate(t["layers"]):
+            arr[i] = VisionLayerC(ln1=f32(ly["ln1"]), ln2=f32(ly["ln2"]),
+                                  **{k: u8(ly[k]) for k in ("q", "k", "v", "o", "gate", "up", "down")})
+        c = VisionConfigC(cfg["n_layer"], cfg["dim"], cfg["n_head"], 64, cfg["n_ff"], cfg["patch"], 2,
+                          cfg.get("image_size", 1540), cfg["proj_dim"], cfg["eps"], cfg["rope_theta"],
+                          (C.c_float * 3)(*cfg["mean"]), (C.c_float * 3)(*cfg["std"]))
+        h = C.c_void_p()
+        _check(lib().htr_vision_create(dev.h, C.byref(c), f32(t["patch_embd"]), f32(t["pre_ln"]), arr,
+                                       f32(t["input_norm"]), u8(t["merger"]), u8(t["mm1"]), u8(t["mm2"]), C.byref(h)))
+        self.h = h.value
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_vision_free(self.h)
+            self.h = None
+
+    def out_shape(self, width: int, height: int, n_layers: int = -1) -> tuple[int, int]:
+        n, d = C.c_size_t(), C.c_size_t()
+        _check(lib().htr_vision_out_shape(self.h, width, height, n_layers, C.byref(n), C.byref(d)))
+        return n.value, d.value
+
+    def encode_gpu(self, rgb: np.ndarray, n_layers: int = -1, out: Buffer | None = None) -> tuple[Buffer, int, int]:
+        """Vision::encode_gpu: the result left on the device → (buffer, rows, width)"""
+        rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+        h, w, _ = rgb.shape
+        n, d = self.out_shape(w, h, n_layers)
+        out = out or self.dev.alloc(n * d * 4)
+        _check(lib().htr_vision_encode(self.h, _ptr(rgb), w, h, n_layers, out.ptr))
+        return out, n, d
+
+    def encode(self, rgb: np.ndarray, n_layers: int = -1) -> np.ndarray:
+        """Vision::encode: the embeddings [n/4][proj_dim] (or the residual [n][dim] after n_layers layers)"""
+        buf, n, d = self.encode_gpu(rgb, n_layers)
+        out = buf.download(np.float32, n * d).reshape(n, d)
+        buf.free()
+        return out

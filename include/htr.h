@@ -133,6 +133,33 @@ int htr_gemm_f16(htr_device *dev, const uint16_t *d_x, size_t m, const htr_weigh
 int htr_gemm_ffn_f16(htr_device *dev, const uint16_t *d_x, size_t m, const htr_weight *w_gate, const htr_weight *w_up,
                      float scale, uint16_t *d_g);
 
+/* ---- the vision encoder (vision.rs:37-263 VisionConfig / Vision, the f16 compute path run_f16 + project) -------- */
+typedef struct htr_vision htr_vision;
+/* VisionConfig (vision.rs:37-84): head dim 64, 2×2 merge, rope θ (10000 for LightOnOCR), the pixel mean / std */
+typedef struct {
+    int n_layer, dim, n_head, d_head, n_ff, patch, merge, image_size, proj_dim;
+    float eps, rope_theta;
+    float mean[3], std[3];
+} htr_vision_config;
+/* one encoder layer's tensors as host bytes: q8_0 GGUF blocks for the projections, f32 for the norms */
+typedef struct {
+    const float *ln1, *ln2;
+    const void *q, *k, *v, *o, *gate, *up, *down;
+} htr_vision_layer;
+/* Vision::from_gguf (vision.rs:177-233): the projections and the projector converted to f16 at load (the down
+ * projection × 64, vision.rs:31-35); patch_embd f32 [dim][3·patch²], norms f32 [dim], merger [dim][4·dim],
+ * mm1 [proj_dim][dim], mm2 [proj_dim][proj_dim] as q8_0 blocks */
+int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, const float *patch_embd, const float *pre_ln,
+                      const htr_vision_layer *layers, const float *input_norm, const void *merger, const void *mm1,
+                      const void *mm2, htr_vision **out);
+int htr_vision_free(htr_vision *v);
+/* the output of an encode of a width × height page (Vision::grid, vision.rs:236-244: both sides on the patch·merge
+ * grid, the longer ≤ image_size): n_layers < 0 → [n/4][proj_dim] embeddings; n_layers ≥ 0 → the residual after that
+ * many layers [n][dim] (the reference's `layers` bisect hook, vision.rs:246-256) */
+int htr_vision_out_shape(htr_vision *v, int width, int height, int n_layers, size_t *n_tokens, size_t *dim);
+/* Vision::encode_gpu (vision.rs:258-263): RGB bytes [height][width][3] → d_out (device memory of the shape above) */
+int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width, int height, int n_layers, float *d_out);
+
 /* ---- the text decoder (text.rs:30-130 TextConfig / TextModel, text.rs:332-375 load) ------------------------------ */
 typedef struct {
     int n_layer, dim, n_head, n_kv, d_head, n_ff, n_vocab, n_ctx_train;

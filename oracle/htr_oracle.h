@@ -20,6 +20,10 @@
  *                                     a brute-force numpy argmax
  *   or_session_prefill / or_session_step
  *                                     an independent numpy float64 forward of the same graph (tiny model shape)
+ *   or_pixel_lut / or_patchify, or_rope2d_table / or_rope2d, or_unfold2x2, or_gelu, or_rms_norm_h, or_matmul_f16,
+ *   or_ffn_f16, or_attention_coop, or_vision_encode
+ *                                     numpy restatements (fp64 closed forms, ggml's rope cache by its own recurrence,
+ *                                     torch-unfold index order by brute force), tests/test_vision_oracle.py
  */
 #ifndef HTR_ORACLE_H
 #define HTR_ORACLE_H
@@ -122,6 +126,34 @@ int or_session_prefill(or_session *s, const int32_t *ids, int n, float *logits);
 int or_session_step(or_session *s, int32_t tok, float *logits);
 /* rewind to n_past positions (the rows beyond are overwritten by later steps) */
 void or_session_rewind(or_session *s, int n_past);
+
+/* ---- the vision encoder (vision.rs:266-423, the f16 compute path; htr_vision_oracle.c) ------------------------- */
+void or_pixel_lut(const float mean[3], const float stdv[3], float *lut);
+void or_patchify(const uint8_t *rgb, int w, int px, int n, int side, const float *lut, float *P);
+void or_rope2d_table(float theta, int d_head, int max_pos, float *out);
+void or_rope2d(float *Q, int n_tok, int n_head, int d_head, int px, int max_pos, const float *cs);
+void or_rms_norm_h(const float *x, const float *w, uint16_t *y, size_t rows, size_t dim, float eps);
+void or_q8_0_to_f16(const uint8_t *blocks, size_t n, float scale, uint16_t *out);
+void or_matmul_f16(const uint16_t *x, const uint16_t *w, float *y, size_t m, size_t n, size_t k, int acc);
+void or_ffn_f16(const uint16_t *x, const uint16_t *wg, const uint16_t *wu, uint16_t *g, size_t m, size_t n, size_t k,
+                float scale);
+void or_matmul_f32(const float *x, const float *w, float *y, size_t m, size_t n, size_t k, int acc);
+void or_attention_coop(const float *q, const float *k, const float *v, uint16_t *o, int n_tok, int n_head,
+                       float scale);
+void or_unfold2x2(const float *x, float *z, int px, int py, int dim);
+void or_gelu(float *x, size_t n);
+
+typedef struct {
+    int n_layer, dim, n_head, d_head, n_ff, patch, merge, proj_dim;
+    float eps, rope_theta, mean[3], std[3];
+} or_vision_cfg;
+typedef struct {
+    const float *ln1, *ln2;
+    const uint8_t *q, *k, *v, *o, *gate, *up, *down; /* q8_0 GGUF blocks */
+} or_vision_layer;
+int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
+                     const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
+                     const uint8_t *rgb, int w, int h, int n_layers, float *out);
 
 #ifdef __cplusplus
 }

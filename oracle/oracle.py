@@ -49,6 +49,19 @@ def lib() -> C.CDLL:
             "or_session_prefill": (i32, [vp, vp, i32, vp]),
             "or_session_step": (i32, [vp, C.c_int32, vp]),
             "or_session_rewind": (None, [vp, i32]),
+            "or_pixel_lut": (None, [vp, vp, vp]),
+            "or_patchify": (None, [vp, i32, i32, i32, i32, vp, vp]),
+            "or_rope2d_table": (None, [f32, i32, i32, vp]),
+            "or_rope2d": (None, [vp, i32, i32, i32, i32, i32, vp]),
+            "or_rms_norm_h": (None, [vp, vp, vp, sz, sz, f32]),
+            "or_q8_0_to_f16": (None, [vp, sz, f32, vp]),
+            "or_matmul_f16": (None, [vp, vp, vp, sz, sz, sz, i32]),
+            "or_ffn_f16": (None, [vp, vp, vp, vp, sz, sz, sz, f32]),
+            "or_matmul_f32": (None, [vp, vp, vp, sz, sz, sz, i32]),
+            "or_attention_coop": (None, [vp, vp, vp, vp, i32, i32, f32]),
+            "or_unfold2x2": (None, [vp, vp, i32, i32, i32]),
+            "or_gelu": (None, [vp, sz]),
+            "or_vision_encode": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -165,29 +178,29 @@ def qkv_post(qkv, qn, kn, cs, n_head, n_kv, pos, eps):
     qkv = np.array(qkv, dtype=np.float32)
     kr = np.zeros(n_kv * 128, np.uint16)
     vr = np.zeros(n_kv * 128, np.uint16)
-    lib().or_qkv_post(_p(qkv), _p(np.ascontiguousarray(qn, np.float32)), _p(np.ascontiguousarray(kn, np.float32)),
-                      _p(np.ascontiguousarray(cs, np.float32)), n_head, n_kv, pos, eps, _p(kr), _p(vr))
+    qn, kn, cs = (np.ascontiguousarray(a, np.float32) for a in (qn, kn, cs))
+    lib().or_qkv_post(_p(qkv), _p(qn), _p(kn), _p(cs), n_head, n_kv, pos, eps, _p(kr), _p(vr))
     return qkv, kr, vr
 
 
 def attn_decode(q, k, v, kv_stride, n_keys, n_head, n_kv, scale) -> np.ndarray:
     out = np.empty(n_head * 128, np.float32)
-    lib().or_attn_decode(_p(np.ascontiguousarray(q, np.float32)), _p(k), _p(v), kv_stride, n_keys, n_head, n_kv,
-                         scale, _p(out))
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_attn_decode(_p(q), _p(k), _p(v), kv_stride, n_keys, n_head, n_kv, scale, _p(out))
     return out
 
 
 def attn_causal(q, k, v, kv_stride, n_q, pos0, n_head, n_kv, scale) -> np.ndarray:
     out = np.empty(n_q * n_head * 128, np.float32)
-    lib().or_attn_causal(_p(np.ascontiguousarray(q, np.float32)), _p(k), _p(v), kv_stride, n_q, pos0, n_head, n_kv,
-                         scale, _p(out))
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_attn_causal(_p(q), _p(k), _p(v), kv_stride, n_q, pos0, n_head, n_kv, scale, _p(out))
     return out
 
 
 def attn_f64(q, k, v, kv_stride, n_keys, n_head, n_kv, scale) -> np.ndarray:
     out = np.empty(n_head * 128, np.float64)
-    lib().or_attn_f64(_p(np.ascontiguousarray(q, np.float32)), _p(k), _p(v), kv_stride, n_keys, n_head, n_kv, scale,
-                      _p(out))
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_attn_f64(_p(q), _p(k), _p(v), kv_stride, n_keys, n_head, n_kv, scale, _p(out))
     return out
 
 
@@ -254,3 +267,133 @@ class Session:
         if lib().or_session_step(self.h, int(tok), _p(out)) != 0:
             raise ValueError("oracle step: bad id or overflow")
         return out
+
+
+# ---- the vision encoder (htr_vision_oracle.c) ----------------------------------------------------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def pixel_lut(mean, std) -> np.ndarray:
+    out = np.empty(768, np.float32)
+    mean, std = _f32(mean), _f32(std)
+    lib().or_pixel_lut(_p(mean), _p(std), _p(out))
+    return out
+
+
+def patchify(rgb: np.ndarray, side: int, lut: np.ndarray) -> np.ndarray:
+    """rgb u8 [h][w][3] → P [n][3·side²]"""
+    h, w, _ = rgb.shape
+    px, py = w // side, h // side
+    out = np.empty((px * py, 3 * side * side), np.float32)
+    rgb, lut = np.ascontiguousarray(rgb, np.uint8), _f32(lut)
+    lib().or_patchify(_p(rgb), w, px, px * py, side, _p(lut), _p(out))
+    return out
+
+
+def rope2d_table(theta: float, d_head: int, max_pos: int) -> np.ndarray:
+    """[2][max_pos][d/4][2] (cos, sin)"""
+    out = np.empty((2, max_pos, d_head // 4, 2), np.float32)
+    lib().or_rope2d_table(theta, d_head, max_pos, _p(out))
+    return out
+
+
+def rope2d(q: np.ndarray, n_head: int, d_head: int, px: int, max_pos: int, cs: np.ndarray) -> np.ndarray:
+    q = np.array(q, dtype=np.float32)
+    cs = _f32(cs)
+    lib().or_rope2d(_p(q), q.shape[0], n_head, d_head, px, max_pos, _p(cs))
+    return q
+
+
+def rms_norm_h(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    out = np.empty(x.shape, np.float16)
+    lib().or_rms_norm_h(_p(x), _p(w), _p(out), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def q8_0_to_f16(blocks: np.ndarray, rows: int, cols: int, scale: float = 1.0) -> np.ndarray:
+    out = np.empty((rows, cols), np.float16)
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    lib().or_q8_0_to_f16(_p(blocks), rows * cols, scale, _p(out))
+    return out
+
+
+def matmul_f16(x16: np.ndarray, w16: np.ndarray, y=None) -> np.ndarray:
+    x16 = np.ascontiguousarray(x16, np.float16)
+    w16 = np.ascontiguousarray(w16, np.float16)
+    m, k = x16.shape
+    n = w16.shape[0]
+    acc = y is not None
+    y = np.zeros((m, n), np.float32) if y is None else np.array(y, dtype=np.float32)
+    lib().or_matmul_f16(_p(x16), _p(w16), _p(y), m, n, k, int(acc))
+    return y
+
+
+def ffn_f16(x16, wg16, wu16, scale: float) -> np.ndarray:
+    x16 = np.ascontiguousarray(x16, np.float16)
+    m, k = x16.shape
+    n = wg16.shape[0]
+    out = np.empty((m, n), np.float16)
+    wg16, wu16 = np.ascontiguousarray(wg16, np.float16), np.ascontiguousarray(wu16, np.float16)
+    lib().or_ffn_f16(_p(x16), _p(wg16), _p(wu16), _p(out), m, n, k, scale)
+    return out
+
+
+def matmul_f32(x, w, y=None) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    acc = y is not None
+    y = np.zeros((x.shape[0], w.shape[0]), np.float32) if y is None else np.array(y, dtype=np.float32)
+    lib().or_matmul_f32(_p(x), _p(w), _p(y), x.shape[0], w.shape[0], x.shape[1], int(acc))
+    return y
+
+
+def attention_coop(q, k, v, n_head: int, scale: float) -> np.ndarray:
+    """q / k / v f32 [n][n_head·64] → f16 [n][n_head·64]"""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.empty(q.shape, np.float16)
+    lib().or_attention_coop(_p(q), _p(k), _p(v), _p(out), q.shape[0], n_head, scale)
+    return out
+
+
+def unfold2x2(x: np.ndarray, px: int, py: int) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(((px // 2) * (py // 2), 4 * x.shape[1]), np.float32)
+    lib().or_unfold2x2(_p(x), _p(out), px, py, x.shape[1])
+    return out
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = np.array(x, dtype=np.float32)
+    lib().or_gelu(_p(x), x.size)
+    return x
+
+
+class VisionCfg(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("dim", C.c_int), ("n_head", C.c_int), ("d_head", C.c_int), ("n_ff", C.c_int),
+                ("patch", C.c_int), ("merge", C.c_int), ("proj_dim", C.c_int), ("eps", C.c_float),
+                ("rope_theta", C.c_float), ("mean", C.c_float * 3), ("std", C.c_float * 3)]
+
+
+class VisionLayerC(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")]
+
+
+def vision_encode(cfg: dict, t: dict, rgb: np.ndarray, n_layers: int = -1) -> np.ndarray:
+    """vision.rs run_f16 + project on the host tensors `t` (q8_0 blocks / f32): n_layers < 0 → the projected
+    embeddings [n/4][proj_dim]; else the residual after n_layers layers [n][dim]"""
+    c = VisionCfg(cfg["n_layer"], cfg["dim"], cfg["n_head"], 64, cfg["n_ff"], cfg["patch"], 2, cfg["proj_dim"],
+                  cfg["eps"], cfg["rope_theta"], (C.c_float * 3)(*cfg["mean"]), (C.c_float * 3)(*cfg["std"]))
+    arr = (VisionLayerC * cfg["n_layer"])()
+    for i, ly in enumerate(t["layers"]):
+        arr[i] = VisionLayerC(**{k: _p(ly[k]) for k in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")})
+    h, w, _ = rgb.shape
+    n = (h // cfg["patch"]) * (w // cfg["patch"])
+    out = np.empty((n, cfg["dim"]) if n_layers >= 0 else (n // 4, cfg["proj_dim"]), np.float32)
+    rgb = np.ascontiguousarray(rgb, np.uint8)
+    rc = lib().or_vision_encode(C.byref(c), _p(t["patch_embd"]), _p(t["pre_ln"]), arr, _p(t["input_norm"]),
+                                _p(t["merger"]), _p(t["mm1"]), _p(t["mm2"]), _p(rgb), w, h, n_layers, _p(out))
+    if rc != 0:
+        raise ValueError("oracle vision_encode: unsupported size")
+    return out

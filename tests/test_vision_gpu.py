@@ -1,0 +1,69 @@
+"""The vision encoder on the GPU (vision.rs:328-423, the f16 compute path) against the vision oracle.
+
+Bars: rel-L2 ≤ 2e-3 against the oracle for every output (the stated bar for the vision path; the reference's own
+kernel bars, text.rs:1123-1293, are 1e-3 … 5e-3 against fp64). Tiny encoders at two page sizes (24 and 80 patches:
+one and three key blocks, ragged GEMM tiles), every depth (after the patch embedding, after one layer, the whole
+encoder with the projector); config 4's page (1540 × 1540, 12100 patches) through its first layer."""
+import numpy as np
+import pytest
+
+import htr
+import oracle as orc
+from helpers import rel_l2
+from test_vision_oracle import tiny_page, tiny_vision_cfg, tiny_vision_tensors
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(dev):
+    cfg = dict(tiny_vision_cfg(), image_size=1540)
+    t = tiny_vision_tensors(cfg)
+    v = htr.Vision(dev, cfg, t)
+    yield cfg, t, v
+    v.free()
+
+
+@pytest.mark.parametrize("w,h", [(56, 84), (112, 140)])
+def test_tiny_encoder_matches_oracle(tiny, w, h):
+    cfg, t, v = tiny
+    rgb = tiny_page(cfg, w, h, seed=w + h)
+    for nl in (0, 1, -1):
+        got = v.encode(rgb, nl)
+        want = orc.vision_encode(cfg, t, rgb, nl)
+        assert got.shape == want.shape, nl
+        e = rel_l2(got, want)
+        print(f"\n[vision {w}x{h} layers {nl}] rel-L2 vs oracle {e:.2e}")
+        assert e < 2e-3, nl
+
+
+def test_encoder_rejects_unbaked_pages(tiny):
+    cfg, t, v = tiny
+    with pytest.raises(htr.HtrError, match="not baked"):
+        v.encode(tiny_page(cfg, 56, 70))
+    with pytest.raises(htr.HtrError, match="not baked"):
+        v.encode(tiny_page(cfg, 1568, 28))
+    with pytest.raises(htr.HtrError, match="layers asked"):
+        v.encode(tiny_page(cfg, 56, 56), 3)
+
+
+def test_config4_first_layer_matches_oracle(dev):
+    """config 4's page and encoder shape: 12100 patches, hidden 1024, 16 heads, SwiGLU 4096 — the residual after the
+    patch embedding and after the first layer; then the whole 24-layer encode with the projector (3025 × 1024, finite)"""
+    from htr import synth
+
+    cfg, t = synth.vision_model()
+    rgb = synth.page(99, 1540, 1540)
+    v = htr.Vision(dev, cfg, t)
+    one = dict(cfg, n_layer=1)
+    t1 = dict(t, layers=t["layers"][:1])
+    for nl in (0, 1):
+        got = v.encode(rgb, nl)
+        want = orc.vision_encode(one, t1, rgb, nl)
+        e = rel_l2(got, want)
+        print(f"\n[vision 1540x1540 layers {nl}] rel-L2 vs oracle {e:.2e}")
+        assert e < 2e-3, nl
+    out = v.encode(rgb)
+    assert out.shape == (3025, 1024)
+    assert np.all(np.isfinite(out))
+    v.free()
