@@ -5,6 +5,7 @@
 // with q·scale, K, V and P rounded to f16, f32 sums, the output rounded to f16), unfold2x2.wgsl, gelu.wgsl, and the
 // f32 matmul of the patch embedding (K = 588) and the projector (f32 activations, f16-valued weights).
 #include <cmath>
+#include <type_traits>
 
 #include "htr_internal.h"
 #include "wave.h"
@@ -62,80 +63,186 @@ __global__ __launch_bounds__(VW) void k_rope2d(float *Q, const float *cs, int n_
     }
 }
 
-// heads_f16.wgsl: K, V f32 [n][H·64] → f16 [H][n_pad][64] (rows n … n_pad − 1 zero)
-__global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V, _Float16 *Kh, _Float16 *Vh, int n_tok,
-                                                  int n_head, int n_pad) {
-    const size_t total = (size_t)n_head * n_pad * 64;
-    for (size_t i = gid(); i < total; i += gsize()) {
-        const int d = (int)(i % 64), t = (int)((i / 64) % n_pad), h = (int)(i / (64 * (size_t)n_pad));
-        float kv = 0.0f, vv = 0.0f;
-        if (t < n_tok) {
-            const size_t src = (size_t)t * n_head * 64 + h * 64 + d;
-            kv = K[src];
-            vv = V[src];
-        }
-        Kh[i] = (_Float16)kv;
-        Vh[i] = (_Float16)vv;
-    }
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Key order of the transposed values inside a block of 32 keys: stored slot 16s + 8h + j (s, h < 2, j < 8) holds key
+// 16s + 8(j / 4) + 4h + j % 4. These are the keys whose scores lane half h holds in registers 8s … 8s + 7 after the
+// 32x32 score MFMAs below, so P·V step s takes its P operand straight from those registers.
+__device__ __forceinline__ int vt_key(int slot) {
+    const int st = slot >> 4, hf = (slot >> 3) & 1, j = slot & 7;
+    return 16 * st + 8 * (j >> 2) + 4 * hf + (j & 3);
 }
 
-// attention_coop.wgsl's arithmetic: O[t][h] = softmax(q16·K16ᵀ)·V16 with q16 = f16(q·scale), keys in blocks of 32
-// with the running max (start −3e38), P = f16(e^(S − max)), l = l·corr + Σ P, O = O·corr + Σ P·v; O / l → f16.
-// grid (⌈n/64⌉, H), 256 threads = 64 queries × 4 lanes (16 dims each, adjacent lanes); the key block staged in LDS.
-constexpr int AQ = 64, AB = 32;
-__global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *Kh, const _Float16 *Vh,
-                                                    _Float16 *O, int n_tok, int n_head, int n_pad, float scale) {
-    __shared__ __attribute__((aligned(16))) _Float16 s_k[AB * 64];
-    __shared__ __attribute__((aligned(16))) _Float16 s_v[AB * 64];
-    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
-    const int ql = tid >> 2, part = tid & 3;  // query within the tile, 16-dim part
-    const int qi = min(blockIdx.x * AQ + ql, n_tok - 1);
-    const int row = n_head * 64;
-    float q[16], acc[16];
-#pragma unroll
-    for (int d = 0; d < 16; d++) {
-        q[d] = (float)(_Float16)(Q[(size_t)qi * row + h * 64 + 16 * part + d] * scale);
-        acc[d] = 0.0f;
+// heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16, keys n … n_pad − 1 zero. K as [H][n_pad][64]; V transposed
+// per head as [H][64][n_pad] with the keys of each block of 32 in vt_key order. grid (n_pad / 32, H), one block of
+// 32 keys of one head per workgroup; V goes through LDS for the transposition.
+__global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V, _Float16 *Kh, _Float16 *Vt, int n_tok,
+                                                  int n_head, int n_pad) {
+    __shared__ _Float16 s_v[32][64 + 2];
+    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int r = tid >> 3, d0 = (tid & 7) * 8, t = 32 * b + r;
+    float kv[8] = {}, vv[8] = {};
+    if (t < n_tok) {
+        const float4 *ks = reinterpret_cast<const float4 *>(K + (size_t)t * n_head * 64 + h * 64 + d0);
+        const float4 *vs = reinterpret_cast<const float4 *>(V + (size_t)t * n_head * 64 + h * 64 + d0);
+        const float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
+        kv[0] = k0.x, kv[1] = k0.y, kv[2] = k0.z, kv[3] = k0.w, kv[4] = k1.x, kv[5] = k1.y, kv[6] = k1.z, kv[7] = k1.w;
+        vv[0] = v0.x, vv[1] = v0.y, vv[2] = v0.z, vv[3] = v0.w, vv[4] = v1.x, vv[5] = v1.y, vv[6] = v1.z, vv[7] = v1.w;
     }
+    half8 kh;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        kh[j] = (_Float16)kv[j];
+        s_v[r][d0 + j] = (_Float16)vv[j];
+    }
+    *reinterpret_cast<half8 *>(Kh + ((size_t)h * n_pad + t) * 64 + d0) = kh;
+    __syncthreads();
+    const int d = tid >> 2, chunk = tid & 3;
+    half8 vt;
+#pragma unroll
+    for (int j = 0; j < 8; j++) vt[j] = s_v[vt_key(8 * chunk + j)][d];
+    *reinterpret_cast<half8 *>(Vt + ((size_t)h * 64 + d) * n_pad + 32 * b + 8 * chunk) = vt;
+}
+
+// attention_coop.wgsl's arithmetic on the f16 MFMAs: O[t][h] = softmax(q16·K16ᵀ)·V16 with q16 = f16(q·scale), keys in
+// blocks of 32 with the running max (start −3e38), P = f16(e^(S − max)), l = l·corr + Σ P, O = O·corr + P·V (f32
+// accumulation in the matrix unit, as the reference's cooperative matrices accumulate); O / l → f16.
+// A wave takes 32 queries of one head. Per key block, Sᵀ (32 keys × 32 queries) = K·q16ᵀ is 4 MFMAs 32x32x16: lane
+// ℓ = 32h + c then holds query c's scores of keys 8(i / 4) + 4h + i % 4 (i < 16), the other 16 in lane ℓ ^ 32. Oᵀ
+// (64 dims × 32 queries) += Vᵀ·Pᵀ is 4 more, lane ℓ accumulating dims 32t + 8(i / 4) + 4h + i % 4 of query c, so the
+// rescale by the query's corr stays in the lane. K and Vᵀ fragments (8 KB a block) are read straight from memory
+// (the head's keys stay in L2), the next block's while the current one is in use.
+// grid: ⌈n / 128⌉ · H workgroups of 4 waves, numbered so that the workgroups of one head run on one XCD.
+constexpr int FQ = 32, FB = 32, FWAVES = VW / 64;
+
+__global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *Kh, const _Float16 *Vt, _Float16 *O,
+                                                    int n_tok, int n_head, int n_pad, int n_qt, float scale) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
+    // workgroup b runs on XCD b % 8: with H a multiple of 8, XCD x takes heads x·H/8 … (x + 1)·H/8 − 1
+    int h, qt;
+    if (n_head % 8 == 0) {
+        const int i = blockIdx.x / 8;
+        h = (blockIdx.x % 8) * (n_head / 8) + i / n_qt;
+        qt = i % n_qt;
+    } else {
+        h = blockIdx.x / n_qt;
+        qt = blockIdx.x % n_qt;
+    }
+    const int row = n_head * 64, q0 = (qt * FWAVES + wave) * FQ;
+    const int qi = min(q0 + c, n_tok - 1);
+    half8 qf[4];  // B operand of step ks: q16[query c][dims 16ks + 8h … + 7]
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const float4 *src = reinterpret_cast<const float4 *>(Q + (size_t)qi * row + h * 64 + 16 * ks + 8 * hf);
+        const float4 x0 = src[0], x1 = src[1];
+        qf[ks][0] = (_Float16)(x0.x * scale), qf[ks][1] = (_Float16)(x0.y * scale);
+        qf[ks][2] = (_Float16)(x0.z * scale), qf[ks][3] = (_Float16)(x0.w * scale);
+        qf[ks][4] = (_Float16)(x1.x * scale), qf[ks][5] = (_Float16)(x1.y * scale);
+        qf[ks][6] = (_Float16)(x1.z * scale), qf[ks][7] = (_Float16)(x1.w * scale);
+    }
+    const _Float16 *kb = Kh + (size_t)h * n_pad * 64 + (size_t)c * 64 + 8 * hf;
+    const _Float16 *vb = Vt + (size_t)h * 64 * n_pad + (size_t)c * n_pad + 8 * hf;
+    // one key block's fragments: K (A operand of step ks: key c, dims 16ks + 8h …) and Vᵀ (A operand of dim tile t,
+    // step st: dim 32t + c, slots 16st + 8h …)
+    struct Frag {
+        half8 k[4], v[2][2];
+    };
+    auto load = [&](Frag &f, int k0) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) f.k[ks] = *reinterpret_cast<const half8 *>(kb + (size_t)k0 * 64 + 16 * ks);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int st = 0; st < 2; st++)
+                f.v[t][st] = *reinterpret_cast<const half8 *>(vb + (size_t)(32 * t) * n_pad + k0 + 16 * st);
+    };
+    f32x16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[t][i] = 0.0f;
     float m = -3.0e38f, l = 0.0f;
-    const _Float16 *kb = Kh + (size_t)h * n_pad * 64, *vb = Vh + (size_t)h * n_pad * 64;
-    for (int k0 = 0; k0 < n_tok; k0 += AB) {
-        __syncthreads();
-        // the block's keys / values: 32 × 64 halves each = 256 × 16 bytes
-        reinterpret_cast<int4 *>(s_k)[tid] = reinterpret_cast<const int4 *>(kb + (size_t)k0 * 64)[tid];
-        reinterpret_cast<int4 *>(s_v)[tid] = reinterpret_cast<const int4 *>(vb + (size_t)k0 * 64)[tid];
-        __syncthreads();
-        const int nb = min(AB, n_tok - k0);
-        float s[AB];
+    // one key block at k0; MASK: the block holds keys ≥ n_tok (the last one only), which take no part in the max and
+    // get p = 0. A rescale by corr = 1 is skipped (x·1 = x).
+    auto block = [&](const Frag &f, int k0, auto mask) {
+        constexpr bool MASK = decltype(mask)::value;
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.k[ks], qf[ks], s, 0, 0, 0);
         float mx = m;
 #pragma unroll
-        for (int j = 0; j < AB; j++) {
-            float d_ = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 16; d++) d_ = fmaf(q[d], (float)s_k[j * 64 + 16 * part + d], d_);
-            d_ += lane_swap<1>(d_, lane);
-            d_ += lane_swap<2>(d_, lane);
-            s[j] = d_;
-            if (j < nb) mx = fmaxf(mx, d_);
-        }
-        const float corr = expf(m - mx);
+        for (int i = 0; i < 16; i++)
+            if (!MASK || k0 + 8 * (i >> 2) + 4 * hf + (i & 3) < n_tok) mx = fmaxf(mx, s[i]);
+        mx = pair_max<32>(mx);
+        // e^(s − mx) = 2^(s·log2 e − mx·log2 e): one fma and v_exp_f32 a score; P rounded to f16 in pairs
+        // (v_cvt_pk_f16_f32, round to nearest even) and summed as f32 by v_dot2 against (1, 1)
+        constexpr float LOG2E = 1.4426950408889634f;
+        const float corr = __builtin_amdgcn_exp2f((m - mx) * LOG2E), nml = -mx * LOG2E;
+        half8 pb[2];
         float ps = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 16; d++) acc[d] *= corr;
-#pragma unroll
-        for (int j = 0; j < AB; j++) {
-            const float p = j < nb ? (float)(_Float16)expf(s[j] - mx) : 0.0f;
-            ps += p;
-#pragma unroll
-            for (int d = 0; d < 16; d++) acc[d] = fmaf(p, (float)s_v[j * 64 + 16 * part + d], acc[d]);
+        for (int i = 0; i < 16; i += 2) {
+            float2_t e = {__builtin_amdgcn_exp2f(fmaf(s[i], LOG2E, nml)),
+                          __builtin_amdgcn_exp2f(fmaf(s[i + 1], LOG2E, nml))};
+            if (MASK) {
+                if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) >= n_tok) e[0] = 0.0f;
+                if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) + 1 >= n_tok) e[1] = 0.0f;
+            }
+            const half2_t p2 = __builtin_convertvector(e, half2_t);
+            pb[i >> 3][i & 7] = p2[0];
+            pb[i >> 3][(i & 7) + 1] = p2[1];
+            ps = __builtin_amdgcn_fdot2(p2, half2_t{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
         }
-        l = l * corr + ps;
+        l = l * corr + pair_sum<32>(ps);
         m = mx;
-    }
-    if (blockIdx.x * AQ + ql < n_tok) {
-        const float inv = 1.0f / l;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
 #pragma unroll
-        for (int d = 0; d < 16; d++) O[(size_t)qi * row + h * 64 + 16 * part + d] = (_Float16)(acc[d] * inv);
+            for (int t = 0; t < 2; t++) o[t] *= corr;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int st = 0; st < 2; st++)
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.v[t][st], pb[st], o[t], 0, 0, 0);
+    };
+    // two fragment sets in turn: the next block loads into one while the other is in use (loads past the last block
+    // repeat the last one: in bounds)
+    const int n_full = n_tok / FB, tail = n_full * FB < n_tok;
+    Frag fa, fb;
+    load(fa, 0);
+    int b = 0;
+    for (; b + 2 <= n_full; b += 2) {
+        load(fb, (b + 1) * FB);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads a whole block ahead of their use
+        block(fa, b * FB, std::false_type{});
+        load(fa, min((b + 2) * FB, n_pad - FB));
+        __builtin_amdgcn_sched_barrier(0);
+        block(fb, (b + 1) * FB, std::false_type{});
+    }
+    if (b < n_full) {  // one full block left in fa, perhaps the tail after it
+        if (tail) load(fb, (b + 1) * FB);
+        block(fa, b * FB, std::false_type{});
+        if (tail) block(fb, (b + 1) * FB, std::true_type{});
+    } else if (tail) {
+        block(fa, b * FB, std::true_type{});
+    }
+    if (q0 + c < n_tok) {
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        const float inv = 1.0f / l;
+        _Float16 *dst = O + (size_t)(q0 + c) * row + h * 64 + 4 * hf;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                *reinterpret_cast<half4 *>(dst + 32 * t + 8 * r) =
+                    half4{(_Float16)(o[t][4 * r] * inv), (_Float16)(o[t][4 * r + 1] * inv),
+                          (_Float16)(o[t][4 * r + 2] * inv), (_Float16)(o[t][4 * r + 3] * inv)};
     }
 }
 
@@ -231,18 +338,20 @@ int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, in
     return htr_launched(dev, "k_rope2d");
 }
 
-int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kh, _Float16 *vh,
+int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kh, _Float16 *vt,
                      int n_tok, int n_head, int n_pad) {
-    hipLaunchKernelGGL(k_heads_f16, dim3(grid_for((size_t)n_head * n_pad * 64)), dim3(VW), 0, st, k, v, kh, vh, n_tok,
-                       n_head, n_pad);
+    if (n_pad % FB || n_pad < n_tok) return htr_fail("vision K / V: %d padded keys for %d tokens", n_pad, n_tok);
+    hipLaunchKernelGGL(k_heads_f16, dim3(n_pad / FB, n_head), dim3(VW), 0, st, k, v, kh, vt, n_tok, n_head, n_pad);
     return htr_launched(dev, "k_heads_f16");
 }
 
-int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kh, const _Float16 *vh,
+int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kh, const _Float16 *vt,
                        _Float16 *o, int n_tok, int n_head, int n_pad, float scale) {
-    if (n_pad % AB || n_pad < n_tok) return htr_fail("vision attention: %d padded keys for %d tokens", n_pad, n_tok);
-    hipLaunchKernelGGL(k_attn_vision, dim3((n_tok + AQ - 1) / AQ, n_head), dim3(VW), 0, st, q, kh, vh, o, n_tok, n_head,
-                       n_pad, scale);
+    if (n_tok < 1 || n_pad % FB || n_pad < n_tok)
+        return htr_fail("vision attention: %d padded keys for %d tokens", n_pad, n_tok);
+    const int n_qt = (n_tok + FQ * FWAVES - 1) / (FQ * FWAVES);
+    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kh, vt, o, n_tok, n_head, n_pad, n_qt,
+                       scale);
     return htr_launched(dev, "k_attn_vision");
 }
 

@@ -50,7 +50,7 @@ struct htr_vision {
     uint8_t *rgb = nullptr;
     size_t rgb_cap = 0;
     float *P = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *tmp = nullptr, *cs = nullptr;
-    _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kh = nullptr, *vh = nullptr;
+    _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kh = nullptr, *vt = nullptr;
 };
 
 namespace {
@@ -69,11 +69,11 @@ int up_w16(htr_device *dev, const void *h, size_t rows, size_t cols, float scale
 
 void free_bufs(htr_vision *v) {
     for (void *p : {(void *)v->rgb, (void *)v->P, (void *)v->x, (void *)v->q, (void *)v->k, (void *)v->v, (void *)v->tmp,
-                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kh, (void *)v->vh})
+                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kh, (void *)v->vt})
         if (p) htr_dev_free(v->dev, p);
     v->rgb = nullptr;
     v->P = v->x = v->q = v->k = v->v = v->tmp = v->cs = nullptr;
-    v->h16 = v->a16 = v->g16 = v->kh = v->vh = nullptr;
+    v->h16 = v->a16 = v->g16 = v->kh = v->vt = nullptr;
     v->n_cap = v->pos_cap = 0;
     v->rgb_cap = 0;
 }
@@ -98,7 +98,7 @@ int ensure_bufs(htr_vision *v, int n, int max_pos, size_t rgb_bytes) {
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->a16);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * f * 2, HTR_MEM_WORK, (void **)&v->g16);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->kh);
-        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->vh);
+        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->vt);
         if (rc < 0) {
             std::string keep = htr_last_error();
             free_bufs(v);
@@ -228,8 +228,8 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
         HTR_TRY(launch_rope2d(dev, st, v->q, v->cs, n, c.n_head, c.d_head, px, max_pos));
         HTR_TRY(launch_rope2d(dev, st, v->k, v->cs, n, c.n_head, c.d_head, px, max_pos));
-        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kh, v->vh, n, c.n_head, n_pad));
-        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kh, v->vh, v->a16, n, c.n_head, n_pad, scale));
+        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kh, v->vt, n, c.n_head, n_pad));
+        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kh, v->vt, v->a16, n, c.n_head, n_pad, scale));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_ACC, v->a16, n, l.o, nullptr, v->x, nullptr, 1.0f));
         HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln2, v->h16, n, d, c.eps));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_FFN, v->h16, n, l.gate, l.up, nullptr, v->g16, 1.0f / FFN_DOWN_SCALE));

@@ -37,6 +37,24 @@ template <int M> __device__ __forceinline__ uint32_t lane_swap_u32(uint32_t v, i
     return __float_as_uint(lane_swap<M>(__uint_as_float(v), lane));
 }
 
+// max / sum of a value and its partner across lane bit M (16 or 32), the same in both lanes. The permlane swap of v
+// with itself returns, in every lane, its own value in one result and the partner's in the other (which one depends
+// on the lane), so the symmetric op takes both without selecting.
+template <int M> __device__ __forceinline__ float pair_max(float v) {
+    static_assert(M == 16 || M == 32, "lane bit");
+    const unsigned u = __float_as_uint(v);
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+template <int M> __device__ __forceinline__ float pair_sum(float v) {
+    static_assert(M == 16 || M == 32, "lane bit");
+    const unsigned u = __float_as_uint(v);
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Σ over the lanes that differ in bits [0, log2(2·M0)): masks M0, M0/2, …, 1
 template <int M0> __device__ __forceinline__ float group_sum(float v, int lane) {
     if constexpr (M0 >= 32) v += lane_swap<32>(v, lane);
