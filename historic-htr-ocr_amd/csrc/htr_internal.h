@@ -160,10 +160,12 @@ int launch_rms_norm_f16(htr_device *dev, hipStream_t st, const float *x, const f
                         float eps);
 int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, int n_tok, int n_head, int d_head, int px,
                   int max_pos);
-int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kh, _Float16 *vt,
-                     int n_tok, int n_head, int n_pad);
-int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kh, const _Float16 *vt,
-                       _Float16 *o, int n_tok, int n_head, int n_pad, float scale);
+// K / V of the vision attention as f16 key blocks of 8 KB per head (vision_kv_bytes in all)
+int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kv, int n_tok,
+                     int n_head);
+size_t vision_kv_bytes(int n_tok, int n_head);
+int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kv, _Float16 *o, int n_tok,
+                       int n_head, float scale);
 int launch_unfold2x2(htr_device *dev, hipStream_t st, const float *x, float *z, int px, int py, int dim);
 int launch_gelu(htr_device *dev, hipStream_t st, float *x, size_t n);
 // Y[M,N] (+)= X[M,K]·Wᵀ, f32 X, W f32 or f16 (w_f16), any K

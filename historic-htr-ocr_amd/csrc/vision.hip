@@ -77,18 +77,24 @@ __device__ __forceinline__ int vt_key(int slot) {
     return 16 * st + 8 * (j >> 2) + 4 * hf + (j & 3);
 }
 
-// heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16, keys n … n_pad − 1 zero. K as [H][n_pad][64]; V transposed
-// per head as [H][64][n_pad] with the keys of each block of 32 in vt_key order. grid (n_pad / 32, H), one block of
-// 32 keys of one head per workgroup; V goes through LDS for the transposition.
-__global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V, _Float16 *Kh, _Float16 *Vt, int n_tok,
-                                                  int n_head, int n_pad) {
+// K / V of one head in blocks of 32 keys, 8 KB a block: K [32 keys][64 dims] then Vᵀ [64 dims][32 slots], f16, in
+// 16-byte chunks placed so that the attention's fragment reads from LDS hit 8 different bank groups in every 8 lanes:
+// K row r, chunk j (dims 8j …) at chunk r·8 + (j ^ (r % 8)); Vᵀ row d, chunk q (slots 8q …) at 256 + d·4 + (q ^ (d/2 % 4))
+constexpr int KVB = 8192;
+__device__ __forceinline__ int kv_kchunk(int r, int j) { return r * 8 + (j ^ (r & 7)); }
+__device__ __forceinline__ int kv_vchunk(int d, int q) { return 256 + d * 4 + (q ^ ((d >> 1) & 3)); }
+
+// heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16 blocks as above, keys n … ⌈n/32⌉·32 − 1 zero. grid (blocks, H),
+// one block of one head per workgroup; V goes through LDS for the transposition.
+__global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V, _Float16 *KV, int n_tok, int n_head,
+                                                  int n_blk) {
     __shared__ _Float16 s_v[32][64 + 2];
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int r = tid >> 3, d0 = (tid & 7) * 8, t = 32 * b + r;
+    const int r = tid >> 3, j8 = tid & 7, t = 32 * b + r;
     float kv[8] = {}, vv[8] = {};
     if (t < n_tok) {
-        const float4 *ks = reinterpret_cast<const float4 *>(K + (size_t)t * n_head * 64 + h * 64 + d0);
-        const float4 *vs = reinterpret_cast<const float4 *>(V + (size_t)t * n_head * 64 + h * 64 + d0);
+        const float4 *ks = reinterpret_cast<const float4 *>(K + (size_t)t * n_head * 64 + h * 64 + 8 * j8);
+        const float4 *vs = reinterpret_cast<const float4 *>(V + (size_t)t * n_head * 64 + h * 64 + 8 * j8);
         const float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
         kv[0] = k0.x, kv[1] = k0.y, kv[2] = k0.z, kv[3] = k0.w, kv[4] = k1.x, kv[5] = k1.y, kv[6] = k1.z, kv[7] = k1.w;
         vv[0] = v0.x, vv[1] = v0.y, vv[2] = v0.z, vv[3] = v0.w, vv[4] = v1.x, vv[5] = v1.y, vv[6] = v1.z, vv[7] = v1.w;
@@ -97,15 +103,16 @@ __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         kh[j] = (_Float16)kv[j];
-        s_v[r][d0 + j] = (_Float16)vv[j];
+        s_v[r][8 * j8 + j] = (_Float16)vv[j];
     }
-    *reinterpret_cast<half8 *>(Kh + ((size_t)h * n_pad + t) * 64 + d0) = kh;
+    half8 *blk = reinterpret_cast<half8 *>(KV + ((size_t)h * n_blk + b) * (KVB / 2));
+    blk[kv_kchunk(r, j8)] = kh;
     __syncthreads();
-    const int d = tid >> 2, chunk = tid & 3;
+    const int d = tid >> 2, q = tid & 3;
     half8 vt;
 #pragma unroll
-    for (int j = 0; j < 8; j++) vt[j] = s_v[vt_key(8 * chunk + j)][d];
-    *reinterpret_cast<half8 *>(Vt + ((size_t)h * 64 + d) * n_pad + 32 * b + 8 * chunk) = vt;
+    for (int j = 0; j < 8; j++) vt[j] = s_v[vt_key(8 * q + j)][d];
+    blk[kv_vchunk(d, q)] = vt;
 }
 
 // attention_coop.wgsl's arithmetic on the f16 MFMAs: O[t][h] = softmax(q16·K16ᵀ)·V16 with q16 = f16(q·scale), keys in
@@ -114,14 +121,16 @@ __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V
 // A wave takes 32 queries of one head. Per key block, Sᵀ (32 keys × 32 queries) = K·q16ᵀ is 4 MFMAs 32x32x16: lane
 // ℓ = 32h + c then holds query c's scores of keys 8(i / 4) + 4h + i % 4 (i < 16), the other 16 in lane ℓ ^ 32. Oᵀ
 // (64 dims × 32 queries) += Vᵀ·Pᵀ is 4 more, lane ℓ accumulating dims 32t + 8(i / 4) + 4h + i % 4 of query c, so the
-// rescale by the query's corr stays in the lane. K and Vᵀ fragments (8 KB a block) are read straight from memory
-// (the head's keys stay in L2), the next block's while the current one is in use.
-// grid: ⌈n / 128⌉ · H workgroups of 4 waves, numbered so that the workgroups of one head run on one XCD.
-constexpr int FQ = 32, FB = 32, FWAVES = VW / 64;
+// rescale by the query's corr stays in the lane.
+// The 4 waves of a workgroup (128 queries) share the key blocks: stages of AST blocks are copied from memory to LDS
+// (coalesced 16-byte loads, the next stage's in flight while the current one is in use) and each wave reads its
+// fragments from there. grid: ⌈n / 128⌉ · H workgroups, numbered so that the workgroups of one head run on one XCD.
+constexpr int FQ = 32, FB = 32, FWAVES = VW / 64, AST = 2;
 
-__global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *Kh, const _Float16 *Vt, _Float16 *O,
-                                                    int n_tok, int n_head, int n_pad, int n_qt, float scale) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hf = lane >> 5, c = lane & 31;
+__global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *KV, _Float16 *O, int n_tok,
+                                                    int n_head, int n_blk, int n_qt, float scale) {
+    __shared__ __attribute__((aligned(16))) half8 s_kv[2][AST * KVB / 16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5, c = lane & 31;
     // workgroup b runs on XCD b % 8: with H a multiple of 8, XCD x takes heads x·H/8 … (x + 1)·H/8 − 1
     int h, qt;
     if (n_head % 8 == 0) {
@@ -144,21 +153,28 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         qf[ks][4] = (_Float16)(x1.x * scale), qf[ks][5] = (_Float16)(x1.y * scale);
         qf[ks][6] = (_Float16)(x1.z * scale), qf[ks][7] = (_Float16)(x1.w * scale);
     }
-    const _Float16 *kb = Kh + (size_t)h * n_pad * 64 + (size_t)c * 64 + 8 * hf;
-    const _Float16 *vb = Vt + (size_t)h * 64 * n_pad + (size_t)c * n_pad + 8 * hf;
-    // one key block's fragments: K (A operand of step ks: key c, dims 16ks + 8h …) and Vᵀ (A operand of dim tile t,
-    // step st: dim 32t + c, slots 16st + 8h …)
-    struct Frag {
-        half8 k[4], v[2][2];
+    // the lane's fragment chunks within a block: K step ks (key c, dims 16ks + 8h …), Vᵀ tile t step st (dim 32t + c,
+    // slots 16st + 8h …)
+    int kc[4], vc[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) kc[ks] = kv_kchunk(c, 2 * ks + hf);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int st = 0; st < 2; st++) vc[2 * t + st] = kv_vchunk(32 * t + c, 2 * st + hf);
+    // stage copies: AST blocks of 512 chunks, 2·AST chunks a thread (blocks past the last repeat it: in bounds)
+    const half8 *gkv = reinterpret_cast<const half8 *>(KV) + (size_t)h * n_blk * (KVB / 16);
+    half8 stg[2 * AST];
+    auto gload = [&](int stage) {
+#pragma unroll
+        for (int i = 0; i < 2 * AST; i++) {
+            const int blk = min(stage * AST + i / 2, n_blk - 1);
+            stg[i] = gkv[(size_t)blk * (KVB / 16) + (i % 2) * VW + tid];
+        }
     };
-    auto load = [&](Frag &f, int k0) {
+    auto lstore = [&](int buf) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) f.k[ks] = *reinterpret_cast<const half8 *>(kb + (size_t)k0 * 64 + 16 * ks);
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int st = 0; st < 2; st++)
-                f.v[t][st] = *reinterpret_cast<const half8 *>(vb + (size_t)(32 * t) * n_pad + k0 + 16 * st);
+        for (int i = 0; i < 2 * AST; i++) s_kv[buf][(i / 2) * (KVB / 16) + (i % 2) * VW + tid] = stg[i];
     };
     f32x16 o[2];
 #pragma unroll
@@ -166,15 +182,20 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
 #pragma unroll
         for (int i = 0; i < 16; i++) o[t][i] = 0.0f;
     float m = -3.0e38f, l = 0.0f;
-    // one key block at k0; MASK: the block holds keys ≥ n_tok (the last one only), which take no part in the max and
-    // get p = 0. A rescale by corr = 1 is skipped (x·1 = x).
-    auto block = [&](const Frag &f, int k0, auto mask) {
+    // one key block at k0 from LDS; MASK: the block holds keys ≥ n_tok (the last one only), which take no part in
+    // the max and get p = 0. A rescale by corr = 1 is skipped (x·1 = x).
+    auto block = [&](const half8 *sb, int k0, auto mask) {
         constexpr bool MASK = decltype(mask)::value;
+        half8 fk[4], fv[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) fk[ks] = sb[kc[ks]];
+#pragma unroll
+        for (int i = 0; i < 4; i++) fv[i] = sb[vc[i]];
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.k[ks], qf[ks], s, 0, 0, 0);
+        for (int ks = 0; ks < 4; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(fk[ks], qf[ks], s, 0, 0, 0);
         float mx = m;
 #pragma unroll
         for (int i = 0; i < 16; i++)
@@ -209,28 +230,26 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int st = 0; st < 2; st++)
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.v[t][st], pb[st], o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fv[2 * t + st], pb[st], o[t], 0, 0, 0);
     };
-    // two fragment sets in turn: the next block loads into one while the other is in use (loads past the last block
-    // repeat the last one: in bounds)
-    const int n_full = n_tok / FB, tail = n_full * FB < n_tok;
-    Frag fa, fb;
-    load(fa, 0);
-    int b = 0;
-    for (; b + 2 <= n_full; b += 2) {
-        load(fb, (b + 1) * FB);
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads a whole block ahead of their use
-        block(fa, b * FB, std::false_type{});
-        load(fa, min((b + 2) * FB, n_pad - FB));
-        __builtin_amdgcn_sched_barrier(0);
-        block(fb, (b + 1) * FB, std::false_type{});
-    }
-    if (b < n_full) {  // one full block left in fa, perhaps the tail after it
-        if (tail) load(fb, (b + 1) * FB);
-        block(fa, b * FB, std::false_type{});
-        if (tail) block(fb, (b + 1) * FB, std::true_type{});
-    } else if (tail) {
-        block(fa, b * FB, std::true_type{});
+    const int n_stage = (n_blk + AST - 1) / AST;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int sg = 0; sg < n_stage; sg++) {
+        const int buf = sg & 1;
+        if (sg + 1 < n_stage) gload(sg + 1);
+#pragma unroll
+        for (int j = 0; j < AST; j++) {
+            const int k0 = (sg * AST + j) * FB;
+            if (k0 + FB <= n_tok)
+                block(s_kv[buf] + j * (KVB / 16), k0, std::false_type{});
+            else if (k0 < n_tok)
+                block(s_kv[buf] + j * (KVB / 16), k0, std::true_type{});
+        }
+        // the other buffer was last read in the previous stage, before the barrier that ended it
+        if (sg + 1 < n_stage) lstore(buf ^ 1);
+        __syncthreads();
     }
     if (q0 + c < n_tok) {
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -338,20 +357,20 @@ int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, in
     return htr_launched(dev, "k_rope2d");
 }
 
-int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kh, _Float16 *vt,
-                     int n_tok, int n_head, int n_pad) {
-    if (n_pad % FB || n_pad < n_tok) return htr_fail("vision K / V: %d padded keys for %d tokens", n_pad, n_tok);
-    hipLaunchKernelGGL(k_heads_f16, dim3(n_pad / FB, n_head), dim3(VW), 0, st, k, v, kh, vt, n_tok, n_head, n_pad);
+int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kv, int n_tok,
+                     int n_head) {
+    const int n_blk = (n_tok + FB - 1) / FB;
+    hipLaunchKernelGGL(k_heads_f16, dim3(n_blk, n_head), dim3(VW), 0, st, k, v, kv, n_tok, n_head, n_blk);
     return htr_launched(dev, "k_heads_f16");
 }
 
-int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kh, const _Float16 *vt,
-                       _Float16 *o, int n_tok, int n_head, int n_pad, float scale) {
-    if (n_tok < 1 || n_pad % FB || n_pad < n_tok)
-        return htr_fail("vision attention: %d padded keys for %d tokens", n_pad, n_tok);
-    const int n_qt = (n_tok + FQ * FWAVES - 1) / (FQ * FWAVES);
-    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kh, vt, o, n_tok, n_head, n_pad, n_qt,
-                       scale);
+size_t vision_kv_bytes(int n_tok, int n_head) { return (size_t)n_head * ((n_tok + FB - 1) / FB) * KVB; }
+
+int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kv, _Float16 *o, int n_tok,
+                       int n_head, float scale) {
+    if (n_tok < 1) return htr_fail("vision attention: %d tokens", n_tok);
+    const int n_qt = (n_tok + FQ * FWAVES - 1) / (FQ * FWAVES), n_blk = (n_tok + FB - 1) / FB;
+    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kv, o, n_tok, n_head, n_blk, n_qt, scale);
     return htr_launched(dev, "k_attn_vision");
 }
 

@@ -50,7 +50,7 @@ struct htr_vision {
     uint8_t *rgb = nullptr;
     size_t rgb_cap = 0;
     float *P = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *tmp = nullptr, *cs = nullptr;
-    _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kh = nullptr, *vt = nullptr;
+    _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kv = nullptr;
 };
 
 namespace {
@@ -69,11 +69,11 @@ int up_w16(htr_device *dev, const void *h, size_t rows, size_t cols, float scale
 
 void free_bufs(htr_vision *v) {
     for (void *p : {(void *)v->rgb, (void *)v->P, (void *)v->x, (void *)v->q, (void *)v->k, (void *)v->v, (void *)v->tmp,
-                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kh, (void *)v->vt})
+                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kv})
         if (p) htr_dev_free(v->dev, p);
     v->rgb = nullptr;
     v->P = v->x = v->q = v->k = v->v = v->tmp = v->cs = nullptr;
-    v->h16 = v->a16 = v->g16 = v->kh = v->vt = nullptr;
+    v->h16 = v->a16 = v->g16 = v->kv = nullptr;
     v->n_cap = v->pos_cap = 0;
     v->rgb_cap = 0;
 }
@@ -84,7 +84,7 @@ int ensure_bufs(htr_vision *v, int n, int max_pos, size_t rgb_bytes) {
     htr_device *dev = v->dev;
     if (n > v->n_cap || max_pos > v->pos_cap || rgb_bytes > v->rgb_cap) {
         free_bufs(v);
-        const size_t d = c.dim, f = c.n_ff, pp = 3 * (size_t)c.patch * c.patch, n_pad = (size_t)(n + 31) / 32 * 32;
+        const size_t d = c.dim, f = c.n_ff, pp = 3 * (size_t)c.patch * c.patch;
         const size_t qkv = (size_t)n * std::max<size_t>(d, (size_t)c.proj_dim);
         int rc = htr_dev_alloc(dev, rgb_bytes, HTR_MEM_WORK, (void **)&v->rgb);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * pp * 4, HTR_MEM_WORK, (void **)&v->P);
@@ -97,8 +97,7 @@ int ensure_bufs(htr_vision *v, int n, int max_pos, size_t rgb_bytes) {
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->h16);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->a16);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * f * 2, HTR_MEM_WORK, (void **)&v->g16);
-        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->kh);
-        if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_head * n_pad * 64 * 2, HTR_MEM_WORK, (void **)&v->vt);
+        if (rc == 0) rc = htr_dev_alloc(dev, vision_kv_bytes((int)n, c.n_head), HTR_MEM_WORK, (void **)&v->kv);
         if (rc < 0) {
             std::string keep = htr_last_error();
             free_bufs(v);
@@ -208,7 +207,7 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
     HTR_TRY(htr_vision_out_shape(v, width, height, n_layers, nullptr, nullptr));
     const htr_vision_config &c = v->cfg;
     const int px = width / c.patch, py = height / c.patch, n = px * py, d = c.dim, pp = 3 * c.patch * c.patch;
-    const int n_pad = (n + 31) / 32 * 32, max_pos = std::max(px, py);
+    const int max_pos = std::max(px, py);
     const size_t rgb_bytes = (size_t)width * height * 3;
     HTR_TRY(ensure_bufs(v, n, max_pos, rgb_bytes));
     hipStream_t st = dev->stream;
@@ -228,8 +227,8 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
         HTR_TRY(launch_rope2d(dev, st, v->q, v->cs, n, c.n_head, c.d_head, px, max_pos));
         HTR_TRY(launch_rope2d(dev, st, v->k, v->cs, n, c.n_head, c.d_head, px, max_pos));
-        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kh, v->vt, n, c.n_head, n_pad));
-        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kh, v->vt, v->a16, n, c.n_head, n_pad, scale));
+        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kv, n, c.n_head));
+        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kv, v->a16, n, c.n_head, scale));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_ACC, v->a16, n, l.o, nullptr, v->x, nullptr, 1.0f));
         HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln2, v->h16, n, d, c.eps));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_FFN, v->h16, n, l.gate, l.up, nullptr, v->g16, 1.0f / FFN_DOWN_SCALE));
