@@ -126,10 +126,56 @@ __device__ __forceinline__ void st_dev(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NI>
+__device__ __forceinline__ int4 pack8(const float (&f)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const _Float16 lo = (_Float16)f[2 * i], hi = (_Float16)f[2 * i + 1];
+        uint16_t a, b;
+        __builtin_memcpy(&a, &lo, 2);
+        __builtin_memcpy(&b, &hi, 2);
+        u[i] = (uint32_t)a | ((uint32_t)b << 16);
+    }
+    return make_int4((int)u[0], (int)u[1], (int)u[2], (int)u[3]);
+}
+
+// qkv_post.wgsl's per-head RMS norm and RoPE NEOX (pairs (i, i + 64)) at one position, for the 8 dims 8j … 8j + 7
+// of one head's raw row x[128]: the 16 lanes j = 0 … 15 of a lane row hold the head together (Σx² over them); the
+// partner dims (j ^ 8) are read from memory
+__device__ __forceinline__ void post_slice(const float *x, const float *w, const float *rr, int j, int lane, float eps,
+                                           float (&out)[8]) {
+    const int jp = j ^ 8;
+    float a[8], b[8];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float4 va = *reinterpret_cast<const float4 *>(x + 8 * j + 4 * h);
+        const float4 vb = *reinterpret_cast<const float4 *>(x + 8 * jp + 4 * h);
+        a[4 * h] = va.x, a[4 * h + 1] = va.y, a[4 * h + 2] = va.z, a[4 * h + 3] = va.w;
+        b[4 * h] = vb.x, b[4 * h + 1] = vb.y, b[4 * h + 2] = vb.z, b[4 * h + 3] = vb.w;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss = fmaf(a[e], a[e], ss);
+    ss = group_sum<8>(ss, lane);
+    const float scale = 1.0f / sqrtf(ss / (float)D + eps);
+    const int i0 = 8 * (j & 7);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float ya = (a[e] * scale) * w[8 * j + e], yb = (b[e] * scale) * w[8 * jp + e];
+        const float c = rr[2 * (i0 + e)], s = rr[2 * (i0 + e) + 1];
+        out[e] = j < 8 ? ya * c - yb * s : yb * s + ya * c;
+    }
+}
+
+// FUSED: q is the raw [q | k | v] row of the qkv matvec and the kernel does qkv_post's work itself: each workgroup
+// norms and ropes its two q heads; the new key / value (position n_keys − 1) are made from the raw row, rounded to
+// f16 as the cache holds them, used in place of the cache row by the workgroup whose chunk holds them, and stored
+// into the cache by that workgroup (no other workgroup reads that row)
+template <int NI, bool FUSED>
 __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float16 *kc, const _Float16 *vc, int n_kv,
                                                     int n_ctx, const int *pos_dev, int n_keys_arg, int max_chunk,
-                                                    float scale, float *part, uint32_t *counters, float *out) {
+                                                    float scale, float *part, uint32_t *counters, float *out,
+                                                    AttnFuse fz) {
     constexpr int C = 16 * NI;
     constexpr int N = 2 * NI;              // (key, head) values per thread
     constexpr int KL = C >= 64 ? C / 64 : 1;  // keys per lane in the softmax
@@ -144,6 +190,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
     const int j = tid & 15, kk = tid >> 4;
     // keys beyond the cache are never read (the host checks positions first; a bad one yields no output)
     const int n_keys = min(pos_dev ? *pos_dev + 1 : n_keys_arg, n_ctx);
+    if (FUSED && pos_dev && *pos_dev >= n_ctx) return;  // the cache has no such row (the host checks positions first)
     const int n_chunk = (n_keys + C - 1) / C;
     if (c >= n_chunk || n_chunk > max_chunk) return;  // uniform per workgroup
     const int k0 = c * C;
@@ -163,10 +210,33 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         vr[i] = aload16(vb + (size_t)key * D + 8 * j);
     }
     float qa[8], qb[8];
+    int4 knew = make_int4(0, 0, 0, 0), vnew = make_int4(0, 0, 0, 0);
+    const int pos = n_keys - 1;
+    if constexpr (FUSED) {
+        const float *rr = fz.rope + (size_t)pos * D;
+        float ta[8], tb[8], kn8[8], v8[8];
+        post_slice(q + (size_t)h0 * D, fz.qn, rr, j, lane, fz.eps, ta);
+        post_slice(q + (size_t)(h0 + 1) * D, fz.qn, rr, j, lane, fz.eps, tb);
+        post_slice(q + (size_t)(fz.n_head + kvh) * D, fz.kn, rr, j, lane, fz.eps, kn8);
+        const float *vraw = q + (size_t)(fz.n_head + n_kv + kvh) * D + 8 * j;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        qa[e] = q[h0 * D + 8 * j + e] * scale;
-        qb[e] = q[(h0 + 1) * D + 8 * j + e] * scale;
+        for (int e = 0; e < 8; e++) {
+            qa[e] = ta[e] * scale;
+            qb[e] = tb[e] * scale;
+            v8[e] = vraw[e];
+        }
+        knew = pack8(kn8);
+        vnew = pack8(v8);
+        if (c == n_chunk - 1 && kk == 0) {
+            *reinterpret_cast<int4 *>(fz.kc + ((size_t)kvh * n_ctx + pos) * D + 8 * j) = knew;
+            *reinterpret_cast<int4 *>(fz.vc + ((size_t)kvh * n_ctx + pos) * D + 8 * j) = vnew;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            qa[e] = q[h0 * D + 8 * j + e] * scale;
+            qb[e] = q[(h0 + 1) * D + 8 * j + e] * scale;
+        }
     }
 
     // 1. scores
@@ -174,7 +244,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         float kf[8];
-        unpack8(kr[i], kf);
+        unpack8(FUSED && k0 + kk + 16 * i == pos ? knew : kr[i], kf);
         float da = 0.0f, db = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -237,7 +307,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         float vf[8];
-        unpack8(vr[i], vf);
+        unpack8(FUSED && k0 + kk + 16 * i == pos ? vnew : vr[i], vf);
         const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -401,7 +471,7 @@ int launch_qkv_post(htr_device *dev, hipStream_t st, float *qkv, const float *qn
 
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
-                       const AttnScratch &sc, float *out) {
+                       const AttnScratch &sc, float *out, const AttnFuse *fuse) {
     if (n_head != 2 * n_kv) return htr_fail("decode attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
     if (sc.chunk < 16 || sc.chunk > MAX_CHUNK_KEYS || (sc.chunk & (sc.chunk - 1)))
         return htr_fail("decode attention: chunk %d (a power of two, 16 … %d)", sc.chunk, MAX_CHUNK_KEYS);
@@ -411,7 +481,18 @@ int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const ui
                         sc.chunk, n_ctx, MAX_CHUNKS);
     const int grid_x = pos_dev ? sc.max_chunk : (n_keys + sc.chunk - 1) / sc.chunk;
     const dim3 grid(grid_x, n_kv);
-#define HTR_ATTN(NI)                                                                                                       hipLaunchKernelGGL(k_attn_decode<NI>, grid, dim3(AW), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc, n_kv,                         n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part, sc.counters, out)
+    const AttnFuse fz = fuse ? *fuse : AttnFuse{};
+    if (fuse && (fz.n_head != n_head || !fz.qn || !fz.kn || !fz.rope || !fz.kc || !fz.vc))
+        return htr_fail("decode attention: incomplete qkv_post arguments");
+#define HTR_ATTN(NI)                                                                                                   \
+    if (fuse)                                                                                                          \
+        hipLaunchKernelGGL((k_attn_decode<NI, true>), grid, dim3(AW), 0, st, q, (const _Float16 *)kc,                  \
+                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part,           \
+                           sc.counters, out, fz);                                                                      \
+    else                                                                                                               \
+        hipLaunchKernelGGL((k_attn_decode<NI, false>), grid, dim3(AW), 0, st, q, (const _Float16 *)kc,                 \
+                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part,           \
+                           sc.counters, out, fz)
     switch (sc.chunk / 16) {
     case 1: HTR_ATTN(1); break;
     case 2: HTR_ATTN(2); break;

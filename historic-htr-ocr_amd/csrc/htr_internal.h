@@ -84,6 +84,8 @@ struct DmvMat {
     const _Float16 *d;
     int rows;
 };
+// rows per wave of the decoder-shaped matvec (one workgroup per CU), 0 when the shape is not one
+int dmv_full_rw(htr_device *dev, int mode, const DmvMat *mats, int n_mats, int k);
 int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, int n_mats, int k, const float *x,
                const float *nw, float eps, float *y, int acc);
 int launch_dmv_many(htr_device *dev, hipStream_t st, const DmvMat *mats, int n, int k, const float *x, float *y);
@@ -105,9 +107,16 @@ int attn_chunk_for(int n_ctx);
 size_t attn_part_bytes(int n_head, int max_chunk);
 // bytes of the split-K ticket counters (one 128-byte line per KV head; zero, self-resetting)
 size_t attn_counter_bytes(int n_kv);
+// qkv_post's work done inside the attention (q then is the raw [q | k | v] row; the new key / value go to kc / vc)
+struct AttnFuse {
+    const float *qn, *kn, *rope;
+    float eps;
+    int n_head;
+    _Float16 *kc, *vc;
+};
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
-                       const AttnScratch &sc, float *out);
+                       const AttnScratch &sc, float *out, const AttnFuse *fuse = nullptr);
 // prefill pieces: per-head norm + rope + KV store over n_tok rows
 int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k, const float *v, const float *qn,
                              const float *kn, const float *rope, int n_tok, int n_head, int n_kv, int pos0, int n_ctx,

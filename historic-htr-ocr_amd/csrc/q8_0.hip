@@ -279,6 +279,104 @@ template <int RW, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv(
     }
 }
 
+// The decoder's own shapes: K = 1024·NG (each lane holds NG whole groups of 16, no lane idle) and rows a multiple of
+// the tile, launched as one workgroup per CU with RW = rows / (4·CUs) rows a wave. A decode matvec is latency bound
+// (all of its loads go out at once); what is left is the VALU work after the loads land, and one wave per SIMD pays
+// the per-wave part (x, the norm, addressing, the reduction) once instead of once per row. No clamps or guards: the
+// host checks the shape. Same arithmetic as k_dmv (dot16 per group, fma by the block scale, wave_sum_rows).
+template <int RW, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv_full(const DmvK a) {
+    constexpr int NM = MODE == DMV_FFN ? 2 : 1;
+    constexpr int RT = WAVES * RW;
+    constexpr int K = 1024 * NG, NB = K / 32, PER_ROW = NB / 8;  // 16-byte scale units a row
+    constexpr int RP = RW == 3 ? 4 : RW;                          // rows reduced together (a power of two)
+    static_assert(RT * PER_ROW <= WG, "one scale unit per thread");
+    __shared__ _Float16 s_d[NM][RT * NB + 8];  // + one 16-byte slot that threads without a unit write
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.x * RT, wrow0 = row0 + wave * RW;
+    auto mat_of = [&](int row, int &lr) -> DmvMat {
+        if (MODE != DMV_QKV) {
+            lr = row;
+            return a.m[0];
+        }
+        const DmvMat m0 = uniform_mat(a.m[0]), m1 = uniform_mat(a.m[1]), m2 = uniform_mat(a.m[2]);
+        const int r0 = m0.rows, r01 = r0 + m1.rows;
+        const bool in1 = row >= r0, in2 = row >= r01;
+        lr = row - (in2 ? r01 : in1 ? r0 : 0);
+        DmvMat m;
+        m.q = in2 ? m2.q : in1 ? m1.q : m0.q;
+        m.d = in2 ? m2.d : in1 ? m1.d : m0.d;
+        m.rows = in2 ? m2.rows : in1 ? m1.rows : m0.rows;
+        return m;
+    };
+    float xv[NG][16], wv[NG][16];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = lane + 64 * i;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 v = gload16f(a.x + 16 * g + 4 * j);
+            xv[i][4 * j] = v.x, xv[i][4 * j + 1] = v.y, xv[i][4 * j + 2] = v.z, xv[i][4 * j + 3] = v.w;
+            if (MODE != DMV_PLAIN) {
+                const float4 w = gload16f(a.nw + 16 * g + 4 * j);
+                wv[i][4 * j] = w.x, wv[i][4 * j + 1] = w.y, wv[i][4 * j + 2] = w.z, wv[i][4 * j + 3] = w.w;
+            }
+        }
+    }
+    // the tile's scales: thread u < RT·PER_ROW moves unit u % PER_ROW of tile row u / PER_ROW (the others repeat
+    // unit 0 into the spare slot: no branch, which would hold the loads back until their use)
+    const bool has = threadIdx.x < RT * PER_ROW;
+    const int su = has ? threadIdx.x : 0, sr = su / PER_ROW, sp = su % PER_ROW;
+    uint4 sv[NM];
+    {
+        int lr;
+        const DmvMat m = mat_of(row0 + sr, lr);
+        sv[0] = gload16u(m.d + (size_t)lr * NB + 8 * sp);
+        if (NM == 2) sv[NM - 1] = gload16u(a.m[1].d + (size_t)lr * NB + 8 * sp);
+    }
+    int4 qv[NM][RW][NG];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        int lr;
+        const DmvMat m = mat_of(wrow0 + r, lr);
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            qv[0][r][i] = gload16(m.q + (size_t)lr * K + 16 * (lane + 64 * i));
+            if (NM == 2) qv[NM - 1][r][i] = gload16(a.m[1].q + (size_t)lr * K + 16 * (lane + 64 * i));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load is out before the norm waits for x
+    if (MODE != DMV_PLAIN) norm_x<NG>(xv, wv, a.eps, K, lane);
+    const int at = has ? sr * NB + 8 * sp : RT * NB;
+#pragma unroll
+    for (int t = 0; t < NM; t++) *reinterpret_cast<uint4 *>(s_d[t] + at) = sv[t];
+    __syncthreads();
+    float acc[NM][RP];
+#pragma unroll
+    for (int t = 0; t < NM; t++)
+#pragma unroll
+        for (int r = 0; r < RP; r++) {
+            float sum = 0.0f;
+            if (r < RW) {
+                const _Float16 *s_row = s_d[t] + (wave * RW + r) * NB;
+#pragma unroll
+                for (int i = 0; i < NG; i++)
+                    sum = fmaf(dot16(qv[t][r < RW ? r : 0][i], xv[i]), (float)s_row[(lane + 64 * i) >> 1], sum);
+            }
+            acc[t][r] = sum;
+        }
+    float v[NM];
+#pragma unroll
+    for (int t = 0; t < NM; t++) v[t] = wave_sum_rows<RP>(acc[t], lane);
+    constexpr int SPREAD = 64 / RP;
+    if ((lane & (SPREAD - 1)) == 0 && lane / SPREAD < RW) {
+        const int row = wrow0 + lane / SPREAD;
+        float out = v[0];
+        if (MODE == DMV_FFN) out = (v[0] / (1.0f + expf(-v[0]))) * v[NM - 1];
+        if (a.acc) out = a.y[row] + out;
+        a.y[row] = out;
+    }
+}
+
 template <int RW, int NG> __global__ __launch_bounds__(WG) void k_dmv_many(const DmvManyK a) {
     constexpr int RT = WAVES * RW;
     __shared__ _Float16 s_d[RT * NG * 32];
@@ -369,6 +467,15 @@ int rows_per_wave(int n_rows, int n_cu, int ng_lane, int nm) {
 
 }  // namespace
 
+int dmv_full_rw(htr_device *dev, int mode, const DmvMat *mats, int n_mats, int k) {
+    int rows = 0;
+    for (int i = 0; i < n_mats; i++) rows += mats[i].rows;
+    if (mode == DMV_FFN) rows = mats[0].rows;
+    if (k % 1024 != 0 || k > 3072 || rows % (WAVES * dev->n_cu) != 0) return 0;
+    const int rw = rows / (WAVES * dev->n_cu);
+    return rw <= 4 ? rw : 0;
+}
+
 int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, int n_mats, int k, const float *x,
                const float *nw, float eps, float *y, int acc) {
     if (k <= 0 || k % 32 != 0 || k > 4096) return htr_fail("matvec: K = %d (a multiple of 32, at most 4096)", k);
@@ -391,6 +498,32 @@ int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, in
     a.y = y;
     a.acc = acc;
     const int ng_lane = (k / 16 + 63) / 64;
+    const int full_rw = dmv_full_rw(dev, mode, mats, n_mats, k);
+    if (full_rw > 0) {
+        const dim3 grid(rows / (WAVES * full_rw));
+#define HTR_FULL(RW, MODE)                                                                                             \
+    switch (k / 1024) {                                                                                                \
+    case 1: hipLaunchKernelGGL((k_dmv_full<RW, 1, MODE>), grid, dim3(WG), 0, st, a); break;                            \
+    case 2: hipLaunchKernelGGL((k_dmv_full<RW, 2, MODE>), grid, dim3(WG), 0, st, a); break;                            \
+    default: hipLaunchKernelGGL((k_dmv_full<RW, 3, MODE>), grid, dim3(WG), 0, st, a); break;                           \
+    }
+#define HTR_FULL_RW(MODE)                                                                                              \
+    switch (full_rw) {                                                                                                 \
+    case 1: HTR_FULL(1, MODE) break;                                                                                   \
+    case 2: HTR_FULL(2, MODE) break;                                                                                   \
+    case 3: HTR_FULL(3, MODE) break;                                                                                   \
+    default: HTR_FULL(4, MODE) break;                                                                                  \
+    }
+        switch (mode) {
+        case DMV_PLAIN: HTR_FULL_RW(DMV_PLAIN) break;
+        case DMV_NORM: HTR_FULL_RW(DMV_NORM) break;
+        case DMV_QKV: HTR_FULL_RW(DMV_QKV) break;
+        default: HTR_FULL_RW(DMV_FFN) break;
+        }
+#undef HTR_FULL_RW
+#undef HTR_FULL
+        return htr_launched(dev, "k_dmv_full");
+    }
     const int rw = rows_per_wave(rows, dev->n_cu, ng_lane, mode == DMV_FFN ? 2 : 1);
     int rc = -1;
     switch (mode) {

@@ -3,7 +3,7 @@
 // decode (text.rs:587-625), on the kernels of q8_0.hip / attention.hip / choose.hip / gemm.hip.
 //
 // The decode step (record_step, text.rs:540-578 with layers_fused, text.rs:630-647) is 1 + 6·n_layer + 1 launches:
-//   embed → per layer: qkv matvec (attn_norm fused) → qkv_post (q/k norm, RoPE, f16 KV store) → split-K attention
+//   embed → per layer: qkv matvec (attn_norm fused) → split-K attention (q/k norm, RoPE and the f16 KV store fused)
 //   (merge fused) → o matvec (+ residual) → gate/up matvec (ffn_norm + SwiGLU fused) → down matvec (+ residual)
 //   → LM head (output_norm fused) [→ token choice].
 // Position and history length live in device memory (state[0] = pos, state[1] = len), so one captured HIP graph of
@@ -118,10 +118,9 @@ int record_step(htr_session *s, hipStream_t st) {
         uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
         DmvMat qkv[3] = {{ly.q->q, ly.q->d, qd}, {ly.k->q, ly.k->d, kvd}, {ly.v->q, ly.v->d, kvd}};
         HTR_TRY(launch_dmv(dev, st, DMV_QKV, qkv, 3, c.dim, s->x, ly.attn_norm, c.eps, s->qkv, 0));
-        HTR_TRY(launch_qkv_post(dev, st, s->qkv, ly.q_norm, ly.k_norm, s->rope, c.n_head, c.n_kv, s->state, 0, s->n_ctx,
-                                c.eps, kc, vc));
+        const AttnFuse fz{ly.q_norm, ly.k_norm, s->rope, c.eps, c.n_head, (_Float16 *)kc, (_Float16 *)vc};
         HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale, s->asc,
-                                   s->attn));
+                                   s->attn, &fz));
         DmvMat o = {ly.o->q, ly.o->d, c.dim};
         HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
         DmvMat gu[2] = {{ly.gate->q, ly.gate->d, c.n_ff}, {ly.up->q, ly.up->d, c.n_ff}};
