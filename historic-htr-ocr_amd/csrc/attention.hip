@@ -100,8 +100,9 @@ __global__ __launch_bounds__(64) void k_qk_rows(float *q, float *k, const float 
 constexpr int AW = 256;
 constexpr int MAX_CHUNK_KEYS = 256;  // C ≤ 256 (NI ≤ 16)
 constexpr int MAX_CHUNKS = 256;      // chunks per KV head: n_ctx ≤ 65536
-constexpr int MERGE_PREFETCH = 64;   // chunk partials each merging thread holds in registers (= the wave size: their
-                                     // weights are read from the lanes that hold them)
+constexpr int MERGE_FAST = 32;       // chunks merged by the branch-free path (each merging thread holds their o
+                                     // partials in registers; n_ctx ≤ 8192 stays within it)
+static_assert(MAX_CHUNKS % MERGE_FAST == 0, "the merge's weight groups fit s_w");
 constexpr int CNT_STRIDE = 32;       // ticket counters 128 bytes apart: the KV heads' atomics do not share a line
 
 __device__ __forceinline__ int4 aload16(const void *p) { return *reinterpret_cast<const int4 *>(p); }
@@ -140,29 +141,42 @@ __device__ __forceinline__ int4 pack8(const float (&f)[8]) {
 }
 
 // qkv_post.wgsl's per-head RMS norm and RoPE NEOX (pairs (i, i + 64)) at one position, for the 8 dims 8j … 8j + 7
-// of one head's raw row x[128]: the 16 lanes j = 0 … 15 of a lane row hold the head together (Σx² over them); the
-// partner dims (j ^ 8) are read from memory
-__device__ __forceinline__ void post_slice(const float *x, const float *w, const float *rr, int j, int lane, float eps,
-                                           float (&out)[8]) {
+// of one head's raw row: the 16 lanes j = 0 … 15 of a lane row hold the head together (Σx² over them); the lane also
+// holds the partner dims (slice j ^ 8). Loads first (post_load), the arithmetic later (post_apply), so that the
+// loads go out before the K / V loads and the arithmetic waits for these alone.
+struct PostIn {
+    float4 a[2], b[2], wa[2], wb[2];
+};
+__device__ __forceinline__ void post_load(PostIn &p, const float *x, const float *w, int j) {
     const int jp = j ^ 8;
-    float a[8], b[8];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        const float4 va = *reinterpret_cast<const float4 *>(x + 8 * j + 4 * h);
-        const float4 vb = *reinterpret_cast<const float4 *>(x + 8 * jp + 4 * h);
-        a[4 * h] = va.x, a[4 * h + 1] = va.y, a[4 * h + 2] = va.z, a[4 * h + 3] = va.w;
-        b[4 * h] = vb.x, b[4 * h + 1] = vb.y, b[4 * h + 2] = vb.z, b[4 * h + 3] = vb.w;
+        p.a[h] = *reinterpret_cast<const float4 *>(x + 8 * j + 4 * h);
+        p.b[h] = *reinterpret_cast<const float4 *>(x + 8 * jp + 4 * h);
+        p.wa[h] = *reinterpret_cast<const float4 *>(w + 8 * j + 4 * h);
+        p.wb[h] = *reinterpret_cast<const float4 *>(w + 8 * jp + 4 * h);
     }
+}
+__device__ __forceinline__ void unpack4x2(const float4 (&v)[2], float (&f)[8]) {
+    f[0] = v[0].x, f[1] = v[0].y, f[2] = v[0].z, f[3] = v[0].w, f[4] = v[1].x, f[5] = v[1].y, f[6] = v[1].z, f[7] = v[1].w;
+}
+// cs: the (c, s) pairs of rope indices 8(j % 8) … + 7
+__device__ __forceinline__ void post_apply(const PostIn &p, const float (&cs)[16], int j, int lane, float eps,
+                                           float (&out)[8]) {
+    float a[8], b[8], wa[8], wb[8];
+    unpack4x2(p.a, a);
+    unpack4x2(p.b, b);
+    unpack4x2(p.wa, wa);
+    unpack4x2(p.wb, wb);
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) ss = fmaf(a[e], a[e], ss);
     ss = group_sum<8>(ss, lane);
     const float scale = 1.0f / sqrtf(ss / (float)D + eps);
-    const int i0 = 8 * (j & 7);
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const float ya = (a[e] * scale) * w[8 * j + e], yb = (b[e] * scale) * w[8 * jp + e];
-        const float c = rr[2 * (i0 + e)], s = rr[2 * (i0 + e) + 1];
+        const float ya = (a[e] * scale) * wa[e], yb = (b[e] * scale) * wb[e];
+        const float c = cs[2 * e], s = cs[2 * e + 1];
         out[e] = j < 8 ? ya * c - yb * s : yb * s + ya * c;
     }
 }
@@ -196,6 +210,23 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
     const int k0 = c * C;
     const int h0 = 2 * kvh;
 
+    // FUSED: the raw q / k / v slices, norm weights and rope row go out first (they come from L2, the keys from HBM)
+    const int pos = n_keys - 1;
+    PostIn pin[3];
+    float4 vraw[2], rope4[4];
+    if constexpr (FUSED) {
+        post_load(pin[0], q + (size_t)h0 * D, fz.qn, j);
+        post_load(pin[1], q + (size_t)(h0 + 1) * D, fz.qn, j);
+        post_load(pin[2], q + (size_t)(fz.n_head + kvh) * D, fz.kn, j);
+        const float *vr0 = q + (size_t)(fz.n_head + n_kv + kvh) * D + 8 * j;
+        vraw[0] = *reinterpret_cast<const float4 *>(vr0);
+        vraw[1] = *reinterpret_cast<const float4 *>(vr0 + 4);
+        const float *rr = fz.rope + (size_t)pos * D + 16 * (j & 7);
+#pragma unroll
+        for (int i = 0; i < 4; i++) rope4[i] = *reinterpret_cast<const float4 *>(rr + 4 * i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
     // 0. every K and V load of the chunk (keys past n_keys read the last key and are masked)
     const _Float16 *kb = kc + (size_t)kvh * n_ctx * D, *vb = vc + (size_t)kvh * n_ctx * D;
     int4 kr[NI], vr[NI];
@@ -209,21 +240,24 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         const int key = min(k0 + kk + 16 * i, n_keys - 1);
         vr[i] = aload16(vb + (size_t)key * D + 8 * j);
     }
+    if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);  // the K / V loads are out before the arithmetic
     float qa[8], qb[8];
     int4 knew = make_int4(0, 0, 0, 0), vnew = make_int4(0, 0, 0, 0);
-    const int pos = n_keys - 1;
     if constexpr (FUSED) {
-        const float *rr = fz.rope + (size_t)pos * D;
+        float cs[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            cs[4 * i] = rope4[i].x, cs[4 * i + 1] = rope4[i].y, cs[4 * i + 2] = rope4[i].z, cs[4 * i + 3] = rope4[i].w;
+        }
         float ta[8], tb[8], kn8[8], v8[8];
-        post_slice(q + (size_t)h0 * D, fz.qn, rr, j, lane, fz.eps, ta);
-        post_slice(q + (size_t)(h0 + 1) * D, fz.qn, rr, j, lane, fz.eps, tb);
-        post_slice(q + (size_t)(fz.n_head + kvh) * D, fz.kn, rr, j, lane, fz.eps, kn8);
-        const float *vraw = q + (size_t)(fz.n_head + n_kv + kvh) * D + 8 * j;
+        post_apply(pin[0], cs, j, lane, fz.eps, ta);
+        post_apply(pin[1], cs, j, lane, fz.eps, tb);
+        post_apply(pin[2], cs, j, lane, fz.eps, kn8);
+        unpack4x2(vraw, v8);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             qa[e] = ta[e] * scale;
             qb[e] = tb[e] * scale;
-            v8[e] = vraw[e];
         }
         knew = pack8(kn8);
         vnew = pack8(v8);
@@ -347,42 +381,53 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
                  (uint32_t)(n_chunk - 1);
     __syncthreads();
     if (!s_last) return;
-    // the merge: wave w → head h0 + (w >> 1), dims (w & 1)·64 + lane. The m and l of the chunks lane, lane + 64, … go
-    // out first, then the o partials: the weights are computed while the o loads are in flight
+    // the merge: wave w → head h0 + (w >> 1), dims (w & 1)·64 + lane
     const int mh = h0 + (wave >> 1), md = (wave & 1) * 64 + lane;
     const float *ph = part + (size_t)mh * max_chunk * (D + 2);
-    float mv[MAX_CHUNKS / 64], lv[MAX_CHUNKS / 64];
+    float O = 0.0f, L;
+    if (n_chunk <= MERGE_FAST) {
+        // every load at once, branch-free (chunk indexes clamped; what lies past n_chunk gets weight 0): lane ℓ's
+        // chunk statistics (m, l of chunk ℓ) and this thread's dim of every chunk's o; the weights are worked out
+        // while the o loads are in flight
+        const int cl = min(lane, n_chunk - 1);
+        float mv = ld_dev(ph + (size_t)cl * (D + 2)), lv = ld_dev(ph + (size_t)cl * (D + 2) + 1);
+        float ov[MERGE_FAST];
 #pragma unroll
-    for (int k = 0; k < MAX_CHUNKS / 64; k++) {
-        const int cc = lane + 64 * k;
-        mv[k] = cc < n_chunk ? ld_dev(ph + (size_t)cc * (D + 2)) : -INFINITY;
-        lv[k] = cc < n_chunk ? ld_dev(ph + (size_t)cc * (D + 2) + 1) : 0.0f;
+        for (int i = 0; i < MERGE_FAST; i++) ov[i] = ld_dev(ph + (size_t)min(i, n_chunk - 1) * (D + 2) + 2 + md);
+        if (lane >= n_chunk) mv = -INFINITY, lv = 0.0f;
+        const float mx = wave_max(mv, lane);
+        const float w = expf(mv - mx);  // lanes past n_chunk: e^(−inf) = 0
+        L = wave_sum(lv * w, lane);
+        // the weights straight from the lanes that hold them (a scalar operand of the fma)
+#pragma unroll
+        for (int i = 0; i < MERGE_FAST; i++)
+            O = fmaf(ov[i], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i)), O);
+    } else {
+        // long contexts: the weights through LDS (zero past n_chunk up to a whole group), the o partials in groups of
+        // MERGE_FAST chunks, each group's loads at once
+        float mx = -INFINITY;
+        for (int cc = lane; cc < n_chunk; cc += 64) mx = fmaxf(mx, ld_dev(ph + (size_t)cc * (D + 2)));
+        mx = wave_max(mx, lane);
+        const int n_up = (n_chunk + MERGE_FAST - 1) / MERGE_FAST * MERGE_FAST;
+        float l = 0.0f;
+        for (int cc = lane; cc < n_up; cc += 64) {
+            const int cl = min(cc, n_chunk - 1);
+            const float mc = ld_dev(ph + (size_t)cl * (D + 2)), lc = ld_dev(ph + (size_t)cl * (D + 2) + 1);
+            const float w = cc < n_chunk ? expf(mc - mx) : 0.0f;
+            s_w[wave][cc] = w;
+            l = fmaf(lc, w, l);
+        }
+        L = wave_sum(l, lane);
+        __builtin_amdgcn_wave_barrier();
+        for (int c0 = 0; c0 < n_chunk; c0 += MERGE_FAST) {
+            float ov[MERGE_FAST];
+#pragma unroll
+            for (int i = 0; i < MERGE_FAST; i++)
+                ov[i] = ld_dev(ph + (size_t)min(c0 + i, n_chunk - 1) * (D + 2) + 2 + md);
+#pragma unroll
+            for (int i = 0; i < MERGE_FAST; i++) O = fmaf(ov[i], s_w[wave][c0 + i], O);
+        }
     }
-    float ov[MERGE_PREFETCH];
-#pragma unroll
-    for (int i = 0; i < MERGE_PREFETCH; i++) ov[i] = i < n_chunk ? ld_dev(ph + (size_t)i * (D + 2) + 2 + md) : 0.0f;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < MAX_CHUNKS / 64; k++) mx = fmaxf(mx, mv[k]);
-    mx = wave_max(mx, lane);
-    float L = 0.0f, w0 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < MAX_CHUNKS / 64; k++) {
-        const int cc = lane + 64 * k;
-        const float w = expf(mv[k] - mx);  // chunks past the end: e^(−inf) = 0
-        if (k == 0) w0 = w;
-        else if (cc < n_chunk) s_w[wave][cc] = w;  // chunks ≥ 64 (long contexts): through LDS
-        L = fmaf(lv[k], w, L);
-    }
-    L = wave_sum(L, lane);
-    // the first 64 chunks' weights straight from the lane that holds them (a scalar operand of the fma; LDS reads
-    // would put one LDS round trip per chunk on this dependent chain)
-    float O = 0.0f;
-#pragma unroll
-    for (int i = 0; i < MERGE_PREFETCH; i++)
-        if (i < n_chunk) O = fmaf(ov[i], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w0), i)), O);
-    __builtin_amdgcn_wave_barrier();
-    for (int cc = MERGE_PREFETCH; cc < n_chunk; cc++) O = fmaf(ld_dev(ph + (size_t)cc * (D + 2) + 2 + md), s_w[wave][cc], O);
     out[mh * D + md] = O / L;
     if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
 }

@@ -2,7 +2,7 @@
 // (text.rs:437-521), the CPU-choice step (text.rs:524-537), the GPU token choice (text.rs:165-232) and the run-ahead
 // decode (text.rs:587-625), on the kernels of q8_0.hip / attention.hip / choose.hip / gemm.hip.
 //
-// The decode step (record_step, text.rs:540-578 with layers_fused, text.rs:630-647) is 1 + 6·n_layer + 1 launches:
+// The decode step (record_step, text.rs:540-578 with layers_fused, text.rs:630-647) is 1 + 5·n_layer + 1 launches:
 //   embed → per layer: qkv matvec (attn_norm fused) → split-K attention (q/k norm, RoPE and the f16 KV store fused)
 //   (merge fused) → o matvec (+ residual) → gate/up matvec (ffn_norm + SwiGLU fused) → down matvec (+ residual)
 //   → LM head (output_norm fused) [→ token choice].
