@@ -105,7 +105,12 @@ constexpr int MERGE_FAST = 32;       // chunks merged by the branch-free path (e
 static_assert(MAX_CHUNKS % MERGE_FAST == 0, "the merge's weight groups fit s_w");
 constexpr int CNT_STRIDE = 32;       // ticket counters 128 bytes apart: the KV heads' atomics do not share a line
 
-__device__ __forceinline__ int4 aload16(const void *p) { return *reinterpret_cast<const int4 *>(p); }
+// the KV cache stream: non-temporal loads (each key / value is read once a step)
+typedef int gint4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 aload16(const void *p) {
+    const gint4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) gint4 *)(uintptr_t)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ void unpack8(const int4 w, float (&f)[8]) {
     const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
