@@ -239,10 +239,15 @@ extern "C" int htr_download(htr_device *dev, void *h_dst, const void *d_src, siz
 
 // ---- device copy (gpu.rs:2102-2110 Batch::copy → copy_words.wgsl) ---------------------------------------------------
 
-// dst[i] = src[i] over n 16-byte units (grid-stride), then the tail of < 16 bytes
+// dst[i] = src[i] over n 16-byte units (grid-stride, non-temporal: a copy touches each byte once), then the tail of
+// < 16 bytes
+typedef int gint4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_copy16(const int4 *src, int4 *dst, size_t n16, const uint8_t *src_tail,
                                                 uint8_t *dst_tail, int tail) {
-    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+    const auto *s = (const __attribute__((address_space(1))) gint4 *)(uintptr_t)src;
+    auto *d = (__attribute__((address_space(1))) gint4 *)(uintptr_t)dst;
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
     if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
 
