@@ -161,6 +161,9 @@ int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, siz
 enum { GEMM_F32 = 0, GEMM_ACC = 1, GEMM_FFN = 2 };
 int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x, int m, const htr_weight *w,
                     const htr_weight *w2, float *y, _Float16 *y16, float scale);
+// Q / K / V of one input as one GEMM over the three weights (rows a multiple of 256), three f32 outputs
+int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
+                        const htr_weight *wk, const htr_weight *wv, float *q, float *k, float *v);
 
 // the vision encoder's other kernels (vision.hip)
 int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const float *lut, int w, int px, int n,

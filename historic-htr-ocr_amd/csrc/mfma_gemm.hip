@@ -1,18 +1,30 @@
 // The vision encoder's GEMMs on gfx950's matrix cores: Y[M,N] (+)= X[M,K] · W[N,K]ᵀ with X and W f16 in memory and
-// f32 accumulation, and the fused FFN first half G = silu(X·Wgᵀ) · (X·Wuᵀ) · scale → f16.
+// f32 accumulation, the fused FFN first half G = silu(X·Wgᵀ) · (X·Wuᵀ) · scale → f16, and Q / K / V as one GEMM over
+// the three weights.
 //
 // Reference semantics: matmul_coopd.wgsl (Batch::matmul_f16x, gpu.rs:2019-2042) and ffn_coopd.wgsl (Batch::ffn_f16,
 // gpu.rs:2048-2086; out_scale = 1/64, vision.rs:31-35). The schedule is this library's own:
 //
-//   tile      a 256-thread workgroup owns a 128 × 128 output tile; its 4 waves own 64 × 64 each, as 2 × 2
-//             v_mfma_f32_32x32x16_f16 tiles (lane layouts checked on the GPU: A lane ℓ holds A[ℓ%32][8(ℓ/32) …+7],
-//             B lane ℓ holds B[8(ℓ/32) …+7][ℓ%32], D lane ℓ register r is row 8(r/4) + 4(ℓ/32) + r%4, column ℓ%32);
-//   K         in steps of 32 through LDS, double-buffered: the next step's global loads (16 B a lane) are in flight
-//             while the current one feeds the matrix cores; one workgroup barrier per step. LDS rows are padded to
-//             80 bytes so the fragment reads (16 B a lane, 32 rows) fall on distinct banks;
-//   order     the tiles are dealt to the 8 XCDs in contiguous bands (workgroup b runs on XCD b mod 8), so an XCD's
-//             L2 keeps a band of X rows and the W tiles they meet;
-//   rows      rows past M read row M−1 and are not stored (no padding required of the caller).
+//   tile      a 512-thread workgroup (8 waves) owns a 256 × 256 tile of X rows × W rows; wave (wm, wn) of 2 × 4 owns
+//             128 × 64 of it as 4 × 2 v_mfma_f32_32x32x16_f16 tiles (lane layouts checked on the GPU: A lane ℓ holds
+//             A[ℓ%32][8(ℓ/32) …+7], B lane ℓ holds B[8(ℓ/32) …+7][ℓ%32], D lane ℓ register r is row 8(r/4) + 4(ℓ/32)
+//             + r%4, column ℓ%32). The FFN's W tile is 128 gate rows and the same 128 up rows in alternating blocks
+//             of 32, so a wave's two column tiles are one gate and one up tile of the same outputs;
+//   K         in stages of 32 through a ring of 4 LDS stages (32 KB each) filled by direct-to-LDS loads
+//             (global_load_lds_dwordx4): the stage 3 ahead is loading while one is computed. Inside a stage a row's
+//             four 16-byte chunks sit at chunk ^ (row/4 % 4): 16 consecutive rows of one chunk fall on 16 different
+//             16-byte bank groups (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes);
+//   pipeline  the fragments of stage kt are read from LDS during stage kt − 1; stage kt runs its first 8 MFMAs, then
+//             waits for stage kt + 1 and the workgroup barrier while they drain, issues the loads of stage kt + 3
+//             and the fragment reads of stage kt + 1, then its last 8 MFMAs. Waits are explicit s_waitcnt vmcnt
+//             (the LDS loads' completion) and a bare s_barrier (no fence that would wait for the stages in flight);
+//   order     tiles are dealt to the 8 XCDs in contiguous bands (workgroup b runs on XCD b mod 8); inside a band
+//             groups of 4 tile rows are walked column by column, so the workgroups resident on an XCD share both
+//             their X rows and their W rows in its L2;
+//   edges     rows past M read row M − 1 and are not stored; a last tile past N (N an odd multiple of 128) reads its
+//             W rows clamped and stores nothing there. K/32 may be odd.
+// Measured at M = 12100 on one MI355X: 886 TFLOP/s at N = 8192, K = 1024 and 898 at N = 1024, K = 4096, against
+// ≈ 2.0 PFLOP/s sustained by MFMAs from registers (the earlier 128 × 128, one-stage-ahead kernel: 374 – 641).
 #include "htr_internal.h"
 
 namespace {
@@ -20,138 +32,186 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int GW = 256;
-constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int LDK = BK + 8;  // LDS row stride in halves (80 bytes)
+constexpr int GW = 512, NW = GW / 64;   // threads, waves
+constexpr int BM = 256, BN = 256;        // tile: X rows × W rows
+constexpr int WM = 2, WN = 4;            // wave grid
+constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles a wave: 4 × 2
+constexpr int ST = 4;                    // LDS stages of 32 K each
+constexpr int ACH = BM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
+constexpr int AI = ACH / GW, BI = BCH / GW;                 // direct-to-LDS loads a wave a stage
+constexpr int GROUP = 4;                 // tile rows walked together
 constexpr int XCDS = 8;
+constexpr int MAX_W = 3;
 
 struct GemmK {
-    const _Float16 *x;   // [M][K]
-    const _Float16 *w;   // [N][K]
-    const _Float16 *w2;  // FFN: up [N][K]
-    float *y;            // [M][N] f32 (F32 / ACC)
-    _Float16 *y16;       // FFN: [M][N] f16
-    int m, n, k;
-    float scale;  // FFN output scale
+    const _Float16 *x;          // [M][K]
+    const _Float16 *w[MAX_W];   // F32 / ACC: W split in n_w equal row blocks; FFN: gate, up
+    int n_w, rows_w;            // weights, rows of each
+    float *y[MAX_W];            // F32 / ACC: [M][rows_w] each (the output columns of weight i)
+    _Float16 *y16;              // FFN: [M][rows_w] f16
+    int m, k;
+    float scale;                // FFN output scale
     int tiles_m, tiles_n;
 };
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// the tile of workgroup b: XCD x = b mod 8 takes the x-th contiguous band of tiles (row-major over (m, n))
-__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int &tm, int &tn) {
-    const int total = tiles_m * tiles_n;
-    const int xcd = b % XCDS, i = b / XCDS;
-    const int per = total / XCDS, extra = total % XCDS;
-    const int t = xcd * per + min(xcd, extra) + i;
-    tm = t / tiles_n;
-    tn = t - tm * tiles_n;
-}
+// the 16-byte chunk slot of (row r, chunk c) in a stage region
+__device__ __forceinline__ int chunk_slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
 
 template <int EPI> __global__ __launch_bounds__(GW) void k_gemm_f16(const GemmK a) {
-    constexpr int NB = EPI == GEMM_FFN ? 2 : 1;  // weight matrices
-    __shared__ __attribute__((aligned(16))) _Float16 s_a[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[2][NB][BN * LDK];
+    __shared__ __attribute__((aligned(16))) int4 s_t[ST * SCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
+    // tile: XCD band, then groups of GROUP tile rows walked column by column
     int tm, tn;
-    tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-    const int row0 = tm * BM, col0 = tn * BN;
-    const int k = a.k, nk = k / BK;
-
-    // global → registers: thread t moves the 16-byte chunks (row t/4 + 64·i, chunk t%4) of the A and B tiles
-    const int lr = tid >> 2, lc = tid & 3;
-    const size_t xo0 = (size_t)min(row0 + lr, a.m - 1) * k + 8 * lc;
-    const size_t xo1 = (size_t)min(row0 + lr + 64, a.m - 1) * k + 8 * lc;
-    const size_t wo0 = (size_t)(col0 + lr) * k + 8 * lc;
-    const size_t wo1 = (size_t)(col0 + lr + 64) * k + 8 * lc;
-    int4 ra0, ra1, rb0[NB], rb1[NB];
-#define HTR_GEMM_LOAD(kt)                                                                                              \
-    {                                                                                                                  \
-        const size_t kk_ = (size_t)(kt) * BK;                                                                          \
-        ra0 = *reinterpret_cast<const int4 *>(a.x + xo0 + kk_);                                                        \
-        ra1 = *reinterpret_cast<const int4 *>(a.x + xo1 + kk_);                                                        \
-        rb0[0] = *reinterpret_cast<const int4 *>(a.w + wo0 + kk_);                                                     \
-        rb1[0] = *reinterpret_cast<const int4 *>(a.w + wo1 + kk_);                                                     \
-        if (NB == 2) {                                                                                                 \
-            rb0[NB - 1] = *reinterpret_cast<const int4 *>(a.w2 + wo0 + kk_);                                           \
-            rb1[NB - 1] = *reinterpret_cast<const int4 *>(a.w2 + wo1 + kk_);                                           \
-        }                                                                                                              \
+    {
+        const int total = a.tiles_m * a.tiles_n, b = blockIdx.x, xcd = b % XCDS, i = b / XCDS;
+        const int per = total / XCDS, extra = total % XCDS;
+        const int t = xcd * per + min(xcd, extra) + i;
+        const int gsz = GROUP * a.tiles_n, g = t / gsz, gr = t % gsz, gm = min(GROUP, a.tiles_m - g * GROUP);
+        tm = g * GROUP + gr % gm;
+        tn = gr / gm;
     }
-#define HTR_GEMM_STORE(buf)                                                                                            \
-    {                                                                                                                  \
-        *reinterpret_cast<int4 *>(&s_a[buf][lr * LDK + 8 * lc]) = ra0;                                                 \
-        *reinterpret_cast<int4 *>(&s_a[buf][(lr + 64) * LDK + 8 * lc]) = ra1;                                          \
-        _Pragma("unroll") for (int t = 0; t < NB; t++) {                                                               \
-            *reinterpret_cast<int4 *>(&s_b[buf][t][lr * LDK + 8 * lc]) = rb0[t];                                       \
-            *reinterpret_cast<int4 *>(&s_b[buf][t][(lr + 64) * LDK + 8 * lc]) = rb1[t];                                \
-        }                                                                                                              \
-    }
-
-    f32x16 acc[NB][2][2];
-#pragma unroll
-    for (int t = 0; t < NB; t++)
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[t][i][j][r] = 0.0f;
-
-    HTR_GEMM_LOAD(0)
-    HTR_GEMM_STORE(0)
-    __syncthreads();
-    const int fr = lane & 31, fk = 8 * (lane >> 5);  // fragment row within a 32-block, k offset
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) HTR_GEMM_LOAD(kt + 1)
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ks++) {
-            half8 af[2], bf[NB][2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                af[i] = *reinterpret_cast<const half8 *>(&s_a[cur][(wm * 64 + 32 * i + fr) * LDK + 16 * ks + fk]);
-#pragma unroll
-            for (int t = 0; t < NB; t++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    bf[t][j] =
-                        *reinterpret_cast<const half8 *>(&s_b[cur][t][(wn * 64 + 32 * j + fr) * LDK + 16 * ks + fk]);
-#pragma unroll
-            for (int t = 0; t < NB; t++)
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[t][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[t][j], acc[t][i][j], 0, 0, 0);
+    const int row0 = tm * BM, k = a.k, nk = k / 32, m = a.m;
+    // the W rows of tile row r (0 … BN−1): F32 / ACC the tile's rows of the stacked weights (one weight a tile, the
+    // last tile past the end clamped); FFN blocks of 32 alternating gate / up rows of the tile's 128 outputs
+    const int8_t wsel = EPI == GEMM_FFN ? 0 : (int8_t)min((tn * BN) / a.rows_w, a.n_w - 1);
+    const _Float16 *wbase = a.w[wsel];
+    const int wrow0 = EPI == GEMM_FFN ? tn * (BN / 2) : tn * BN - wsel * a.rows_w;
+    auto w_row = [&](int r, const _Float16 *&base) -> int {
+        if (EPI == GEMM_FFN) {
+            base = (r >> 5) & 1 ? a.w[1] : a.w[0];
+            return wrow0 + (r >> 6) * 32 + (r & 31);
         }
-        if (kt + 1 < nk) HTR_GEMM_STORE(cur ^ 1)
-        __syncthreads();
+        base = wbase;
+        return min(wrow0 + r, a.rows_w - 1);
+    };
+    auto issue = [&](int ks, int buf) {
+        const size_t kk = (size_t)min(ks, nk - 1) * 32;
+#pragma unroll
+        for (int i = 0; i < AI; i++) {
+            const int s = 64 * (wave + NW * i) + lane, r = s >> 2, c = (s & 3) ^ ((r >> 2) & 3);
+            __builtin_amdgcn_global_load_lds((const void *)(a.x + (size_t)min(row0 + r, m - 1) * k + kk + 8 * c),
+                                             (void __attribute__((address_space(3))) *)&s_t[buf * SCH + 64 * (wave + NW * i)],
+                                             16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BI; i++) {
+            const int s = 64 * (wave + NW * i) + lane, r = s >> 2, c = (s & 3) ^ ((r >> 2) & 3);
+            const _Float16 *base;
+            const int wr = w_row(r, base);
+            __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)wr * k + kk + 8 * c),
+                                             (void __attribute__((address_space(3))) *)&s_t[buf * SCH + ACH + 64 * (wave + NW * i)],
+                                             16, 0, 0);
+        }
+    };
+    // the lane's fragment slots: A tile i, B tile j, k half h (chunk 2h + lane/32 of row … + lane%32)
+    int ao[TM][2], bo[TN][2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) ao[i][h] = chunk_slot(wm * TM * 32 + 32 * i + (lane & 31), 2 * h + (lane >> 5));
+#pragma unroll
+        for (int j = 0; j < TN; j++) bo[j][h] = ACH + chunk_slot(wn * TN * 32 + 32 * j + (lane & 31), 2 * h + (lane >> 5));
     }
-
-#undef HTR_GEMM_LOAD
-#undef HTR_GEMM_STORE
+    struct Frag {
+        half8 a[2][TM], b[2][TN];
+    };
+    auto read = [&](Frag &f, int stage) {
+        const int4 *st = s_t + (stage % ST) * SCH;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) f.a[h][i] = *reinterpret_cast<const half8 *>(st + ao[i][h]);
+#pragma unroll
+            for (int j = 0; j < TN; j++) f.b[h][j] = *reinterpret_cast<const half8 *>(st + bo[j][h]);
+        }
+    };
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    auto mfma_half = [&](const Frag &f, int h) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+    };
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++) issue(s, s);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((ST - 2) * (AI + BI)) : "memory");  // stage 0 is in
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    Frag f0, f1;
+    read(f0, 0);
+    // one stage: cur holds its fragments; nxt receives stage kt + 1's. The stages in flight at the wait are kt + 1 …
+    // kt + ST − 2 (the one to wait for and ST − 3 later ones); the buffer refilled after the barrier held stage kt − 1,
+    // which every wave finished reading in the stage before
+    auto step = [&](Frag &cur, Frag &nxt, int kt) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(cur, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((ST - 3) * (AI + BI)) : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(kt + ST - 1, (kt + ST - 1) % ST);
+        read(nxt, kt + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(cur, 1);
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        step(f0, f1, kt);
+        step(f1, f0, kt + 1);
+    }
+    if (kt < nk) step(f0, f1, kt);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS load left in flight when the wave ends
 
     // epilogue: lane ℓ, register r → row 8(r/4) + 4(ℓ/32) + r%4, column ℓ%32 of each 32 × 32 tile
+    if (EPI == GEMM_FFN) {
+        const int col = tn * (BN / 2) + wn * 32 + (lane & 31);  // gate tile j = 0, up tile j = 1
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = col0 + wn * 64 + 32 * j + (lane & 31);
+        for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = row0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= a.m) continue;
-                const size_t o = (size_t)row * a.n + col;
-                if (EPI == GEMM_F32) a.y[o] = acc[0][i][j][r];
-                if (EPI == GEMM_ACC) a.y[o] = a.y[o] + acc[0][i][j][r];
-                if (EPI == GEMM_FFN) {
-                    const float g = acc[0][i][j][r], u = acc[NB - 1][i][j][r];
-                    a.y16[o] = (_Float16)(silu(g) * u * a.scale);
-                }
+                const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < m) a.y16[(size_t)row * a.rows_w + col] = (_Float16)(silu(acc[i][0][r]) * acc[i][1][r] * a.scale);
             }
-        }
+        return;
     }
+    float *y = a.y[wsel];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int col = wrow0 + wn * TN * 32 + 32 * j + (lane & 31);
+        if (col >= a.rows_w) continue;  // the part of a last tile past N
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row >= m) continue;
+                float *o = y + (size_t)row * a.rows_w + col;
+                *o = EPI == GEMM_ACC ? *o + acc[i][j][r] : acc[i][j][r];
+            }
+    }
+}
+
+int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
+    a.tiles_m = (a.m + BM - 1) / BM;
+    a.tiles_n = epi == GEMM_FFN ? a.rows_w / (BN / 2) : (a.n_w * a.rows_w + BN - 1) / BN;
+    const dim3 grid(a.tiles_m * a.tiles_n);
+    switch (epi) {
+    case GEMM_F32: hipLaunchKernelGGL(k_gemm_f16<GEMM_F32>, grid, dim3(GW), 0, st, a); break;
+    case GEMM_ACC: hipLaunchKernelGGL(k_gemm_f16<GEMM_ACC>, grid, dim3(GW), 0, st, a); break;
+    case GEMM_FFN: hipLaunchKernelGGL(k_gemm_f16<GEMM_FFN>, grid, dim3(GW), 0, st, a); break;
+    default: return htr_fail("gemm_f16: epilogue %d", epi);
+    }
+    return htr_launched(dev, "k_gemm_f16");
 }
 
 }  // namespace
@@ -161,30 +221,48 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
     if (!w || !w->h) return htr_fail("gemm_f16: the weight has no f16 plane (htr_weight_q8_0_f16)");
     const int n = (int)w->rows, k = (int)w->cols;
     if (m < 1) return htr_fail("gemm_f16: %d rows", m);
-    if (n % BN || k % BK)
-        return htr_fail("gemm_f16: W [%d x %d]: rows a multiple of %d, columns a multiple of %d", n, k, BN, BK);
+    if (n % 128 || k % 32)
+        return htr_fail("gemm_f16: W [%d x %d]: rows a multiple of 128, columns a multiple of 32", n, k);
     if (epi == GEMM_FFN && (!w2 || !w2->h || (int)w2->rows != n || (int)w2->cols != k))
         return htr_fail("gemm_f16: the FFN's up weight must match the gate weight [%d x %d]", n, k);
     GemmK a{};
     a.x = x;
-    a.w = w->h;
-    a.w2 = epi == GEMM_FFN ? w2->h : nullptr;
-    a.y = y;
+    a.w[0] = w->h;
+    a.w[1] = epi == GEMM_FFN ? w2->h : w->h;
+    a.w[2] = w->h;
+    a.n_w = 1;
+    a.rows_w = n;
+    a.y[0] = a.y[1] = a.y[2] = y;
     a.y16 = y16;
     a.m = m;
-    a.n = n;
     a.k = k;
     a.scale = scale;
-    a.tiles_m = (m + BM - 1) / BM;
-    a.tiles_n = n / BN;
-    const dim3 grid(a.tiles_m * a.tiles_n);
-    switch (epi) {
-    case GEMM_F32: hipLaunchKernelGGL(k_gemm_f16<GEMM_F32>, grid, dim3(GW), 0, st, a); break;
-    case GEMM_ACC: hipLaunchKernelGGL(k_gemm_f16<GEMM_ACC>, grid, dim3(GW), 0, st, a); break;
-    case GEMM_FFN: hipLaunchKernelGGL(k_gemm_f16<GEMM_FFN>, grid, dim3(GW), 0, st, a); break;
-    default: return htr_fail("gemm_f16: epilogue %d", epi);
-    }
-    return htr_launched(dev, "k_gemm_f16");
+    return launch(dev, st, epi, a);
+}
+
+int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
+                        const htr_weight *wk, const htr_weight *wv, float *q, float *kk, float *v) {
+    const htr_weight *ws[3] = {wq, wk, wv};
+    for (const htr_weight *w : ws)
+        if (!w || !w->h) return htr_fail("gemm_f16_qkv: a weight has no f16 plane (htr_weight_q8_0_f16)");
+    const int n = (int)wq->rows, k = (int)wq->cols;
+    if (m < 1) return htr_fail("gemm_f16_qkv: %d rows", m);
+    if (n % BN || k % 32 || (int)wk->rows != n || (int)wv->rows != n || (int)wk->cols != k || (int)wv->cols != k)
+        return htr_fail("gemm_f16_qkv: three W [%d x %d], rows a multiple of %d, columns of 32", n, k, BN);
+    GemmK a{};
+    a.x = x;
+    a.w[0] = wq->h;
+    a.w[1] = wk->h;
+    a.w[2] = wv->h;
+    a.n_w = 3;
+    a.rows_w = n;
+    a.y[0] = q;
+    a.y[1] = kk;
+    a.y[2] = v;
+    a.m = m;
+    a.k = k;
+    a.scale = 1.0f;
+    return launch(dev, st, GEMM_F32, a);
 }
 
 // ---- ABI ------------------------------------------------------------------------------------------------------------

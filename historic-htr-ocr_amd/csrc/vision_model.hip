@@ -222,9 +222,13 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
     for (int li = 0; li < nl; li++) {
         const VLayer &l = v->layers[li];
         HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln1, v->h16, n, d, c.eps));
-        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.q, nullptr, v->q, nullptr, 1.0f));
-        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.k, nullptr, v->k, nullptr, 1.0f));
-        HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
+        if (c.dim % 256 == 0) {
+            HTR_TRY(launch_gemm_f16_qkv(dev, st, v->h16, n, l.q, l.k, l.v, v->q, v->k, v->v));
+        } else {
+            HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.q, nullptr, v->q, nullptr, 1.0f));
+            HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.k, nullptr, v->k, nullptr, 1.0f));
+            HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
+        }
         HTR_TRY(launch_rope2d(dev, st, v->q, v->cs, n, c.n_head, c.d_head, px, max_pos));
         HTR_TRY(launch_rope2d(dev, st, v->k, v->cs, n, c.n_head, c.d_head, px, max_pos));
         HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kv, n, c.n_head));
