@@ -437,61 +437,111 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
     if (tid == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
 }
 
-// ---- prefill causal attention --------------------------------------------------------------------------------------
+// ---- prefill causal attention ----------------------------------------------------------------------------------------
 //
-// grid (⌈n_q/64⌉, n_head), 128 threads = 64 queries × 2 halves of the head dim (adjacent lanes). K / V tiles of 32 keys
-// are staged in LDS as f32; online softmax per query (f32).
-constexpr int CQ = 64, CT = 32;
+// attention_causal.wgsl's arithmetic (text.rs:484-499, the F32 path): q·scale, f32 scores, an online softmax in f32,
+// out = O / l — on the f32 matrix cores (v_mfma_f32_16x16x4f32: f32 products and sums in the matrix unit's order).
+// grid (⌈n_q/32⌉, n_kv), 256 threads = 4 waves: wave w takes q head 2·kvh + (w & 1) (GQA group 2) and the 16 queries
+// 32·x + 16·(w >> 1) …; both heads share the KV head's keys. Keys in stages of 32 through LDS (K [32][128 + 8] f16,
+// Vᵀ [128][32 + 4] f16: padded rows, so 16 lanes' reads fall on distinct banks), each stage as two blocks of 16.
+// Per block, Sᵀ (16 keys × 16 queries) = K·(q·scale)ᵀ is 32 MFMAs over the 128 dims (lane group g = ℓ/16 takes dims
+// 32g …), leaving lane ℓ = 16g + c the scores of keys 4g … 4g + 3 for query c (its partners across lane bits 4 and 5
+// hold the rest); masked keys (after the query) are −inf, the running max starts at −3e38. Oᵀ (128 dims × 16 queries)
+// += Vᵀ·Pᵀ is 32 more, lane ℓ accumulating dims 16t + 4g … of query c, so the rescale stays in the lane.
+constexpr int PQ = 32, PK = 32, KS = D + 8, VS = PK + 4;
 
-__global__ __launch_bounds__(128) void k_attn_causal(const float *q, const _Float16 *kc, const _Float16 *vc, int n_q,
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_attn_causal(const float *q, const _Float16 *kc, const _Float16 *vc, int n_q,
                                                      int pos0, int n_head, int n_kv, int n_ctx, float scale,
                                                      float *out) {
-    __shared__ float s_k[CT][D];
-    __shared__ float s_v[CT][D];
-    const int h = blockIdx.y, kvh = h / (n_head / n_kv);
-    const int tid = threadIdx.x, ql = tid >> 1, half = tid & 1;
-    const int qi_raw = blockIdx.x * CQ + ql;
-    const int qi = min(qi_raw, n_q - 1);
+    __shared__ __attribute__((aligned(16))) _Float16 s_k[PK * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 s_vt[D * VS];
+    const int kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = 2 * kvh + (wave & 1);
+    const int q0 = blockIdx.x * PQ + 16 * (wave >> 1);
+    const int g = lane >> 4, c = lane & 15;
+    const int qi = min(q0 + c, n_q - 1);
     const int qpos = pos0 + qi;
-    const int last_q = min(blockIdx.x * CQ + CQ - 1, n_q - 1);
-    const int kend = pos0 + last_q + 1;
-    float qv[64], acc[64];
-    const float *qr = q + ((size_t)qi * n_head + h) * D + half * 64;
+    const int wlast = pos0 + min(q0 + 15, n_q - 1);                  // the wave's last query position
+    const int glast = pos0 + min((int)blockIdx.x * PQ + PQ - 1, n_q - 1);  // the workgroup's
+    // the B operand of Sᵀ at MFMA step s: q[query c][dim 32g + s]·scale
+    float qf[32];
+    {
+        const float4 *qr = reinterpret_cast<const float4 *>(q + ((size_t)qi * n_head + h) * D + 32 * g);
 #pragma unroll
-    for (int i = 0; i < 64; i++) {
-        qv[i] = qr[i] * scale;
-        acc[i] = 0.0f;
+        for (int i = 0; i < 8; i++) {
+            const float4 v = qr[i];
+            qf[4 * i] = v.x * scale, qf[4 * i + 1] = v.y * scale, qf[4 * i + 2] = v.z * scale, qf[4 * i + 3] = v.w * scale;
+        }
     }
-    float m = -INFINITY, l = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -3.0e38f, l = 0.0f;
     const _Float16 *kb = kc + (size_t)kvh * n_ctx * D, *vb = vc + (size_t)kvh * n_ctx * D;
-    for (int k0 = 0; k0 < kend; k0 += CT) {
-        __syncthreads();
-        for (int e = tid; e < CT * D; e += 128) {
-            const int t = e / D, d = e % D;
-            const int kj = min(k0 + t, kend - 1);
-            s_k[t][d] = (float)kb[(size_t)kj * D + d];
-            s_v[t][d] = (float)vb[(size_t)kj * D + d];
+    const int n_stage = glast / PK + 1;
+    for (int st = 0; st < n_stage; st++) {
+        const int k0 = st * PK;
+        __syncthreads();  // the previous stage is no longer read
+        // K and V of keys k0 … k0 + 31 (past the workgroup's last query: its row, masked): 512 chunks of 16 bytes
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
+            const size_t key = (size_t)min(k0 + r, glast);
+            const int4 kv = *reinterpret_cast<const int4 *>(kb + key * D + 8 * cc);
+            const half8 vv = *reinterpret_cast<const half8 *>(vb + key * D + 8 * cc);
+            *reinterpret_cast<int4 *>(s_k + r * KS + 8 * cc) = kv;
+#pragma unroll
+            for (int e = 0; e < 8; e++) s_vt[(8 * cc + e) * VS + r] = vv[e];
         }
         __syncthreads();
-        const int nk = min(CT, max(0, qpos + 1 - k0));
-        for (int t = 0; t < nk; t++) {
-            float dp = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 64; i++) dp = fmaf(qv[i], s_k[t][half * 64 + i], dp);
-            const float sc = dp + __shfl_xor(dp, 1, 64);
-            const float mn = fmaxf(m, sc);
-            const float corr = expf(m - mn), p = expf(sc - mn);
-            l = fmaf(l, corr, p);
+        for (int sb = 0; sb < 2; sb++) {
+            const int kb0 = k0 + 16 * sb;
+            if (kb0 > wlast) break;  // no key of this block is visible to the wave's queries (uniform)
+            f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const _Float16 *krow = s_k + (16 * sb + c) * KS + 32 * g;
 #pragma unroll
-            for (int i = 0; i < 64; i++) acc[i] = fmaf(p, s_v[t][half * 64 + i], acc[i] * corr);
-            m = mn;
+            for (int s4 = 0; s4 < 4; s4++) {
+                const half8 kh = *reinterpret_cast<const half8 *>(krow + 8 * s4);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kh[e], qf[8 * s4 + e], sacc, 0, 0, 0);
+            }
+            float sv[4], mx = m;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sv[i] = kb0 + 4 * g + i <= qpos ? sacc[i] : -INFINITY;
+                mx = fmaxf(mx, sv[i]);
+            }
+            mx = pair_max<32>(pair_max<16>(mx));
+            const float corr = expf(m - mx);
+            float p[4], ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = expf(sv[i] - mx);  // masked: e^(−inf) = 0
+                ps += p[i];
+            }
+            l = l * corr + pair_sum<32>(pair_sum<16>(ps));
+            m = mx;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const half4 vt = *reinterpret_cast<const half4 *>(s_vt + (16 * t + c) * VS + 16 * sb + 4 * g);
+                o[t] *= corr;
+#pragma unroll
+                for (int s = 0; s < 4; s++) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vt[s], p[s], o[t], 0, 0, 0);
+            }
         }
     }
-    if (qi_raw < n_q) {
+    if (q0 + c < n_q) {
         const float inv = 1.0f / l;
-        float *o = out + ((size_t)qi * n_head + h) * D + half * 64;
+        float *orow = out + ((size_t)(q0 + c) * n_head + h) * D + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 64; i++) o[i] = acc[i] * inv;
+        for (int t = 0; t < 8; t++)
+            *reinterpret_cast<float4 *>(orow + 16 * t) = make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
     }
 }
 
@@ -564,7 +614,10 @@ int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k
 
 int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out) {
-    hipLaunchKernelGGL(k_attn_causal, dim3((n_q + CQ - 1) / CQ, n_head), dim3(128), 0, st, q, (const _Float16 *)kc,
+    if (n_head != 2 * n_kv) return htr_fail("causal attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
+    if (n_q < 1 || pos0 < 0 || pos0 + n_q > n_ctx)
+        return htr_fail("causal attention: %d queries from position %d in a %d-row cache", n_q, pos0, n_ctx);
+    hipLaunchKernelGGL(k_attn_causal, dim3((n_q + PQ - 1) / PQ, n_kv), dim3(256), 0, st, q, (const _Float16 *)kc,
                        (const _Float16 *)vc, n_q, pos0, n_head, n_kv, n_ctx, scale, out);
     return htr_launched(dev, "k_attn_causal");
 }

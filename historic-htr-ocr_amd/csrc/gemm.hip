@@ -3,8 +3,14 @@
 // Reference semantics: matmul.wgsl:47-91 (F32 path: W dequantised exactly — q·d is exact in f32 — and f32 fma
 // accumulation; acc = 1 adds onto Y, the residual stream), rms_norm.wgsl:21-41, swiglu.wgsl:18-24 (text.rs:484-518).
 //
-// The GEMM: 64×64 output tiles, 256 threads with 4×4 outputs each, K in steps of 32 = one q8_0 block, so a tile's
-// column needs one scale; X and the dequantised W tile are staged in LDS as f32.
+// The GEMM on the matrix cores (k_gemm_q8_0_mfma; N a multiple of 64): v_mfma_f32_32x32x2_f32 keeps the F32 path's
+// f32 products and sums (the order is the matrix unit's). 64×64 output tiles (M is the prompt length, ~1000, so small
+// tiles keep 256+ workgroups busy), 4 waves of one 32×32 MFMA tile each, K in steps of 32 = one q8_0 block: X and the
+// exactly dequantised W tile are staged in LDS as f32 (double-buffered, the next step's global loads in flight),
+// 16-byte chunks placed at chunk ^ (row/2 % 8) so 16 lanes' 16-byte reads fall on 16 bank groups. Lane half h takes
+// the 16 consecutive k of 16h … 16h + 15 over the step's 16 MFMAs (k-slot h of each), so a lane's fragments are 4
+// contiguous 16-byte reads. Measured (1023 rows): see the bench's prefill. Other shapes: k_gemm_q8_0_f32, 64×64
+// tiles, 256 threads with 4×4 outputs each in f32 fma.
 #include "htr_internal.h"
 
 namespace {
@@ -88,12 +94,86 @@ __global__ __launch_bounds__(256) void k_swiglu(float *g, const float *u, size_t
     }
 }
 
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int mf_slot(int r, int q) { return 8 * r + (q ^ ((r >> 1) & 7)); }
+
+__global__ __launch_bounds__(256) void k_gemm_q8_0_mfma(const float *x, const int8_t *wq, const _Float16 *wd, float *y,
+                                                        int m, int n, int k, int acc) {
+    __shared__ __attribute__((aligned(16))) float4 s_a[2][64 * 8];  // [row][chunk] f32, 8 KB a buffer
+    __shared__ __attribute__((aligned(16))) float4 s_b[2][64 * 8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
+    const int nb = k / 32;
+    // staging: thread t moves row t/4, k 8·(t%4) … + 7 of the X tile and of the W tile
+    const int lr = tid >> 2, lq = tid & 3;
+    const float *xr = x + (size_t)min(row0 + lr, m - 1) * k + 8 * lq;
+    const int8_t *wr = wq + (size_t)(col0 + lr) * k + 8 * lq;
+    const _Float16 *dr = wd + (size_t)(col0 + lr) * nb;
+    float4 ra0, ra1;
+    int2 rq;
+    float rd;
+    auto gload = [&](int kb) {
+        const float4 *xs = reinterpret_cast<const float4 *>(xr + 32 * kb);
+        ra0 = xs[0];
+        ra1 = xs[1];
+        rq = *reinterpret_cast<const int2 *>(wr + 32 * kb);
+        rd = (float)dr[kb];
+    };
+    auto lstore = [&](int buf) {
+        s_a[buf][mf_slot(lr, 2 * lq)] = ra0;
+        s_a[buf][mf_slot(lr, 2 * lq + 1)] = ra1;
+        const uint32_t u0 = (uint32_t)rq.x, u1 = (uint32_t)rq.y;
+        s_b[buf][mf_slot(lr, 2 * lq)] = make_float4((float)(int8_t)u0 * rd, (float)(int8_t)(u0 >> 8) * rd,
+                                                    (float)(int8_t)(u0 >> 16) * rd, (float)(int8_t)(u0 >> 24) * rd);
+        s_b[buf][mf_slot(lr, 2 * lq + 1)] = make_float4((float)(int8_t)u1 * rd, (float)(int8_t)(u1 >> 8) * rd,
+                                                        (float)(int8_t)(u1 >> 16) * rd, (float)(int8_t)(u1 >> 24) * rd);
+    };
+    f32x16 c;
+#pragma unroll
+    for (int r = 0; r < 16; r++) c[r] = 0.0f;
+    const int fr_a = wm * 32 + (lane & 31), fr_b = wn * 32 + (lane & 31), h = lane >> 5;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < nb; kb++) {
+        const int cur = kb & 1;
+        if (kb + 1 < nb) gload(kb + 1);
+        float a[16], b[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 va = s_a[cur][mf_slot(fr_a, 4 * h + q)], vb = s_b[cur][mf_slot(fr_b, 4 * h + q)];
+            a[4 * q] = va.x, a[4 * q + 1] = va.y, a[4 * q + 2] = va.z, a[4 * q + 3] = va.w;
+            b[4 * q] = vb.x, b[4 * q + 1] = vb.y, b[4 * q + 2] = vb.z, b[4 * q + 3] = vb.w;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 16; s2++) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s2], b[s2], c, 0, 0, 0);
+        if (kb + 1 < nb) lstore(cur ^ 1);
+        __syncthreads();
+    }
+    const int col = col0 + wn * 32 + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int row = row0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= m) continue;
+        float *o = y + (size_t)row * n + col;
+        *o = acc ? *o + c[r] : c[r];
+    }
+}
+
 }  // namespace
 
 int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
                          int acc) {
     if (!w->q) return htr_fail("gemm: weight has no q8_0 planes");
     dim3 grid(((int)w->rows + BN - 1) / BN, (m + BM - 1) / BM);
+    if (w->rows % 64 == 0 && w->cols % 32 == 0) {
+        hipLaunchKernelGGL(k_gemm_q8_0_mfma, grid, dim3(256), 0, st, x, w->q, w->d, y, m, (int)w->rows, (int)w->cols,
+                           acc);
+        return htr_launched(dev, "k_gemm_q8_0_mfma");
+    }
     hipLaunchKernelGGL(k_gemm_q8_0_f32, grid, dim3(256), 0, st, x, w->q, w->d, y, m, (int)w->rows, (int)w->cols, acc);
     return htr_launched(dev, "k_gemm_q8_0_f32");
 }

@@ -78,11 +78,12 @@ __device__ __forceinline__ int vt_key(int slot) {
 }
 
 // K / V of one head in blocks of 32 keys, 8 KB a block: K [32 keys][64 dims] then Vᵀ [64 dims][32 slots], f16, in
-// 16-byte chunks placed so that the attention's fragment reads from LDS hit 8 different bank groups in every 8 lanes:
-// K row r, chunk j (dims 8j …) at chunk r·8 + (j ^ (r % 8)); Vᵀ row d, chunk q (slots 8q …) at 256 + d·4 + (q ^ (d/2 % 4))
+// 16-byte chunks placed so that the attention's fragment reads from LDS hit 16 different 16-byte bank groups in every
+// 16 lanes (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes): K row r, chunk j (dims 8j …) at
+// chunk r·8 + (j ^ (r/2 % 8)); Vᵀ row d, chunk q (slots 8q …) at 256 + d·4 + (q ^ (d/4 % 4))
 constexpr int KVB = 8192;
-__device__ __forceinline__ int kv_kchunk(int r, int j) { return r * 8 + (j ^ (r & 7)); }
-__device__ __forceinline__ int kv_vchunk(int d, int q) { return 256 + d * 4 + (q ^ ((d >> 1) & 3)); }
+__device__ __forceinline__ int kv_kchunk(int r, int j) { return r * 8 + (j ^ ((r >> 1) & 7)); }
+__device__ __forceinline__ int kv_vchunk(int d, int q) { return 256 + d * 4 + (q ^ ((d >> 2) & 3)); }
 
 // heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16 blocks as above, keys n … ⌈n/32⌉·32 − 1 zero. grid (blocks, H),
 // one block of one head per workgroup; V goes through LDS for the transposition.
