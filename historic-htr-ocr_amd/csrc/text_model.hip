@@ -61,6 +61,9 @@ struct htr_session {
     int *state = nullptr;  // [pos, len]
     AttnScratch asc{};
     hipGraphExec_t step_graph = nullptr;  // the CPU-choice step (no token choice)
+    // the prefill's row buffers (ids, x, h, q, k, v, attention, g, u) for up to pre_cap rows, kept across calls
+    void *pre = nullptr;
+    size_t pre_cap = 0;
 };
 
 struct htr_choice {
@@ -266,7 +269,7 @@ extern "C" int htr_session_free(htr_session *s) {
     if (s->step_graph) hipGraphExecDestroy(s->step_graph);
     for (void *p : {(void *)s->kc, (void *)s->vc, (void *)s->rope, (void *)s->x, (void *)s->qkv, (void *)s->attn,
                     (void *)s->g, (void *)s->logits, (void *)s->tok, (void *)s->state, (void *)s->asc.part,
-                    (void *)s->asc.counters})
+                    (void *)s->asc.counters, s->pre})
         if (p) htr_dev_free(dev, p);
     delete s;
     return 0;
@@ -352,24 +355,33 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
     const int l = (int)n, d = c.dim, f = c.n_ff, qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const int pos0 = s->n_past;
     hipStream_t st = dev->stream;
+    // the row buffers, grown on demand and kept by the session (a prefill is often followed by more)
+    const size_t per_row = 4 * ((size_t)2 * d + 2 * (size_t)qd + 2 * (size_t)kvd + 2 * (size_t)f) + 16;
+    int rc = 0;
+    if (n > s->pre_cap) {
+        if (s->pre) htr_dev_free(dev, s->pre);
+        s->pre = nullptr;
+        s->pre_cap = 0;
+        rc = htr_dev_alloc(dev, n * per_row, HTR_MEM_WORK, &s->pre);
+        if (rc == 0) s->pre_cap = n;
+    }
     uint32_t *d_tok = nullptr;
     float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *a = nullptr, *g = nullptr,
           *u = nullptr;
-    auto cleanup = [&] {
-        for (void *p : {(void *)d_tok, (void *)x, (void *)h, (void *)q, (void *)k, (void *)v, (void *)a, (void *)g,
-                        (void *)u})
-            if (p) htr_dev_free(dev, p);
-    };
-    int rc = htr_dev_alloc(dev, n * 4, HTR_MEM_WORK, (void **)&d_tok);
-    if (rc == 0) rc = htr_upload(dev, d_tok, tok.data(), n * 4);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * d * 4, HTR_MEM_WORK, (void **)&x);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * d * 4, HTR_MEM_WORK, (void **)&h);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * qd * 4, HTR_MEM_WORK, (void **)&q);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * kvd * 4, HTR_MEM_WORK, (void **)&k);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * kvd * 4, HTR_MEM_WORK, (void **)&v);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * qd * 4, HTR_MEM_WORK, (void **)&a);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * f * 4, HTR_MEM_WORK, (void **)&g);
-    if (rc == 0) rc = htr_dev_alloc(dev, (size_t)l * f * 4, HTR_MEM_WORK, (void **)&u);
+    if (rc == 0) {
+        float *p = (float *)s->pre;
+        const size_t cap = s->pre_cap;
+        x = p, p += cap * d;
+        h = p, p += cap * d;
+        q = p, p += cap * qd;
+        k = p, p += cap * kvd;
+        v = p, p += cap * kvd;
+        a = p, p += cap * qd;
+        g = p, p += cap * f;
+        u = p, p += cap * f;
+        d_tok = (uint32_t *)p;
+        rc = htr_upload(dev, d_tok, tok.data(), n * 4);
+    }
     const float scale = 1.0f / sqrtf((float)HEAD);
     if (rc == 0) rc = launch_embed(dev, st, m->tok_embd, d_tok, l, x);
     for (int li = 0; li < c.n_layer && rc == 0; li++) {
@@ -397,9 +409,7 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
     }
     if (rc == 0) rc = htr_sync(dev);
     if (rc == 0 && h_logits) rc = htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4);
-    std::string keep = rc < 0 ? htr_last_error() : "";
-    cleanup();
-    if (rc < 0) return htr_fail("%s", keep.c_str());
+    if (rc < 0) return rc;
     s->n_past += l;
     return 0;
 }
