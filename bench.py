@@ -38,6 +38,27 @@ def log(msg: str) -> None:
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+def prefill_on_f32_path(dev, cfg, te, on, layers, ids) -> float:
+    """the same prefill on the F32 compute path (exact q8_0 values in the GEMMs): a second model, a warm call timed"""
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F32
+    try:
+        m = htr.TextModel(dev, htr.TextConfig(**cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+    s = m.session(len(ids))
+    s.prefill(ids)
+    s.rewind(0)
+    dev.sync()
+    t0 = time.perf_counter()
+    s.prefill(ids)
+    dt = time.perf_counter() - t0
+    log(f"prefill {len(ids)} tokens (f32 path): {dt * 1e3:.1f} ms")
+    s.free()
+    m.free()
+    return dt
+
+
 def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     from htr import synth
 
@@ -59,7 +80,8 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     t0 = time.perf_counter()
     s.prefill(prompt[:-1])
     prefill_s = time.perf_counter() - t0
-    log(f"prefill {prompt_len - 1} tokens: {prefill_s * 1e3:.1f} ms (first call {prefill_cold_s * 1e3:.1f} ms)")
+    path = "f16" if dev.compute == htr.COMPUTE_F16 else "f32"
+    log(f"prefill {prompt_len - 1} tokens ({path} path): {prefill_s * 1e3:.1f} ms (first call {prefill_cold_s * 1e3:.1f} ms)")
     preset = htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new)
     ch = s.choice(preset, prompt, chunk=16, depth=2)
 
@@ -81,12 +103,15 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     dt = time.perf_counter() - t0
     same = all(r == reads[0] for r in reads) and (ref is None or ref == reads[0])
     log(f"decode: {steps} reads × {n_new} tokens in {dt:.3f} s, identical reads: {same}")
+    prefill_f32_s = prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s
     out = {
         "tok_s": steps * n_new / dt,
         "ms_per_read": dt / steps * 1e3,
         "ms_per_token": dt / (steps * n_new) * 1e3,
         "prefill_ms": prefill_s * 1e3,
         "prefill_first_call_ms": prefill_cold_s * 1e3,
+        "prefill_compute_path": path,
+        "prefill_f32_path_ms": prefill_f32_s * 1e3,
         "reads_identical": same,
         "first_tokens": reads[0][:8],
     }

@@ -454,9 +454,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
+// OT: the output's type — f32, or f16 (rounded to nearest even: the value the f16 path's o-projection tile holds)
+template <typename OT>
 __global__ __launch_bounds__(256) void k_attn_causal(const float *q, const _Float16 *kc, const _Float16 *vc, int n_q,
                                                      int pos0, int n_head, int n_kv, int n_ctx, float scale,
-                                                     float *out) {
+                                                     OT *out) {
     __shared__ __attribute__((aligned(16))) _Float16 s_k[PK * KS];
     __shared__ __attribute__((aligned(16))) _Float16 s_vt[D * VS];
     const int kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -538,10 +540,18 @@ __global__ __launch_bounds__(256) void k_attn_causal(const float *q, const _Floa
     }
     if (q0 + c < n_q) {
         const float inv = 1.0f / l;
-        float *orow = out + ((size_t)(q0 + c) * n_head + h) * D + 4 * g;
+        OT *orow = out + ((size_t)(q0 + c) * n_head + h) * D + 4 * g;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
-            *reinterpret_cast<float4 *>(orow + 16 * t) = make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+        for (int t = 0; t < 8; t++) {
+            if constexpr (sizeof(OT) == 4) {
+                *reinterpret_cast<float4 *>(orow + 16 * t) =
+                    make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+            } else {
+                const half4 hv = {(_Float16)(o[t][0] * inv), (_Float16)(o[t][1] * inv), (_Float16)(o[t][2] * inv),
+                                  (_Float16)(o[t][3] * inv)};
+                *reinterpret_cast<half4 *>(orow + 16 * t) = hv;
+            }
+        }
     }
 }
 
@@ -613,13 +623,20 @@ int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k
 }
 
 int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
-                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out) {
+                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out, _Float16 *out16) {
     if (n_head != 2 * n_kv) return htr_fail("causal attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
     if (n_q < 1 || pos0 < 0 || pos0 + n_q > n_ctx)
         return htr_fail("causal attention: %d queries from position %d in a %d-row cache", n_q, pos0, n_ctx);
-    hipLaunchKernelGGL(k_attn_causal, dim3((n_q + PQ - 1) / PQ, n_kv), dim3(256), 0, st, q, (const _Float16 *)kc,
-                       (const _Float16 *)vc, n_q, pos0, n_head, n_kv, n_ctx, scale, out);
-    return htr_launched(dev, "k_attn_causal");
+    if (!out == !out16) return htr_fail("causal attention: one output, f32 or f16");
+    const dim3 grid((n_q + PQ - 1) / PQ, n_kv);
+    if (out) {
+        hipLaunchKernelGGL(k_attn_causal<float>, grid, dim3(256), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc,
+                           n_q, pos0, n_head, n_kv, n_ctx, scale, out);
+        return htr_launched(dev, "k_attn_causal");
+    }
+    hipLaunchKernelGGL(k_attn_causal<_Float16>, grid, dim3(256), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc,
+                       n_q, pos0, n_head, n_kv, n_ctx, scale, out16);
+    return htr_launched(dev, "k_attn_causal<f16>");
 }
 
 // ---- ABI ------------------------------------------------------------------------------------------------------------

@@ -11,12 +11,22 @@
 // the 16 consecutive k of 16h … 16h + 15 over the step's 16 MFMAs (k-slot h of each), so a lane's fragments are 4
 // contiguous 16-byte reads. Measured (1023 rows): see the bench's prefill. Other shapes: k_gemm_q8_0_f32, 64×64
 // tiles, 256 threads with 4×4 outputs each in f32 fma.
+//
+// The f16 compute path (matmul_coop_q8_0 / matmul128h_q8_0, gpu.rs:1976-1995) rounds X and the dequantised W to f16
+// where they enter the tiles and accumulates in f32: k_gemm_q8_0_f32<true> does that for any shape (the MFMA kernels
+// of that path, on f16 planes made by k_q8_to_f16, are in mfma_gemm.hip).
+#include <algorithm>
+
 #include "htr_internal.h"
 
 namespace {
 
 constexpr int BM = 64, BN = 64, BK = 32;
 
+// R16: X and W values rounded to f16 (round to nearest even) as they enter the tiles
+template <bool R16> __device__ __forceinline__ float tile_val(float v) { return R16 ? (float)(_Float16)v : v; }
+
+template <bool R16>
 __global__ __launch_bounds__(256) void k_gemm_q8_0_f32(const float *x, const int8_t *wq, const _Float16 *wd, float *y,
                                                        int m, int n, int k, int acc) {
     __shared__ float s_a[BK][BM + 4];
@@ -31,7 +41,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8_0_f32(const float *x, const int
         for (int i = 0; i < 8; i++) {
             const int e = tid + 256 * i, r = e / BK, cc = e % BK;
             const int gr = row0 + r;
-            s_a[cc][r] = gr < m ? x[(size_t)gr * k + k0 + cc] : 0.0f;
+            s_a[cc][r] = gr < m ? tile_val<R16>(x[(size_t)gr * k + k0 + cc]) : 0.0f;
         }
         // W tile: 64 columns × 32 quants of one block each, times that block's scale
 #pragma unroll
@@ -39,7 +49,7 @@ __global__ __launch_bounds__(256) void k_gemm_q8_0_f32(const float *x, const int
             const int e = tid + 256 * i, r = e / BK, cc = e % BK;
             const int gc = col0 + r;
             float v = 0.0f;
-            if (gc < n) v = (float)wq[(size_t)gc * k + k0 + cc] * (float)wd[(size_t)gc * nb + k0 / 32];
+            if (gc < n) v = tile_val<R16>((float)wq[(size_t)gc * k + k0 + cc] * (float)wd[(size_t)gc * nb + k0 / 32]);
             s_b[cc][r] = v;
         }
         __syncthreads();
@@ -163,7 +173,34 @@ __global__ __launch_bounds__(256) void k_gemm_q8_0_mfma(const float *x, const in
     }
 }
 
+// the f16 plane of a q8_0 weight: h = f16(q · d) (round to nearest even), 8 values a thread
+__global__ __launch_bounds__(256) void k_q8_to_f16(const int8_t *q, const _Float16 *d, _Float16 *h, size_t n8,
+                                                    int cols) {
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+        const size_t e = 8 * i, r = e / cols, c = e % cols;
+        const float s = (float)d[r * (cols / 32) + c / 32];
+        const int2 v = *reinterpret_cast<const int2 *>(q + e);
+        const uint32_t u[2] = {(uint32_t)v.x, (uint32_t)v.y};
+        _Float16 o[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = (_Float16)((float)(int8_t)(u[j / 4] >> (8 * (j % 4))) * s);
+        int4 out;
+        __builtin_memcpy(&out, o, 16);
+        *reinterpret_cast<int4 *>(h + e) = out;
+    }
+}
+
 }  // namespace
+
+int weight_attach_f16(htr_device *dev, hipStream_t st, htr_weight *w) {
+    if (w->h) return 0;
+    if (!w->q) return htr_fail("weight_attach_f16: the weight has no q8_0 planes");
+    HTR_TRY(htr_dev_alloc(dev, w->rows * w->cols * 2, HTR_MEM_WEIGHTS, (void **)&w->h));
+    const size_t n8 = w->rows * w->cols / 8;  // cols is a multiple of 32
+    const int grid = (int)std::min<size_t>((n8 + 255) / 256, (size_t)dev->n_cu * 16);
+    hipLaunchKernelGGL(k_q8_to_f16, dim3(grid), dim3(256), 0, st, w->q, w->d, w->h, n8, (int)w->cols);
+    return htr_launched(dev, "k_q8_to_f16");
+}
 
 int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
                          int acc) {
@@ -174,8 +211,18 @@ int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const 
                            acc);
         return htr_launched(dev, "k_gemm_q8_0_mfma");
     }
-    hipLaunchKernelGGL(k_gemm_q8_0_f32, grid, dim3(256), 0, st, x, w->q, w->d, y, m, (int)w->rows, (int)w->cols, acc);
+    hipLaunchKernelGGL(k_gemm_q8_0_f32<false>, grid, dim3(256), 0, st, x, w->q, w->d, y, m, (int)w->rows,
+                       (int)w->cols, acc);
     return htr_launched(dev, "k_gemm_q8_0_f32");
+}
+
+int launch_gemm_q8_0_r16(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
+                         int acc) {
+    if (!w->q) return htr_fail("gemm: weight has no q8_0 planes");
+    dim3 grid(((int)w->rows + BN - 1) / BN, (m + BM - 1) / BM);
+    hipLaunchKernelGGL(k_gemm_q8_0_f32<true>, grid, dim3(256), 0, st, x, w->q, w->d, y, m, (int)w->rows,
+                       (int)w->cols, acc);
+    return htr_launched(dev, "k_gemm_q8_0_f32<r16>");
 }
 
 int launch_rms_norm(htr_device *dev, hipStream_t st, const float *x, const float *w, float *y, int rows, int dim,
@@ -188,4 +235,15 @@ int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, siz
     const int grid = (int)std::min<size_t>((n + 255) / 256, 16384);
     hipLaunchKernelGGL(k_swiglu, dim3(grid), dim3(256), 0, st, g, u, n);
     return htr_launched(dev, "k_swiglu");
+}
+
+// ---- ABI ------------------------------------------------------------------------------------------------------------
+
+extern "C" int htr_matmul_q8_0(htr_device *dev, const float *d_x, size_t m, const htr_weight *w, float *d_y, int acc) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!d_x || !d_y || !w) return htr_fail("htr_matmul_q8_0: null argument");
+    if (m == 0) return 0;
+    if (m > (size_t)INT32_MAX / 2) return htr_fail("htr_matmul_q8_0: %zu rows", m);
+    return dev->compute == HTR_COMPUTE_F32 ? launch_gemm_q8_0_f32(dev, dev->stream, d_x, w, d_y, (int)m, acc)
+                                           : launch_gemm_q8_0_r16(dev, dev->stream, d_x, w, d_y, (int)m, acc);
 }

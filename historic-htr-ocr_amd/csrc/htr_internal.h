@@ -38,6 +38,8 @@ struct htr_device {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     // decode steps replayed as captured HIP graphs (HTR_GRAPHS=0 at open: launched one by one)
     bool use_graphs = true;
+    // the compute path of the models created on this device (HTR_COMPUTE_F16 / HTR_COMPUTE_F32)
+    int compute = HTR_COMPUTE_F16;
 };
 
 enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3 };
@@ -121,8 +123,10 @@ int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const ui
 int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k, const float *v, const float *qn,
                              const float *kn, const float *rope, int n_tok, int n_head, int n_kv, int pos0, int n_ctx,
                              float eps, uint16_t *kc, uint16_t *vc);
+// out [n_q][n_head·128] f32, or f16 into out16 (the f16 path's o-projection input) when out is NULL
 int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
-                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out);
+                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out,
+                       _Float16 *out16 = nullptr);
 
 // token choice (choose.hip)
 struct ChooseArgs {
@@ -149,19 +153,23 @@ size_t choose_best_bytes(int rows);
 size_t choose_ticket_bytes(int rows);
 int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a);
 
-// dense kernels (gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ with W q8_0 (exact dequant), f32; rms_norm rows; swiglu
+// dense kernels (gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ with W q8_0 (exact dequant), f32; the same with X and W rounded to
+// f16 at the tiles (the f16 compute path, any shape); rms_norm rows; swiglu; a weight's f16 plane made on the device
 int launch_gemm_q8_0_f32(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
                          int acc);
+int launch_gemm_q8_0_r16(htr_device *dev, hipStream_t st, const float *x, const htr_weight *w, float *y, int m,
+                         int acc);
+int weight_attach_f16(htr_device *dev, hipStream_t st, htr_weight *w);
 int launch_rms_norm(htr_device *dev, hipStream_t st, const float *x, const float *w, float *y, int rows, int dim,
                     float eps);
 int launch_swiglu(htr_device *dev, hipStream_t st, float *g, const float *u, size_t n);
 
 // MFMA GEMM (mfma_gemm.hip): Y[M,N] (+)= X[M,K]·Wᵀ, X and W f16, f32 accumulation. GEMM_FFN: w = gate, w2 = up,
-// y16 = f16(silu(X·Wgᵀ)·(X·Wuᵀ)·scale). W rows a multiple of 128, K a multiple of 32.
+// y16 = f16(silu(X·Wgᵀ)·(X·Wuᵀ)·scale). W rows a multiple of 64 (the FFN: 128), K a multiple of 32.
 enum { GEMM_F32 = 0, GEMM_ACC = 1, GEMM_FFN = 2 };
 int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x, int m, const htr_weight *w,
                     const htr_weight *w2, float *y, _Float16 *y16, float scale);
-// Q / K / V of one input as one GEMM over the three weights (rows a multiple of 256), three f32 outputs
+// Q / K / V of one input as one GEMM over the three stacked weights (rows each a multiple of 64), three f32 outputs
 int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
                         const htr_weight *wk, const htr_weight *wv, float *q, float *k, float *v);
 

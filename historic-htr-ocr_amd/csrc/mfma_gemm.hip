@@ -1,30 +1,35 @@
-// The vision encoder's GEMMs on gfx950's matrix cores: Y[M,N] (+)= X[M,K] · W[N,K]ᵀ with X and W f16 in memory and
-// f32 accumulation, the fused FFN first half G = silu(X·Wgᵀ) · (X·Wuᵀ) · scale → f16, and Q / K / V as one GEMM over
-// the three weights.
+// GEMMs on gfx950's matrix cores: Y[M,N] (+)= X[M,K] · W[N,K]ᵀ with X and W f16 in memory and f32 accumulation,
+// the fused FFN first half G = silu(X·Wgᵀ) · (X·Wuᵀ) · scale → f16, and Q / K / V as one GEMM over the three
+// stacked weights. The vision encoder's GEMMs and, on the f16 compute path, the text prefill's.
 //
-// Reference semantics: matmul_coopd.wgsl (Batch::matmul_f16x, gpu.rs:2019-2042) and ffn_coopd.wgsl (Batch::ffn_f16,
-// gpu.rs:2048-2086; out_scale = 1/64, vision.rs:31-35). The schedule is this library's own:
+// Reference semantics: matmul_coopd.wgsl (Batch::matmul_f16x, gpu.rs:2019-2042), ffn_coopd.wgsl (Batch::ffn_f16,
+// gpu.rs:2048-2086; out_scale = 1/64, vision.rs:31-35) and matmul_coop.wgsl (Batch::matmul on F16Coop,
+// gpu.rs:1976-1984: X and the dequantised W rounded to f16, f32 accumulation). The schedule is this library's own:
 //
-//   tile      a 512-thread workgroup (8 waves) owns a 256 × 256 tile of X rows × W rows; wave (wm, wn) of 2 × 4 owns
-//             128 × 64 of it as 4 × 2 v_mfma_f32_32x32x16_f16 tiles (lane layouts checked on the GPU: A lane ℓ holds
+//   tile      a workgroup owns a BM × BN tile of X rows × W rows, split over a WM × WN grid of waves, each wave
+//             TM × TN v_mfma_f32_32x32x16_f16 tiles (lane layouts checked on the GPU: A lane ℓ holds
 //             A[ℓ%32][8(ℓ/32) …+7], B lane ℓ holds B[8(ℓ/32) …+7][ℓ%32], D lane ℓ register r is row 8(r/4) + 4(ℓ/32)
-//             + r%4, column ℓ%32). The FFN's W tile is 128 gate rows and the same 128 up rows in alternating blocks
-//             of 32, so a wave's two column tiles are one gate and one up tile of the same outputs;
-//   K         in stages of 32 through a ring of 4 LDS stages (32 KB each) filled by direct-to-LDS loads
-//             (global_load_lds_dwordx4): the stage 3 ahead is loading while one is computed. Inside a stage a row's
-//             four 16-byte chunks sit at chunk ^ (row/4 % 4): 16 consecutive rows of one chunk fall on 16 different
-//             16-byte bank groups (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes);
-//   pipeline  the fragments of stage kt are read from LDS during stage kt − 1; stage kt runs its first 8 MFMAs, then
-//             waits for stage kt + 1 and the workgroup barrier while they drain, issues the loads of stage kt + 3
-//             and the fragment reads of stage kt + 1, then its last 8 MFMAs. Waits are explicit s_waitcnt vmcnt
+//             + r%4, column ℓ%32). Three tile shapes: 256 × 256 (8 waves of 128 × 64), 128 × 128 and 64 × 64 (4
+//             waves of 64 × 64 / 32 × 32); the launch takes the largest that still gives half a workgroup per CU.
+//             The FFN's W tile is BN/2 gate rows and the same BN/2 up rows in alternating blocks of 32, so a wave's
+//             two column tiles are one gate and one up tile of the same outputs;
+//   K         in stages of 32 through a ring of 4 LDS stages filled by direct-to-LDS loads (global_load_lds_dwordx4):
+//             the stage 3 ahead is loading while one is computed. Inside a stage a row's four 16-byte chunks sit at
+//             chunk ^ (row/4 % 4): 16 consecutive rows of one chunk fall on 16 different 16-byte bank groups
+//             (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes);
+//   pipeline  the fragments of stage kt are read from LDS during stage kt − 1; stage kt runs its first half of MFMAs,
+//             then waits for stage kt + 1 and the workgroup barrier while they drain, issues the loads of stage
+//             kt + 3 and the fragment reads of stage kt + 1, then its second half. Waits are explicit s_waitcnt vmcnt
 //             (the LDS loads' completion) and a bare s_barrier (no fence that would wait for the stages in flight);
 //   order     tiles are dealt to the 8 XCDs in contiguous bands (workgroup b runs on XCD b mod 8); inside a band
 //             groups of 4 tile rows are walked column by column, so the workgroups resident on an XCD share both
 //             their X rows and their W rows in its L2;
-//   edges     rows past M read row M − 1 and are not stored; a last tile past N (N an odd multiple of 128) reads its
-//             W rows clamped and stores nothing there. K/32 may be odd.
-// Measured at M = 12100 on one MI355X: 886 TFLOP/s at N = 8192, K = 1024 and 898 at N = 1024, K = 4096, against
-// ≈ 2.0 PFLOP/s sustained by MFMAs from registers (the earlier 128 × 128, one-stage-ahead kernel: 374 – 641).
+//   edges     rows past M read row M − 1 and are not stored; W rows past a weight's end (a last tile that runs over)
+//             are read clamped and not stored. Stacked weights start on tile boundaries. K/32 may be odd.
+// Measured at M = 12100 on one MI355X (256 × 256 tiles): 886 TFLOP/s at N = 8192, K = 1024 and 898 at N = 1024,
+// K = 4096, against ≈ 2.0 PFLOP/s sustained by MFMAs from registers.
+#include <algorithm>
+
 #include "htr_internal.h"
 
 namespace {
@@ -32,23 +37,31 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int GW = 512, NW = GW / 64;   // threads, waves
-constexpr int BM = 256, BN = 256;        // tile: X rows × W rows
-constexpr int WM = 2, WN = 4;            // wave grid
-constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles a wave: 4 × 2
-constexpr int ST = 4;                    // LDS stages of 32 K each
-constexpr int ACH = BM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
-constexpr int AI = ACH / GW, BI = BCH / GW;                 // direct-to-LDS loads a wave a stage
-constexpr int GROUP = 4;                 // tile rows walked together
+template <int BM_, int BN_, int WM_, int WN_> struct Tile {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;  // tile: X rows × W rows; wave grid
+    static constexpr int NW = WM * WN, GW = 64 * NW;                // waves, threads
+    static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles a wave
+    static constexpr int ACH = BM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
+    static constexpr int AI = ACH / GW, BI = BCH / GW;              // direct-to-LDS loads a wave a stage
+    static_assert(TM >= 1 && TN >= 1 && AI * GW == ACH && BI * GW == BCH, "tile shape");
+};
+using T256 = Tile<256, 256, 2, 4>;
+using T128 = Tile<128, 128, 2, 2>;
+using T64 = Tile<64, 64, 2, 2>;
+
+constexpr int ST = 4;      // LDS stages of 32 K each
+constexpr int GROUP = 4;   // tile rows walked together
 constexpr int XCDS = 8;
 constexpr int MAX_W = 3;
 
 struct GemmK {
     const _Float16 *x;          // [M][K]
-    const _Float16 *w[MAX_W];   // F32 / ACC: W split in n_w equal row blocks; FFN: gate, up
-    int n_w, rows_w;            // weights, rows of each
-    float *y[MAX_W];            // F32 / ACC: [M][rows_w] each (the output columns of weight i)
-    _Float16 *y16;              // FFN: [M][rows_w] f16
+    const _Float16 *w[MAX_W];   // F32 / ACC: the stacked weights; FFN: gate, up
+    int n_w;                    // weights
+    int rows[MAX_W];            // rows of each (FFN: both the gate's)
+    int start[MAX_W];           // F32 / ACC: the first stacked row of each (a multiple of BN)
+    float *y[MAX_W];            // F32 / ACC: [M][rows[i]] each (the output columns of weight i)
+    _Float16 *y16;              // FFN: [M][rows[0]] f16
     int m, k;
     float scale;                // FFN output scale
     int tiles_m, tiles_n;
@@ -59,7 +72,10 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 // the 16-byte chunk slot of (row r, chunk c) in a stage region
 __device__ __forceinline__ int chunk_slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
 
-template <int EPI> __global__ __launch_bounds__(GW) void k_gemm_f16(const GemmK a) {
+template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(const GemmK a) {
+    constexpr int BM = T::BM, BN = T::BN, WN = T::WN, NW = T::NW, TM = T::TM, TN = T::TN;
+    constexpr int ACH = T::ACH, SCH = T::SCH, AI = T::AI, BI = T::BI;
+    static_assert(EPI != GEMM_FFN || TN == 2, "the FFN pairs one gate and one up tile a wave");
     __shared__ __attribute__((aligned(16))) int4 s_t[ST * SCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -74,18 +90,21 @@ template <int EPI> __global__ __launch_bounds__(GW) void k_gemm_f16(const GemmK 
         tn = gr / gm;
     }
     const int row0 = tm * BM, k = a.k, nk = k / 32, m = a.m;
-    // the W rows of tile row r (0 … BN−1): F32 / ACC the tile's rows of the stacked weights (one weight a tile, the
-    // last tile past the end clamped); FFN blocks of 32 alternating gate / up rows of the tile's 128 outputs
-    const int8_t wsel = EPI == GEMM_FFN ? 0 : (int8_t)min((tn * BN) / a.rows_w, a.n_w - 1);
+    // the W rows of tile row r (0 … BN−1): F32 / ACC the tile's rows of the stacked weights (one weight a tile, rows
+    // past its end clamped); FFN blocks of 32 alternating gate / up rows of the tile's BN/2 outputs
+    int wsel = 0;
+    if (EPI != GEMM_FFN)
+        for (int i = 1; i < a.n_w; i++) wsel += tn * BN >= a.start[i];
     const _Float16 *wbase = a.w[wsel];
-    const int wrow0 = EPI == GEMM_FFN ? tn * (BN / 2) : tn * BN - wsel * a.rows_w;
+    const int wrows = a.rows[wsel];
+    const int wrow0 = EPI == GEMM_FFN ? tn * (BN / 2) : tn * BN - a.start[wsel];
     auto w_row = [&](int r, const _Float16 *&base) -> int {
         if (EPI == GEMM_FFN) {
             base = (r >> 5) & 1 ? a.w[1] : a.w[0];
             return wrow0 + (r >> 6) * 32 + (r & 31);
         }
         base = wbase;
-        return min(wrow0 + r, a.rows_w - 1);
+        return min(wrow0 + r, wrows - 1);
     };
     auto issue = [&](int ks, int buf) {
         const size_t kk = (size_t)min(ks, nk - 1) * 32;
@@ -180,7 +199,7 @@ template <int EPI> __global__ __launch_bounds__(GW) void k_gemm_f16(const GemmK 
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < m) a.y16[(size_t)row * a.rows_w + col] = (_Float16)(silu(acc[i][0][r]) * acc[i][1][r] * a.scale);
+                if (row < m) a.y16[(size_t)row * a.rows[0] + col] = (_Float16)(silu(acc[i][0][r]) * acc[i][1][r] * a.scale);
             }
         return;
     }
@@ -188,30 +207,70 @@ template <int EPI> __global__ __launch_bounds__(GW) void k_gemm_f16(const GemmK 
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int col = wrow0 + wn * TN * 32 + 32 * j + (lane & 31);
-        if (col >= a.rows_w) continue;  // the part of a last tile past N
+        if (col >= wrows) continue;  // the part of a last tile past the weight's end
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (row >= m) continue;
-                float *o = y + (size_t)row * a.rows_w + col;
+                float *o = y + (size_t)row * wrows + col;
                 *o = EPI == GEMM_ACC ? *o + acc[i][j][r] : acc[i][j][r];
             }
     }
 }
 
-int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
-    a.tiles_m = (a.m + BM - 1) / BM;
-    a.tiles_n = epi == GEMM_FFN ? a.rows_w / (BN / 2) : (a.n_w * a.rows_w + BN - 1) / BN;
+template <class T> int tiles_for(const GemmK &a, int epi, int &tm, int &tn) {
+    tm = (a.m + T::BM - 1) / T::BM;
+    if (epi == GEMM_FFN) {
+        if (a.rows[0] % (T::BN / 2)) return -1;
+        tn = a.rows[0] / (T::BN / 2);
+        return tm * tn;
+    }
+    for (int i = 1; i < a.n_w; i++)
+        if (a.start[i] % T::BN) return -1;
+    tn = (a.start[a.n_w - 1] + a.rows[a.n_w - 1] + T::BN - 1) / T::BN;
+    return tm * tn;
+}
+
+template <class T> void launch_tile(hipStream_t st, int epi, const GemmK &a) {
     const dim3 grid(a.tiles_m * a.tiles_n);
     switch (epi) {
-    case GEMM_F32: hipLaunchKernelGGL(k_gemm_f16<GEMM_F32>, grid, dim3(GW), 0, st, a); break;
-    case GEMM_ACC: hipLaunchKernelGGL(k_gemm_f16<GEMM_ACC>, grid, dim3(GW), 0, st, a); break;
-    case GEMM_FFN: hipLaunchKernelGGL(k_gemm_f16<GEMM_FFN>, grid, dim3(GW), 0, st, a); break;
-    default: return htr_fail("gemm_f16: epilogue %d", epi);
+    case GEMM_F32: hipLaunchKernelGGL((k_gemm_f16<GEMM_F32, T>), grid, dim3(T::GW), 0, st, a); break;
+    case GEMM_ACC: hipLaunchKernelGGL((k_gemm_f16<GEMM_ACC, T>), grid, dim3(T::GW), 0, st, a); break;
+    default:
+        if constexpr (T::TN == 2) hipLaunchKernelGGL((k_gemm_f16<GEMM_FFN, T>), grid, dim3(T::GW), 0, st, a);
+        break;
     }
-    return htr_launched(dev, "k_gemm_f16");
+}
+
+// the largest tile shape that gives at least half a workgroup per CU; else the one with the most tiles (the FFN: 256
+// or 128 — a wave pairs one gate and one up tile)
+int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
+    if (epi != GEMM_F32 && epi != GEMM_ACC && epi != GEMM_FFN) return htr_fail("gemm_f16: epilogue %d", epi);
+    const int want = std::max(1, dev->n_cu / 2);
+    int tm, tn;
+    const int n_tiles[3] = {tiles_for<T256>(a, epi, tm, tn), tiles_for<T128>(a, epi, tm, tn),
+                            epi == GEMM_FFN ? -1 : tiles_for<T64>(a, epi, tm, tn)};
+    int pick = -1;
+    for (int i = 0; i < 3 && pick < 0; i++)
+        if (n_tiles[i] >= want) pick = i;
+    for (int i = 0; i < 3 && pick < 0; i++)
+        if (n_tiles[i] >= 0 && (pick < 0 || n_tiles[i] > n_tiles[pick])) pick = i;
+    if (pick < 0) return htr_fail("gemm_f16: no tile shape fits weights of %d rows", a.rows[0]);
+    if (pick == 0) {
+        tiles_for<T256>(a, epi, a.tiles_m, a.tiles_n);
+        launch_tile<T256>(st, epi, a);
+        return htr_launched(dev, "k_gemm_f16<256>");
+    }
+    if (pick == 1) {
+        tiles_for<T128>(a, epi, a.tiles_m, a.tiles_n);
+        launch_tile<T128>(st, epi, a);
+        return htr_launched(dev, "k_gemm_f16<128>");
+    }
+    tiles_for<T64>(a, epi, a.tiles_m, a.tiles_n);
+    launch_tile<T64>(st, epi, a);
+    return htr_launched(dev, "k_gemm_f16<64>");
 }
 
 }  // namespace
@@ -221,8 +280,9 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
     if (!w || !w->h) return htr_fail("gemm_f16: the weight has no f16 plane (htr_weight_q8_0_f16)");
     const int n = (int)w->rows, k = (int)w->cols;
     if (m < 1) return htr_fail("gemm_f16: %d rows", m);
-    if (n % 128 || k % 32)
-        return htr_fail("gemm_f16: W [%d x %d]: rows a multiple of 128, columns a multiple of 32", n, k);
+    if (n % 64 || k % 32 || (epi == GEMM_FFN && n % 128))
+        return htr_fail("gemm_f16: W [%d x %d]: rows a multiple of %d, columns a multiple of 32", n, k,
+                        epi == GEMM_FFN ? 128 : 64);
     if (epi == GEMM_FFN && (!w2 || !w2->h || (int)w2->rows != n || (int)w2->cols != k))
         return htr_fail("gemm_f16: the FFN's up weight must match the gate weight [%d x %d]", n, k);
     GemmK a{};
@@ -231,7 +291,7 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
     a.w[1] = epi == GEMM_FFN ? w2->h : w->h;
     a.w[2] = w->h;
     a.n_w = 1;
-    a.rows_w = n;
+    a.rows[0] = a.rows[1] = a.rows[2] = n;
     a.y[0] = a.y[1] = a.y[2] = y;
     a.y16 = y16;
     a.m = m;
@@ -245,17 +305,22 @@ int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int 
     const htr_weight *ws[3] = {wq, wk, wv};
     for (const htr_weight *w : ws)
         if (!w || !w->h) return htr_fail("gemm_f16_qkv: a weight has no f16 plane (htr_weight_q8_0_f16)");
-    const int n = (int)wq->rows, k = (int)wq->cols;
+    const int k = (int)wq->cols;
     if (m < 1) return htr_fail("gemm_f16_qkv: %d rows", m);
-    if (n % BN || k % 32 || (int)wk->rows != n || (int)wv->rows != n || (int)wk->cols != k || (int)wv->cols != k)
-        return htr_fail("gemm_f16_qkv: three W [%d x %d], rows a multiple of %d, columns of 32", n, k, BN);
+    for (const htr_weight *w : ws)
+        if ((int)w->cols != k || w->rows % 64 || k % 32)
+            return htr_fail("gemm_f16_qkv: W [%zu x %zu]: rows a multiple of 64, %d columns (a multiple of 32)",
+                            w->rows, w->cols, k);
     GemmK a{};
     a.x = x;
-    a.w[0] = wq->h;
-    a.w[1] = wk->h;
-    a.w[2] = wv->h;
     a.n_w = 3;
-    a.rows_w = n;
+    int start = 0;
+    for (int i = 0; i < 3; i++) {
+        a.w[i] = ws[i]->h;
+        a.rows[i] = (int)ws[i]->rows;
+        a.start[i] = start;
+        start += a.rows[i];
+    }
     a.y[0] = q;
     a.y[1] = kk;
     a.y[2] = v;

@@ -71,6 +71,18 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
     dev->ordinal = ordinal;
     const char *graphs = getenv("HTR_GRAPHS");
     dev->use_graphs = !(graphs && strcmp(graphs, "0") == 0);
+    // gpu.rs:1107-1115: OCR_WGPU_COMPUTE forces a compute path (coop and f16 are one path here: f16 operands into the
+    // matrix cores, f32 sums); unset, the best one — f16 on matrix units, as Compute::choose picks on such a device
+    if (const char *want = getenv("OCR_WGPU_COMPUTE")) {
+        if (strcmp(want, "f32") == 0) {
+            dev->compute = HTR_COMPUTE_F32;
+        } else if (strcmp(want, "f16") == 0 || strcmp(want, "coop") == 0) {
+            dev->compute = HTR_COMPUTE_F16;
+        } else {
+            delete dev;
+            return htr_fail("OCR_WGPU_COMPUTE=%s: f32, f16 or coop", want);
+        }
+    }
     snprintf(dev->name, sizeof dev->name, "%s (%s)", prop.name, prop.gcnArchName);
     dev->n_cu = prop.multiProcessorCount;
     // default priority: one stream for every launch of this device
@@ -91,6 +103,21 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
         return htr_fail("hipEventCreate: %s", hipGetErrorString(e));
     }
     *out = dev;
+    return 0;
+}
+
+extern "C" int htr_device_set_compute(htr_device *dev, int compute) {
+    if (!dev) return htr_fail("htr_device_set_compute: null device");
+    if (compute != HTR_COMPUTE_F32 && compute != HTR_COMPUTE_F16)
+        return htr_fail("compute path %d: HTR_COMPUTE_F32 (%d) or HTR_COMPUTE_F16 (%d)", compute, HTR_COMPUTE_F32,
+                        HTR_COMPUTE_F16);
+    dev->compute = compute;
+    return 0;
+}
+
+extern "C" int htr_device_compute(htr_device *dev, int *compute) {
+    if (!dev || !compute) return htr_fail("htr_device_compute: null argument");
+    *compute = dev->compute;
     return 0;
 }
 

@@ -44,6 +44,8 @@ std::vector<float> rope_table(float base, int d_head, int n_pos) {
 struct htr_text_model {
     htr_device *dev = nullptr;
     htr_text_config cfg{};
+    int compute = HTR_COMPUTE_F16;  // the device's compute path at creation
+    bool mfma16 = false;            // f16 path: the projections carry f16 planes for the MFMA GEMMs
     htr_weight *tok_embd = nullptr;
     float *output_norm = nullptr;
     std::vector<Layer> layers;
@@ -252,6 +254,16 @@ extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg
     }
     if (rc == 0) rc = upload_w(dev, tok_embd, c.n_vocab, d, "token_embd", &m->tok_embd);
     if (rc == 0) rc = upload_vec(dev, output_norm, d, &m->output_norm);
+    // the f16 compute path's prefill GEMMs read f16(q·d) planes (matmul_coop_q8_0 rounds the dequantised W to f16 as
+    // it loads a tile); the MFMA kernels take rows in multiples of 64 (the FFN's 128), else the tiled kernel rounds
+    m->compute = dev->compute;
+    m->mfma16 = m->compute == HTR_COMPUTE_F16 && d % 64 == 0 && f % 128 == 0;
+    for (int i = 0; i < c.n_layer && rc == 0 && m->mfma16; i++) {
+        Layer &l = m->layers[i];
+        for (htr_weight *w : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down})
+            if (rc == 0) rc = weight_attach_f16(dev, dev->stream, w);
+    }
+    if (rc == 0 && m->mfma16) rc = htr_sync(dev);
     if (rc < 0) {
         std::string keep = htr_last_error();
         htr_text_model_free(m);
@@ -383,24 +395,44 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         rc = htr_upload(dev, d_tok, tok.data(), n * 4);
     }
     const float scale = 1.0f / sqrtf((float)HEAD);
+    // the f16 path on the matrix cores: the GEMM inputs are written as f16 — the values matmul_coop_q8_0's tiles hold
+    // (h, the attention output and g in the first halves of their f32 rows' space); the FFN's first GEMM fuses SwiGLU
+    _Float16 *h16 = (_Float16 *)h, *a16 = (_Float16 *)a, *g16 = (_Float16 *)g;
     if (rc == 0) rc = launch_embed(dev, st, m->tok_embd, d_tok, l, x);
-    for (int li = 0; li < c.n_layer && rc == 0; li++) {
+    for (int li = 0; li < c.n_layer && rc == 0 && m->mfma16; li++) {
+        const Layer &ly = m->layers[li];
+        uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
+        rc = launch_rms_norm_f16(dev, st, x, ly.attn_norm, h16, l, d, c.eps);
+        if (rc == 0) rc = launch_gemm_f16_qkv(dev, st, h16, l, ly.q, ly.k, ly.v, q, k, v);
+        if (rc == 0)
+            rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
+                                          s->n_ctx, c.eps, kc, vc);
+        if (rc == 0)
+            rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, nullptr, a16);
+        if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_ACC, a16, l, ly.o, nullptr, x, nullptr, 1.0f);
+        if (rc == 0) rc = launch_rms_norm_f16(dev, st, x, ly.ffn_norm, h16, l, d, c.eps);
+        if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_FFN, h16, l, ly.gate, ly.up, nullptr, g16, 1.0f);
+        if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_ACC, g16, l, ly.down, nullptr, x, nullptr, 1.0f);
+    }
+    // the F32 path (exact q8_0 values, f32 sums), or the f16 path's rounding on the tiled kernel for other shapes
+    auto gemm = m->compute == HTR_COMPUTE_F32 ? launch_gemm_q8_0_f32 : launch_gemm_q8_0_r16;
+    for (int li = 0; li < c.n_layer && rc == 0 && !m->mfma16; li++) {
         const Layer &ly = m->layers[li];
         uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
         rc = launch_rms_norm(dev, st, x, ly.attn_norm, h, l, d, c.eps);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.q, q, l, 0);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.k, k, l, 0);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.v, v, l, 0);
+        if (rc == 0) rc = gemm(dev, st, h, ly.q, q, l, 0);
+        if (rc == 0) rc = gemm(dev, st, h, ly.k, k, l, 0);
+        if (rc == 0) rc = gemm(dev, st, h, ly.v, v, l, 0);
         if (rc == 0)
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
                                           s->n_ctx, c.eps, kc, vc);
         if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, a);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, a, ly.o, x, l, 1);
+        if (rc == 0) rc = gemm(dev, st, a, ly.o, x, l, 1);
         if (rc == 0) rc = launch_rms_norm(dev, st, x, ly.ffn_norm, h, l, d, c.eps);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.gate, g, l, 0);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, h, ly.up, u, l, 0);
+        if (rc == 0) rc = gemm(dev, st, h, ly.gate, g, l, 0);
+        if (rc == 0) rc = gemm(dev, st, h, ly.up, u, l, 0);
         if (rc == 0) rc = launch_swiglu(dev, st, g, u, (size_t)l * f);
-        if (rc == 0) rc = launch_gemm_q8_0_f32(dev, st, g, ly.down, x, l, 1);
+        if (rc == 0) rc = gemm(dev, st, g, ly.down, x, l, 1);
     }
     // head (text.rs:655-658): output_norm + the tied LM head on the last row
     if (rc == 0) {

@@ -19,15 +19,16 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhtr.so")
 
 MEM_WEIGHTS, MEM_KV_CACHE, MEM_WORK, MEM_READBACK = 0, 1, 2, 3
+COMPUTE_F32, COMPUTE_F16 = 0, 1
 
 # every symbol include/htr.h declares
 SYMBOLS = [
     "htr_last_error", "htr_device_open", "htr_device_close", "htr_alive", "htr_set_fatal_hook", "htr_debug_mark_lost",
-    "htr_sync", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free",
+    "htr_sync", "htr_device_set_compute", "htr_device_compute", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free",
     "htr_upload", "htr_download", "htr_copy", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
-    "htr_choose_many", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
+    "htr_choose_many", "htr_matmul_q8_0", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
     "htr_vision_out_shape", "htr_vision_encode", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
@@ -92,6 +93,8 @@ def lib() -> C.CDLL:
             "htr_set_fatal_hook": (i32, [vp, FATAL_HOOK, vp]),
             "htr_debug_mark_lost": (i32, [vp, C.c_char_p]),
             "htr_sync": (i32, [vp]),
+            "htr_device_set_compute": (i32, [vp, i32]),
+            "htr_device_compute": (i32, [vp, C.POINTER(i32)]),
             "htr_device_info": (i32, [vp, C.c_char_p, sz, C.POINTER(i32)]),
             "htr_timer_begin": (i32, [vp]),
             "htr_timer_end": (i32, [vp, C.POINTER(f32)]),
@@ -114,6 +117,7 @@ def lib() -> C.CDLL:
             "htr_decode_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
             "htr_choose": (i32, [vp, vp, i32, vp, i32, i32, f32, f32, vp, vp, vp]),
             "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),
+            "htr_matmul_q8_0": (i32, [vp, vp, sz, vp, vp, i32]),
             "htr_gemm_f16": (i32, [vp, vp, sz, vp, vp, i32]),
             "htr_gemm_ffn_f16": (i32, [vp, vp, sz, vp, vp, f32, vp]),
             "htr_vision_create": (i32, [vp, C.POINTER(VisionConfigC), vp, vp, C.POINTER(VisionLayerC), vp, vp, vp, vp,
@@ -237,6 +241,18 @@ class Device:
     def sync(self) -> None:
         _check(lib().htr_sync(self.h))
 
+    @property
+    def compute(self) -> int:
+        """the compute path (COMPUTE_F16 by default, as the reference picks on a device with matrix units;
+        OCR_WGPU_COMPUTE=f32 at open or a set forces COMPUTE_F32); models keep the path of their creation"""
+        c = C.c_int()
+        _check(lib().htr_device_compute(self.h, C.byref(c)))
+        return c.value
+
+    @compute.setter
+    def compute(self, value: int) -> None:
+        _check(lib().htr_device_set_compute(self.h, int(value)))
+
     def info(self) -> tuple[str, int]:
         name = C.create_string_buffer(256)
         n_cu = C.c_int()
@@ -337,6 +353,11 @@ def choose(dev: Device, logits: Buffer, n_vocab: int, hist: Buffer, length: int,
 def choose_many(dev: Device, logits: Buffer, n_vocab: int, n: int, hist: Buffer, hist_stride: int, length: int,
                 window: int, rp: float, tok: Buffer) -> None:
     _check(lib().htr_choose_many(dev.h, logits.ptr, n_vocab, n, hist.ptr, hist_stride, length, window, rp, tok.ptr))
+
+
+def matmul_q8_0(dev: Device, x: Buffer, m: int, w: Weight, y: Buffer, acc: bool = False) -> None:
+    """y[m][N] (+)= x·Wᵀ (x f32 [m][K], w q8_0) on the device's compute path: F32 exact, F16 operands rounded to f16"""
+    _check(lib().htr_matmul_q8_0(dev.h, x.ptr, m, w.h, y.ptr, int(acc)))
 
 
 def gemm_f16(dev: Device, x16: Buffer, m: int, w: Weight, y: Buffer, acc: bool = False) -> None:

@@ -50,6 +50,15 @@ int htr_set_fatal_hook(htr_device *dev, htr_fatal_hook hook, void *user);
 int htr_debug_mark_lost(htr_device *dev, const char *why);
 /* wait for the device's queue (gpu.rs:1458-1485 Gpu::wait) */
 int htr_sync(htr_device *dev);
+/* the compute path (gpu.rs:1101-1137 Gpu::with_compute / Compute::choose, OCR_WGPU_COMPUTE): HTR_COMPUTE_F16 — the
+ * default, and what the reference picks on a device with f16 and matrix units (F16Coop) — rounds the prefill GEMMs' X
+ * and dequantised W to f16 and sums in f32 (matmul_coop_q8_0); HTR_COMPUTE_F32 computes them from the exact q8_0
+ * values in f32 (matmul128_q8_0). OCR_WGPU_COMPUTE = f32 / f16 / coop at open sets it as the reference's env var does.
+ * A text model keeps the path of its device at creation. The decode step and the vision encoder run the f16 paths'
+ * kernels on either setting (f32 arithmetic in the decode; the vision encoder's F32 path is not built). */
+enum { HTR_COMPUTE_F32 = 0, HTR_COMPUTE_F16 = 1 };
+int htr_device_set_compute(htr_device *dev, int compute);
+int htr_device_compute(htr_device *dev, int *compute);
 /* the device name and compute-unit count, for reports */
 int htr_device_info(htr_device *dev, char *name, size_t name_len, int *n_cu);
 /* HIP-event timing on the device's stream (measurement helpers, no reference counterpart — the reference's profiler
@@ -123,6 +132,12 @@ int htr_choose(htr_device *dev, float *d_logits, int n_vocab, uint32_t *d_hist, 
  * the 10k-step measurement of the choice kernel (no reference counterpart) */
 int htr_choose_many(htr_device *dev, float *d_logits, int n_vocab, int n, uint32_t *d_hist, int hist_stride, int len,
                     int window, float rp, uint32_t *d_tok);
+
+/* Y[m][N] (+= with acc) X·Wᵀ, X f32 [m][K], W q8_0 [N][K] (gpu.rs:1963-2014 Batch::matmul with a q8_0 weight, the
+ * prefill's GEMMs): on the device's compute path — F32: exact dequant, f32 fma (matmul128_q8_0 / matmul.wgsl);
+ * F16: X and W rounded to f16 as they enter the tiles, f32 sums (matmul128h_q8_0 / matmul_coop_q8_0). Any shape
+ * (K a multiple of 32). */
+int htr_matmul_q8_0(htr_device *dev, const float *d_x, size_t m, const htr_weight *w, float *d_y, int acc);
 
 /* ---- the vision encoder's GEMMs on the matrix cores (gpu.rs:2019-2042 Batch::matmul_f16x → matmul_coopd.wgsl,
  *      gpu.rs:2048-2086 Batch::ffn_f16 → ffn_coopd.wgsl) ------------------------------------------------------- */

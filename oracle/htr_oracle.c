@@ -665,7 +665,10 @@ struct or_session {
     int n_ctx, n_past;
     uint16_t *kc, *vc; /* [layer][pos][n_kv·128] f16, the reference's cache layout (kv_store.wgsl) */
     float *rope;       /* [n_ctx][64] × (cos, sin) */
+    int r16;           /* the prefill GEMMs on the f16 paths' rounding */
 };
+
+void or_session_set_f16(or_session *s, int on) { s->r16 = on != 0; }
 
 or_session *or_session_new(const or_text_cfg *cfg, const uint8_t *tok_embd, const float *output_norm,
                            const or_layer *layers, int n_ctx) {
@@ -702,16 +705,29 @@ int or_session_n_past(const or_session *s) { return s->n_past; }
 
 void or_session_rewind(or_session *s, int n_past) { s->n_past = n_past; }
 
+static inline float round_f16(float v) { return or_f32_from_f16(or_f16_from_f32(v)); }
+
 /* matmul.wgsl:47-91 (F32 path): Y[M,N] (+)= X[M,K]·Wᵀ with W dequantised exactly, acc = fma(x_k, w_k, acc) over k in
- * order. Blocked over rows of X and columns of W for the CPU; each output's fma chain runs over k in order. */
-static void matmul_q8_0(const float *x, const uint8_t *w, float *y, size_t m, size_t n, size_t k, int acc) {
+ * order. Blocked over rows of X and columns of W for the CPU; each output's fma chain runs over k in order.
+ * r16: the f16 paths (matmul_coop.wgsl:47-70 with load4_q8_0.wgsl, matmul128h): X and the dequantised W (q·d, exact
+ * in f32) rounded to f16 (nearest even) as they enter the tiles, the products summed in f32. */
+static void matmul_q8_0(const float *x_in, const uint8_t *w, float *y, size_t m, size_t n, size_t k, int acc, int r16) {
     float *wt = (float *)malloc(k * n * sizeof(float)); /* [k][n] dequantised */
+    const float *x = x_in;
+    float *xr = NULL;
+    if (r16) {
+        xr = (float *)malloc(m * k * sizeof(float));
+        for (size_t i = 0; i < m * k; i++) {
+            xr[i] = round_f16(x_in[i]);
+        }
+        x = xr;
+    }
 #pragma omp parallel for schedule(static)
     for (size_t c = 0; c < n; c++) {
         float row[8192];
         or_q8_0_dequant(w + 34 * (c * (k / 32)), k, row);
         for (size_t i = 0; i < k; i++) {
-            wt[i * n + c] = row[i];
+            wt[i * n + c] = r16 ? round_f16(row[i]) : row[i];
         }
     }
     enum { MT = 4, NT = 32 };
@@ -751,6 +767,11 @@ static void matmul_q8_0(const float *x, const uint8_t *w, float *y, size_t m, si
         }
     }
     free(wt);
+    free(xr);
+}
+
+void or_matmul_q8_0(const float *x, const uint8_t *w, float *y, size_t m, size_t n, size_t k, int acc, int r16) {
+    matmul_q8_0(x, w, y, m, n, k, acc, r16);
 }
 
 /* embed_q8_0.wgsl:28-38 */
@@ -799,9 +820,9 @@ int or_session_prefill(or_session *s, const int32_t *ids, int l, float *logits) 
         const or_layer *ly = &s->layers[li];
         uint16_t *kc = s->kc + (size_t)li * s->n_ctx * kvd, *vc = s->vc + (size_t)li * s->n_ctx * kvd;
         or_rms_norm(x, ly->attn_norm, h, l, d, c->eps);
-        matmul_q8_0(h, ly->q, qr, l, qd, d, 0);
-        matmul_q8_0(h, ly->k, kr, l, kvd, d, 0);
-        matmul_q8_0(h, ly->v, vr, l, kvd, d, 0);
+        matmul_q8_0(h, ly->q, qr, l, qd, d, 0, s->r16);
+        matmul_q8_0(h, ly->k, kr, l, kvd, d, 0, s->r16);
+        matmul_q8_0(h, ly->v, vr, l, kvd, d, 0, s->r16);
         or_rms_norm(qr, ly->q_norm, q, (size_t)l * c->n_head, 128, c->eps);
         or_rms_norm(kr, ly->k_norm, kn, (size_t)l * c->n_kv, 128, c->eps);
         rope_rows(s, q, l, c->n_head, pos0);
@@ -809,14 +830,14 @@ int or_session_prefill(or_session *s, const int32_t *ids, int l, float *logits) 
         or_f16_from_f32_n(kn, kc + (size_t)pos0 * kvd, l * kvd); /* kv_store.wgsl:18-24 */
         or_f16_from_f32_n(vr, vc + (size_t)pos0 * kvd, l * kvd);
         or_attn_causal(q, kc, vc, kvd, l, pos0, c->n_head, c->n_kv, scale, qr);
-        matmul_q8_0(qr, ly->o, x, l, d, qd, 1);
+        matmul_q8_0(qr, ly->o, x, l, d, qd, 1, s->r16);
         or_rms_norm(x, ly->ffn_norm, h, l, d, c->eps);
-        matmul_q8_0(h, ly->gate, g, l, f, d, 0);
-        matmul_q8_0(h, ly->up, u, l, f, d, 0);
+        matmul_q8_0(h, ly->gate, g, l, f, d, 0, s->r16);
+        matmul_q8_0(h, ly->up, u, l, f, d, 0, s->r16);
         for (size_t i = 0; i < (size_t)l * f; i++) { /* swiglu.wgsl:18-24 */
             g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
         }
-        matmul_q8_0(g, ly->down, x, l, d, f, 1);
+        matmul_q8_0(g, ly->down, x, l, d, f, 1, s->r16);
     }
     /* head (text.rs:655-658): rms_norm + matvec_q8_0 of the last row */
     or_rms_norm(x + (size_t)(l - 1) * d, s->output_norm, h, 1, d, c->eps);

@@ -119,9 +119,16 @@ or_session *or_session_new(const or_text_cfg *cfg, const uint8_t *tok_embd, cons
                            const or_layer *layers, int n_ctx);
 void or_session_free(or_session *s);
 int or_session_n_past(const or_session *s);
-/* TextModel::prefill (text.rs:437-521) on the F32 path's kernels: ids at positions n_past…, logits of the last row
+/* TextModel::prefill (text.rs:437-521), the F32 path's kernels unless or_session_set_f16: ids at positions n_past…,
+ * logits of the last row
  * (head: rms_norm + matvec_q8_0, text.rs:655-658). Returns 0, or −1 on a bad id / overflow */
 int or_session_prefill(or_session *s, const int32_t *ids, int n, float *logits);
+/* the prefill GEMMs with the f16 paths' rounding (matmul_coop_q8_0: X and q·d rounded to f16, f32 sums) when on;
+ * the F32 path's (exact) otherwise. The rest of the prefill is the same on both paths. */
+void or_session_set_f16(or_session *s, int on);
+/* Batch::matmul with a q8_0 weight (gpu.rs:1963-2014): Y[m][n] (+)= X·Wᵀ, W as q8_0 blocks [n][k]; r16: the f16
+ * paths' rounding of X and W */
+void or_matmul_q8_0(const float *x, const uint8_t *w, float *y, size_t m, size_t n, size_t k, int acc, int r16);
 /* record_step (text.rs:540-578) on the f16 paths: embed + layers_fused (text.rs:630-647) + dmv_norm LM head */
 int or_session_step(or_session *s, int32_t tok, float *logits);
 /* rewind to n_past positions (the rows beyond are overwritten by later steps) */

@@ -49,6 +49,8 @@ def lib() -> C.CDLL:
             "or_session_prefill": (i32, [vp, vp, i32, vp]),
             "or_session_step": (i32, [vp, C.c_int32, vp]),
             "or_session_rewind": (None, [vp, i32]),
+            "or_session_set_f16": (None, [vp, i32]),
+            "or_matmul_q8_0": (None, [vp, vp, vp, sz, sz, sz, i32, i32]),
             "or_pixel_lut": (None, [vp, vp, vp]),
             "or_patchify": (None, [vp, i32, i32, i32, i32, vp, vp]),
             "or_rope2d_table": (None, [f32, i32, i32, vp]),
@@ -229,7 +231,8 @@ class Session:
     """The decoder restated (text.rs:437-658): prefill on the F32 path's kernels, steps on the fused f16-path kernels.
     The weights are the same host tensors the library gets (dicts of q8_0 block bytes / f32 norms)."""
 
-    def __init__(self, cfg: dict, tok_embd, output_norm, layers: list[dict], n_ctx: int):
+    def __init__(self, cfg: dict, tok_embd, output_norm, layers: list[dict], n_ctx: int, f16: bool = False):
+        """f16: the prefill GEMMs on the f16 paths' rounding (X and q·d rounded to f16, f32 sums)"""
         self._keep = [tok_embd, output_norm, layers]
         self.cfg = cfg
         c = TextCfg(cfg["n_layer"], cfg["dim"], cfg["n_head"], cfg["n_kv"], 128, cfg["n_ff"], cfg["n_vocab"],
@@ -242,6 +245,7 @@ class Session:
         self.h = lib().or_session_new(C.byref(c), _p(tok_embd), _p(output_norm), arr, n_ctx)
         if not self.h:
             raise ValueError("oracle session: unsupported shape")
+        lib().or_session_set_f16(self.h, int(f16))
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -318,6 +322,19 @@ def q8_0_to_f16(blocks: np.ndarray, rows: int, cols: int, scale: float = 1.0) ->
     blocks = np.ascontiguousarray(blocks, np.uint8)
     lib().or_q8_0_to_f16(_p(blocks), rows * cols, scale, _p(out))
     return out
+
+
+def matmul_q8_0(x: np.ndarray, w_blocks: np.ndarray, n: int, y=None, r16: bool = False) -> np.ndarray:
+    """Batch::matmul with a q8_0 weight (gpu.rs:1963-2014): y (+)= x·Wᵀ, W [n][k] as q8_0 block bytes; r16: the f16
+    paths' rounding of X and W"""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    w_blocks = np.ascontiguousarray(w_blocks, np.uint8)
+    assert w_blocks.size == n * (k // 32) * 34
+    acc = y is not None
+    y = np.zeros((m, n), np.float32) if y is None else np.ascontiguousarray(y, np.float32).copy()
+    lib().or_matmul_q8_0(_p(x), _p(w_blocks), _p(y), m, n, k, int(acc), int(r16))
+    return y
 
 
 def matmul_f16(x16: np.ndarray, w16: np.ndarray, y=None) -> np.ndarray:

@@ -2,7 +2,14 @@
 
 Token identity is checked teacher-forced: at every position the oracle computes its own logits from the tokens the GPU
 chose so far and makes its own choice; a differing token is accepted only as a documented near-tie (the oracle's
-logits of the two tokens within 1e-6 relative). Float logits: rel-L2 against the oracle's f32 restatement."""
+logits of the two tokens within 1e-6 relative). Float logits: rel-L2 against the oracle's f32 restatement.
+
+Both compute paths: the F32 path (exact q8_0 values in the prefill GEMMs) is pinned tightly end to end. The f16 path
+(the default; X and q·d rounded to f16 in the prefill GEMMs, as the reference on a device with f16) is pinned tightly
+per GEMM (test_gemm_gpu); end to end its logits are only defined to the sensitivity of f16 rounding: on the tiny model
+a 1e-7 relative nudge of the embeddings moves the fp64 forward with f16-rounded GEMM operands by 1.0e-3 rel-L2 (the
+f32 forward: 3.7e-6), on config 3's shape a 2e-7 nudge of one norm moves the oracle's f16 prefill by 1.9e-3 — two
+correct f16-path results in different summation orders differ by that much. Bars: 5e-3 (tiny), 1e-2 (config 3)."""
 import numpy as np
 import pytest
 
@@ -13,10 +20,20 @@ from helpers import near_tie, rel_l2, synth_text_model, tiny_prompt, tiny_text_m
 pytestmark = pytest.mark.gpu
 
 
+def model_on(dev, path, cfg, te, on, layers):
+    """a TextModel created on the given compute path (a model keeps the path of its creation)"""
+    keep = dev.compute
+    dev.compute = path
+    try:
+        return htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+
+
 @pytest.fixture(scope="module")
 def tiny(dev):
     cfg, te, on, layers = tiny_text_model()
-    m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    m = model_on(dev, htr.COMPUTE_F32, cfg, te, on, layers)
     yield cfg, te, on, layers, m
     m.free()
 
@@ -148,7 +165,7 @@ def test_full_size_decoder_matches_oracle(dev):
     """config 3's model shape (28 layers, dim 1024, 16 / 8 heads, ffn 3072, vocab 151936, tied head) with a 64-token
     prompt and 24 greedy tokens (rp 1.1, window 64): prefill logits and the decode teacher-forced against the oracle"""
     cfg, te, on, layers = synth_text_model()
-    m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    m = model_on(dev, htr.COMPUTE_F32, cfg, te, on, layers)
     prompt = (np.abs(htr.synth_normal(77, 64)) * 1e5).astype(np.int64) % cfg["n_vocab"]
     n_new = 24
     s = m.session(prompt.size + n_new)
@@ -192,3 +209,80 @@ def test_device_health_is_sticky():
             d.sync()
     assert fired[-1] == ("destroyed", "test: device.destroy()") and len(fired) == 2
     d.close()
+
+
+def test_tiny_prefill_f16_path_matches_oracle(dev):
+    """the f16 compute path (MFMA GEMMs on f16 planes; the tiny model's Q / K / V stack 256 + 128 + 128 rows) against
+    the oracle's f16-path prefill and the fp64 forward with f16-rounded GEMM operands, then 10 CPU-choice steps"""
+    from test_oracle import np_forward
+
+    cfg, te, on, layers = tiny_text_model()
+    m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)
+    prompt = tiny_prompt()
+    s = m.session(prompt.size + 16)
+    o = orc.Session(cfg, te, on, layers, prompt.size + 16, f16=True)
+    lg, lo = s.prefill(prompt), o.prefill(prompt)
+    want16 = np_forward(cfg, te, on, layers, list(prompt), r16=True)[-1]
+    eo, e16 = rel_l2(lg, lo), rel_l2(lg, want16)
+    print(f"\n[tiny prefill f16] rel-L2 vs oracle {eo:.2e}, vs fp64 (f16 operands) {e16:.2e}")
+    assert eo < 5e-3 and e16 < 5e-3
+    for i in range(10):
+        t = int(np.argmax(lo))
+        lg, lo = s.step(t), o.step(t)
+        assert rel_l2(lg, lo) < 5e-3, i
+    s.free()
+    m.free()
+
+
+def test_f16_path_other_shapes_use_the_rounding_tiled_kernel(dev):
+    """a model whose dim (160) is no multiple of 64: the f16 path's GEMMs run the tiled kernel with the same rounding
+    (matmul128h_q8_0) — its prefill against the oracle's f16 path"""
+    g = orc.Lcg(77)
+    dim, n_ff, n_vocab, n_layer = 160, 224, 300, 2
+
+    def w(rows, cols, scale):
+        return orc.q8_0_quantize(g.f32(rows * cols, scale))[0]
+
+    def nv(n):
+        return (1.0 + g.f32(n, 0.05)).astype(np.float32)
+
+    layers = [{"attn_norm": nv(dim), "q": w(256, dim, 0.2), "k": w(128, dim, 0.2), "v": w(128, dim, 0.2),
+               "o": w(dim, 256, 0.1), "q_norm": nv(128), "k_norm": nv(128), "ffn_norm": nv(dim),
+               "gate": w(n_ff, dim, 0.2), "up": w(n_ff, dim, 0.2), "down": w(dim, n_ff, 0.1)} for _ in range(n_layer)]
+    cfg = {"n_layer": n_layer, "dim": dim, "n_head": 2, "n_kv": 1, "d_head": 128, "n_ff": n_ff, "n_vocab": n_vocab,
+           "n_ctx_train": 4096, "eps": 1e-6, "rope_base": 1e6}
+    te, on = w(n_vocab, dim, 1.0), nv(dim)
+    prompt = [int(t) for t in orc.Lcg(5).bits(24) % n_vocab]
+    lo16 = orc.Session(cfg, te, on, layers, 32, f16=True).prefill(prompt)
+    lo32 = orc.Session(cfg, te, on, layers, 32).prefill(prompt)
+    m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)
+    s = m.session(32)
+    lg = s.prefill(prompt)
+    e, e32 = rel_l2(lg, lo16), rel_l2(lg, lo32)
+    print(f"\n[dim 160 prefill f16] rel-L2 vs oracle f16 path {e:.2e}, vs its F32 path {e32:.2e}")
+    assert e < 5e-3
+    s.free()
+    m.free()
+
+
+def test_full_size_decoder_f16_path_matches_oracle(dev):
+    """config 3's shape on the f16 path: prefill logits against the oracle's f16-path prefill (bar 1e-2, the path's
+    sensitivity), then 16 greedy tokens teacher-forced against the oracle"""
+    cfg, te, on, layers = synth_text_model()
+    m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)
+    prompt = (np.abs(htr.synth_normal(78, 64)) * 1e5).astype(np.int64) % cfg["n_vocab"]
+    n_new = 16
+    s = m.session(prompt.size + n_new)
+    lg = s.prefill(prompt)
+    o = orc.Session(cfg, te, on, layers, prompt.size + n_new, f16=True)
+    lo = o.prefill(prompt)
+    e = rel_l2(lg, lo)
+    print(f"\n[full prefill f16] rel-L2 vs oracle {e:.2e}")
+    assert e < 1e-2
+    assert int(np.argmax(lg)) == int(np.argmax(lo)) or near_tie(lo, int(np.argmax(lo)), int(np.argmax(lg)))
+    ch = s.choice(htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new), prompt, 8, 2)
+    toks = s.decode_gpu(ch, n_new)
+    assert len(toks) == n_new
+    ch.free()
+    s.free()
+    m.free()

@@ -81,9 +81,14 @@ def test_gemm_rejects_bad_shapes(dev):
     w = htr.Weight(dev, blocks, 100, 64, f16=True)
     xb = dev.alloc(64 * 2 * 4)
     y = dev.alloc(100 * 4 * 4)
-    with pytest.raises(htr.HtrError, match="multiple of 128"):
+    with pytest.raises(htr.HtrError, match="multiple of 64"):
         htr.gemm_f16(dev, xb, 4, w, y)
     w.free()
+    blocks, _ = f16_weight(1, 192, 64)
+    wg = htr.Weight(dev, blocks, 192, 64, f16=True)
+    with pytest.raises(htr.HtrError, match="multiple of 128"):
+        htr.gemm_ffn_f16(dev, xb, 4, wg, wg, 1.0, y)
+    wg.free()
     wq = htr.Weight(dev, htr.synth_q8_0(1, 128, 64), 128, 64)
     with pytest.raises(htr.HtrError, match="f16 plane"):
         htr.gemm_f16(dev, xb, 4, wq, y)
@@ -128,3 +133,89 @@ def test_ffn_config4_shape(dev):
     assert e < 1e-3
     wg.free()
     wu.free()
+
+
+# the tile shapes the launch picks (the largest with ≥ 128 workgroups on 256 CUs, else the one with the most):
+# (1, 1024, 2048) 64 × 64; (1023, 1024, 3072) 64 × 64 (the prefill's down); (512, 4096, 1024) 128 × 128;
+# (1024, 4032, 64) 128 × 128 with a last tile half past N; (50, 192, 64) 64 × 64 over 3 column tiles
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 2048), (1023, 1024, 3072), (512, 4096, 1024), (1024, 4032, 64),
+                                   (50, 192, 64)])
+def test_gemm_f16_tile_shapes(dev, m, n, k):
+    blocks, w16 = f16_weight(m + 3 * n + k, n, k)
+    x = x16(5 * m + k, m, k, 0.5)
+    w = htr.Weight(dev, blocks, n, k, f16=True)
+    y = dev.upload(np.full((m + 3) * n, np.nan, np.float32))
+    htr.gemm_f16(dev, dev.upload(x), m, w, y)
+    got = y.download(np.float32)
+    want = x.astype(np.float64) @ w16.astype(np.float64).T
+    e = rel_l2(got[: m * n].reshape(m, n), want)
+    print(f"\n[gemm f16 {m}x{n}x{k}] rel-L2 vs fp64 {e:.2e}")
+    assert e < 1e-5
+    assert np.all(np.isnan(got[m * n:]))  # rows past M untouched
+    w.free()
+
+
+@pytest.mark.parametrize("m,n,k", [(1023, 3072, 1024), (5, 128, 64)])
+def test_ffn_f16_tile_shapes(dev, m, n, k):
+    """the prefill's gate / up (128 × 128 tiles), SwiGLU fused, scale 1 (the text FFN). Per element: one f16 rounding
+    of the output (2^-11 relative, bar 2^-10) plus the f32 sums' error in g and u carried through silu(g)·u
+    (|∂/∂g|·δg + |silu(g)|·δu with δ = 2^-20 of the sum of the terms' magnitudes — it matters where g or u nearly
+    cancels over K = 1024)"""
+    bg, wg16 = f16_weight(41, n, k)
+    bu, wu16 = f16_weight(42, n, k)
+    x = x16(43, m, k)
+    wg, wu = htr.Weight(dev, bg, n, k, f16=True), htr.Weight(dev, bu, n, k, f16=True)
+    g16 = dev.alloc(m * n * 2)
+    htr.gemm_ffn_f16(dev, dev.upload(x), m, wg, wu, 1.0, g16)
+    got = g16.download(np.float16).reshape(m, n).astype(np.float64)
+    x64, wg64, wu64 = x.astype(np.float64), wg16.astype(np.float64), wu16.astype(np.float64)
+    g, u = x64 @ wg64.T, x64 @ wu64.T
+    sig = 1 / (1 + np.exp(-g))
+    want = g * sig * u
+    dg, du = 2.0 ** -20 * (np.abs(x64) @ np.abs(wg64).T), 2.0 ** -20 * (np.abs(x64) @ np.abs(wu64).T)
+    bound = np.abs(want) * 2.0 ** -10 + np.abs(sig * (1 + g * (1 - sig)) * u) * dg + np.abs(g * sig) * du + 1e-7
+    err = np.abs(got - want)
+    worst = np.unravel_index(np.argmax(err / bound), err.shape)
+    assert np.all(err <= bound), (f"{int(np.sum(err > bound))} elements; worst {worst}: got {got[worst]}, "
+                                  f"want {want[worst]}, g {g[worst]}, u {u[worst]}, bound {bound[worst]}")
+    wg.free()
+    wu.free()
+
+
+@pytest.mark.parametrize("m,n,k", [(7, 96, 256), (70, 100, 96), (130, 64, 32), (64, 192, 1024)])
+def test_matmul_q8_0_on_both_compute_paths(dev, m, n, k):
+    """Batch::matmul with a q8_0 weight (gpu.rs:1963-2014) on the F32 path (exact dequant, f32 sums) and the f16 path
+    (X and q·d rounded to f16, f32 sums) against the oracle's restatement of each (bar 1e-5: f32 summation order). Each
+    result must also sit far closer to its own path's oracle than to the other path's — a dropped or extra rounding
+    fails (the two paths differ by about 3e-4 here)."""
+    import oracle as orc
+
+    blocks = htr.synth_q8_0(m + n + k, n, k)
+    x = htr.synth_normal(3 * m + k, m * k).reshape(m, k)
+    base = htr.synth_normal(9, m * n).reshape(m, n)
+    w = htr.Weight(dev, blocks, n, k)
+    xb = dev.upload(x)
+    want = {p: orc.matmul_q8_0(x, blocks, n, r16=p == htr.COMPUTE_F16) for p in (htr.COMPUTE_F32, htr.COMPUTE_F16)}
+    keep = dev.compute
+    try:
+        for path in (htr.COMPUTE_F32, htr.COMPUTE_F16):
+            other = htr.COMPUTE_F16 if path == htr.COMPUTE_F32 else htr.COMPUTE_F32
+            dev.compute = path
+            y = dev.upload(base)
+            htr.matmul_q8_0(dev, xb, m, w, y, acc=True)
+            got = y.download(np.float32).reshape(m, n) - base
+            e, e_other = rel_l2(got, want[path]), rel_l2(got, want[other])
+            print(f"\n[matmul q8_0 {m}x{n}x{k} path {path}] vs oracle {e:.2e}, vs the other path {e_other:.2e}")
+            assert e < 1e-5
+            assert e_other > 20 * e
+    finally:
+        dev.compute = keep
+    w.free()
+
+
+def test_compute_path_setting(dev):
+    keep = dev.compute
+    assert keep in (htr.COMPUTE_F32, htr.COMPUTE_F16)
+    with pytest.raises(htr.HtrError, match="compute path"):
+        dev.compute = 7
+    assert dev.compute == keep

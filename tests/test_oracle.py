@@ -319,18 +319,26 @@ def test_choose_nan_and_all_neg_inf():
 
 # ---- the decoder ----------------------------------------------------------------------------------------------------
 
-def np_forward(cfg, tok_embd, output_norm, layers, ids):
+def np_forward(cfg, tok_embd, output_norm, layers, ids, r16=False):
     """An fp64 forward of the Qwen3 graph (text.rs:1-19) over `ids`, K / V rounded to f16 like the cache:
-    → logits of every position"""
+    → logits of every position. r16: every layer GEMM's operands (X and the dequantised W) rounded to f16 first, the
+    f16 compute paths' prefill (matmul_coop_q8_0); the LM head stays exact (a matvec on every path)"""
     d, nh, nkv, f, V, eps = cfg["dim"], cfg["n_head"], cfg["n_kv"], cfg["n_ff"], cfg["n_vocab"], cfg["eps"]
     E = np_dequant(tok_embd, V, d)
     x = E[np.asarray(ids)]
     n = x.shape[0]
+
+    def mm(a, w, rows, cols):
+        W = np_dequant(w, rows, cols)
+        if r16:
+            a, W = a.astype(np.float16).astype(np.float64), W.astype(np.float16).astype(np.float64)
+        return a @ W.T
+
     for ly in layers:
         h = np_rms(x, ly["attn_norm"], eps)
-        q = h @ np_dequant(ly["q"], nh * 128, d).T
-        k = h @ np_dequant(ly["k"], nkv * 128, d).T
-        v = h @ np_dequant(ly["v"], nkv * 128, d).T
+        q = mm(h, ly["q"], nh * 128, d)
+        k = mm(h, ly["k"], nkv * 128, d)
+        v = mm(h, ly["v"], nkv * 128, d)
         q = np_rms(q.reshape(n, nh, 128), ly["q_norm"], eps)
         k = np_rms(k.reshape(n, nkv, 128), ly["k_norm"], eps)
         pos = np.arange(n)[:, None, None]
@@ -344,11 +352,11 @@ def np_forward(cfg, tok_embd, output_norm, layers, ids):
         a = np.zeros((n, nh, 128))
         for t in range(n):
             a[t] = np_attention(q[t], k[: t + 1], v[: t + 1], 1 / np.sqrt(128))
-        x = x + a.reshape(n, -1) @ np_dequant(ly["o"], d, nh * 128).T
+        x = x + mm(a.reshape(n, -1), ly["o"], d, nh * 128)
         h = np_rms(x, ly["ffn_norm"], eps)
-        g = h @ np_dequant(ly["gate"], f, d).T
-        u = h @ np_dequant(ly["up"], f, d).T
-        x = x + (g / (1 + np.exp(-g)) * u) @ np_dequant(ly["down"], d, f).T
+        g = mm(h, ly["gate"], f, d)
+        u = mm(h, ly["up"], f, d)
+        x = x + mm(g / (1 + np.exp(-g)) * u, ly["down"], d, f)
     return np_rms(x, output_norm, eps) @ E.T
 
 
@@ -368,6 +376,38 @@ def test_oracle_decoder_matches_fp64_forward():
         w = want[len(prompt) - 1 + i]
         assert rel_l2(lg, w) < 1e-3, i
         assert int(np.argmax(lg)) == int(np.argmax(w)), i
+
+
+@pytest.mark.parametrize("m,n,k", [(7, 96, 256), (33, 64, 1024)])
+def test_oracle_matmul_q8_0_both_paths_match_numpy(m, n, k):
+    """Batch::matmul with a q8_0 weight (gpu.rs:1963-2014): the F32 path against the fp64 product of the exact
+    dequant, the f16 paths (matmul_coop_q8_0 / matmul128h: X and q·d rounded to f16 by numpy's own conversion) against
+    the fp64 product of the rounded operands — f32 summation bar 1e-6; the two paths differ by ~3e-4, so a dropped or
+    misplaced rounding fails"""
+    rng = np.random.default_rng(m * n + k)
+    blocks, _ = orc.q8_0_quantize(rng.normal(0, 0.3, n * k).astype(np.float32))
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    W = np_dequant(blocks, n, k)
+    ref32 = x.astype(np.float64) @ W.T
+    ref16 = x.astype(np.float16).astype(np.float64) @ W.astype(np.float16).astype(np.float64).T
+    y32, y16 = orc.matmul_q8_0(x, blocks, n), orc.matmul_q8_0(x, blocks, n, r16=True)
+    assert rel_l2(y32, ref32) < 1e-6 and rel_l2(y16, ref16) < 1e-6
+    assert rel_l2(ref16, ref32) > 1e-4
+    base = rng.normal(0, 1, (m, n)).astype(np.float32)
+    assert rel_l2(orc.matmul_q8_0(x, blocks, n, y=base, r16=True) - base, ref16) < 1e-5
+
+
+def test_oracle_f16_prefill_matches_fp64_forward_with_rounded_operands():
+    """the oracle's f16-path prefill against the fp64 forward whose layer GEMMs take f16-rounded X and W, on the
+    reference's tiny model. The bar (5e-3) is the path's own sensitivity: a 1e-7 relative nudge of the embeddings moves
+    that fp64 forward by 1.0e-3 (its f32-path twin: 3.7e-6), so two correct f16-path results differ at that level;
+    the F32 path's prefill stays pinned at 1e-3 above and matches its forward to 3e-5"""
+    cfg, te, on, layers = tiny_text_model()
+    prompt = tiny_prompt()
+    want16 = np_forward(cfg, te, on, layers, list(prompt), r16=True)[-1]
+    got = orc.Session(cfg, te, on, layers, 32, f16=True).prefill(prompt)
+    assert rel_l2(got, want16) < 5e-3
+    assert int(np.argmax(got)) == int(np.argmax(want16))
 
 
 def test_oracle_step_equals_prefill_row():
