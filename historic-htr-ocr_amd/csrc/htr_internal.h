@@ -173,6 +173,29 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
 int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
                         const htr_weight *wk, const htr_weight *wv, float *q, float *k, float *v);
 
+// GGUF (gguf.hip): tensor lookup, metadata, the streaming upload through two pinned buffers
+typedef htr_gguf_tensor_info GgufTensor;
+enum { GGUF_F32 = HTR_GGML_F32, GGUF_F16 = HTR_GGML_F16, GGUF_Q8_0 = HTR_GGML_Q8_0, GGUF_BF16 = HTR_GGML_BF16 };
+struct GgufStager {
+    htr_device *dev = nullptr;
+    void *host[2] = {nullptr, nullptr};     // pinned
+    void *dev_buf[2] = {nullptr, nullptr};  // device staging
+    hipEvent_t ev[2] = {nullptr, nullptr};  // the last copy out of each
+    int next = 0;
+    int init(htr_device *d);
+    ~GgufStager();
+};
+int gguf_find(htr_gguf *g, const char *name, const GgufTensor **out);
+bool gguf_has(htr_gguf *g, const char *name);
+bool gguf_has_key(htr_gguf *g, const char *key);
+int gguf_meta_u32(htr_gguf *g, const char *key, uint32_t *out);
+int gguf_meta_f32(htr_gguf *g, const char *key, float *out);
+int gguf_meta_str(htr_gguf *g, const char *key, std::string *out);
+// a q8_0 [rows][cols] weight (GGUF shape [cols, rows]) / an F32 [n] vector streamed onto the device (enqueued on the
+// device's stream: synchronise before the staging goes away)
+int gguf_upload_q8_0(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t rows, size_t cols, htr_weight **out);
+int gguf_upload_f32(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t n, float **out);
+
 // the vision encoder's other kernels (vision.hip)
 int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const float *lut, int w, int px, int n,
                     int side, float *P);

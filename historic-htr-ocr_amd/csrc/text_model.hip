@@ -224,12 +224,66 @@ extern "C" int htr_text_model_free(htr_text_model *m) {
     return 0;
 }
 
-extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg, const void *tok_embd,
-                                     const float *output_norm, const htr_layer_tensors *layers, htr_text_model **out) {
-    HTR_TRY(htr_check_alive(dev));
-    if (!cfg || !layers || !out) return htr_fail("htr_text_model_create: null argument");
-    HTR_TRY(check_model_cfg(*cfg));
-    const htr_text_config &c = *cfg;
+namespace {
+
+// where a model's tensors come from: host arrays (htr_text_model_create) or a GGUF file (htr_text_model_load_gguf).
+// layer < 0: the model-level tensors (token_embd, output_norm)
+struct TensorFeed {
+    virtual int q8(int layer, const char *kind, size_t rows, size_t cols, htr_weight **out) = 0;
+    virtual int vec(int layer, const char *kind, size_t n, float **out) = 0;
+    virtual ~TensorFeed() = default;
+};
+
+struct ArrayFeed : TensorFeed {
+    const htr_layer_tensors *layers;
+    const void *tok_embd;
+    const float *output_norm;
+    ArrayFeed(const htr_layer_tensors *l, const void *te, const float *on) : layers(l), tok_embd(te), output_norm(on) {}
+    int q8(int layer, const char *kind, size_t rows, size_t cols, htr_weight **out) override {
+        const void *h = tok_embd;
+        if (layer >= 0) {
+            const htr_layer_tensors &t = layers[layer];
+            const std::string k = kind;
+            h = k == "attn_q" ? t.q : k == "attn_k" ? t.k : k == "attn_v" ? t.v : k == "attn_output" ? t.o
+                : k == "ffn_gate" ? t.gate : k == "ffn_up" ? t.up : t.down;
+        }
+        return upload_w(dev_, h, rows, cols, kind, out);
+    }
+    int vec(int layer, const char *kind, size_t n, float **out) override {
+        const float *h = output_norm;
+        if (layer >= 0) {
+            const htr_layer_tensors &t = layers[layer];
+            const std::string k = kind;
+            h = k == "attn_norm" ? t.attn_norm : k == "attn_q_norm" ? t.q_norm : k == "attn_k_norm" ? t.k_norm
+                : t.ffn_norm;
+        }
+        return upload_vec(dev_, h, n, out);
+    }
+    htr_device *dev_ = nullptr;
+};
+
+struct GgufFeed : TensorFeed {
+    htr_gguf *g;
+    GgufStager sg;
+    explicit GgufFeed(htr_gguf *gg) : g(gg) {}
+    static std::string name(int layer, const char *kind) {
+        return layer < 0 ? std::string(kind) + ".weight" : "blk." + std::to_string(layer) + "." + kind + ".weight";
+    }
+    int q8(int layer, const char *kind, size_t rows, size_t cols, htr_weight **out) override {
+        const GgufTensor *t;
+        HTR_TRY(gguf_find(g, name(layer, kind).c_str(), &t));
+        return gguf_upload_q8_0(sg, g, *t, rows, cols, out);
+    }
+    int vec(int layer, const char *kind, size_t n, float **out) override {
+        const GgufTensor *t;
+        HTR_TRY(gguf_find(g, name(layer, kind).c_str(), &t));
+        return gguf_upload_f32(sg, g, *t, n, out);
+    }
+};
+
+// TextModel::load's body (text.rs:332-375) over either feed; the f16 planes of the f16 path made after the upload
+int build_model(htr_device *dev, const htr_text_config &c, TensorFeed &feed, htr_text_model **out) {
+    HTR_TRY(check_model_cfg(c));
     const size_t d = c.dim, f = c.n_ff, qd = (size_t)c.n_head * HEAD, kvd = (size_t)c.n_kv * HEAD;
     auto *m = new htr_text_model;
     m->dev = dev;
@@ -237,23 +291,22 @@ extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg
     m->layers.resize(c.n_layer);
     int rc = 0;
     for (int i = 0; i < c.n_layer && rc == 0; i++) {
-        const htr_layer_tensors &t = layers[i];
         Layer &l = m->layers[i];
-        rc = upload_vec(dev, t.attn_norm, d, &l.attn_norm);
-        if (rc == 0) rc = upload_w(dev, t.q, qd, d, "attn_q", &l.q);
-        if (rc == 0) rc = upload_w(dev, t.k, kvd, d, "attn_k", &l.k);
-        if (rc == 0) rc = upload_w(dev, t.v, kvd, d, "attn_v", &l.v);
-        if (rc == 0) rc = upload_w(dev, t.o, d, qd, "attn_output", &l.o);
-        if (rc == 0) rc = upload_vec(dev, t.q_norm, HEAD, &l.q_norm);
-        if (rc == 0) rc = upload_vec(dev, t.k_norm, HEAD, &l.k_norm);
-        if (rc == 0) rc = upload_vec(dev, t.ffn_norm, d, &l.ffn_norm);
-        if (rc == 0) rc = upload_w(dev, t.gate, f, d, "ffn_gate", &l.gate);
-        if (rc == 0) rc = upload_w(dev, t.up, f, d, "ffn_up", &l.up);
-        if (rc == 0) rc = upload_w(dev, t.down, d, f, "ffn_down", &l.down);
+        rc = feed.vec(i, "attn_norm", d, &l.attn_norm);
+        if (rc == 0) rc = feed.q8(i, "attn_q", qd, d, &l.q);
+        if (rc == 0) rc = feed.q8(i, "attn_k", kvd, d, &l.k);
+        if (rc == 0) rc = feed.q8(i, "attn_v", kvd, d, &l.v);
+        if (rc == 0) rc = feed.q8(i, "attn_output", d, qd, &l.o);
+        if (rc == 0) rc = feed.vec(i, "attn_q_norm", HEAD, &l.q_norm);
+        if (rc == 0) rc = feed.vec(i, "attn_k_norm", HEAD, &l.k_norm);
+        if (rc == 0) rc = feed.vec(i, "ffn_norm", d, &l.ffn_norm);
+        if (rc == 0) rc = feed.q8(i, "ffn_gate", f, d, &l.gate);
+        if (rc == 0) rc = feed.q8(i, "ffn_up", f, d, &l.up);
+        if (rc == 0) rc = feed.q8(i, "ffn_down", d, f, &l.down);
         if (rc < 0) rc = htr_fail("blk.%d: %s", i, std::string(htr_last_error()).c_str());
     }
-    if (rc == 0) rc = upload_w(dev, tok_embd, c.n_vocab, d, "token_embd", &m->tok_embd);
-    if (rc == 0) rc = upload_vec(dev, output_norm, d, &m->output_norm);
+    if (rc == 0) rc = feed.q8(-1, "token_embd", c.n_vocab, d, &m->tok_embd);
+    if (rc == 0) rc = feed.vec(-1, "output_norm", d, &m->output_norm);
     // the f16 compute path's prefill GEMMs read f16(q·d) planes (matmul_coop_q8_0 rounds the dequantised W to f16 as
     // it loads a tile); the MFMA kernels take rows in multiples of 64 (the FFN's 128), else the tiled kernel rounds
     m->compute = dev->compute;
@@ -263,13 +316,87 @@ extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg
         for (htr_weight *w : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down})
             if (rc == 0) rc = weight_attach_f16(dev, dev->stream, w);
     }
-    if (rc == 0 && m->mfma16) rc = htr_sync(dev);
+    if (rc == 0) rc = htr_sync(dev);
     if (rc < 0) {
         std::string keep = htr_last_error();
+        htr_sync(dev);  // nothing in flight still reads the staging the caller frees next
         htr_text_model_free(m);
         return htr_fail("%s", keep.c_str());
     }
     *out = m;
+    return 0;
+}
+
+// TextConfig::from_gguf (text.rs:43-76)
+int config_from_gguf(htr_gguf *g, htr_text_config *c) {
+    std::string arch;
+    HTR_TRY(gguf_meta_str(g, "general.architecture", &arch));
+    if (arch != "qwen3") return htr_fail("architecture \"%s\": this engine runs qwen3 only", arch.c_str());
+    auto u = [&](const char *k, int *out) -> int {
+        uint32_t v;
+        HTR_TRY(gguf_meta_u32(g, (std::string("qwen3.") + k).c_str(), &v));
+        if (v > (uint32_t)INT32_MAX) return htr_fail("qwen3.%s = %u", k, v);
+        *out = (int)v;
+        return 0;
+    };
+    int d_head, v_len;
+    HTR_TRY(u("attention.key_length", &d_head));
+    HTR_TRY(u("attention.value_length", &v_len));
+    if (d_head != HEAD || v_len != HEAD) return htr_fail("head dim %d: the attention kernels are written for 128", d_head);
+    c->d_head = d_head;
+    HTR_TRY(u("attention.head_count", &c->n_head));
+    HTR_TRY(u("attention.head_count_kv", &c->n_kv));
+    if (c->n_kv == 0 || c->n_head % c->n_kv != 0) return htr_fail("%d q heads on %d kv heads", c->n_head, c->n_kv);
+    if (gguf_has_key(g, "qwen3.rope.scaling.type") || gguf_has_key(g, "qwen3.rope.dimension_count"))
+        return htr_fail("rope scaling / partial rope in the GGUF: not part of this engine's graph");
+    const GgufTensor *tok;
+    HTR_TRY(gguf_find(g, "token_embd.weight", &tok));
+    HTR_TRY(u("block_count", &c->n_layer));
+    HTR_TRY(u("embedding_length", &c->dim));
+    HTR_TRY(u("feed_forward_length", &c->n_ff));
+    HTR_TRY(gguf_meta_f32(g, "qwen3.attention.layer_norm_rms_epsilon", &c->eps));
+    HTR_TRY(gguf_meta_f32(g, "qwen3.rope.freq_base", &c->rope_base));
+    const uint64_t nv = tok->shape[tok->n_dims - 1];
+    if (nv > (uint64_t)INT32_MAX) return htr_fail("token_embd: %llu rows", (unsigned long long)nv);
+    c->n_vocab = (int)nv;
+    HTR_TRY(u("context_length", &c->n_ctx_train));
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int htr_text_model_create(htr_device *dev, const htr_text_config *cfg, const void *tok_embd,
+                                     const float *output_norm, const htr_layer_tensors *layers, htr_text_model **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!cfg || !layers || !out) return htr_fail("htr_text_model_create: null argument");
+    ArrayFeed feed(layers, tok_embd, output_norm);
+    feed.dev_ = dev;
+    return build_model(dev, *cfg, feed, out);
+}
+
+// text.rs:332-375 TextModel::load
+extern "C" int htr_text_model_load_gguf(htr_device *dev, htr_gguf *g, htr_text_model **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!g || !out) return htr_fail("htr_text_model_load_gguf: null argument");
+    htr_text_config c{};
+    HTR_TRY(config_from_gguf(g, &c));
+    for (int i = 0; i < c.n_layer; i++) {
+        for (const char *absent : {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"}) {
+            const std::string b = "blk." + std::to_string(i) + "." + absent + ".bias";
+            if (gguf_has(g, b.c_str())) return htr_fail("%s is in the GGUF but not part of this engine's graph", b.c_str());
+        }
+        if (gguf_has(g, ("blk." + std::to_string(i) + ".attn_qkv.weight").c_str()))
+            return htr_fail("blk.%d: a fused attn_qkv — this engine reads separate q / k / v", i);
+    }
+    if (gguf_has(g, "output.weight")) return htr_fail("output.weight is in the GGUF: this engine ties the output to token_embd");
+    GgufFeed feed(g);
+    HTR_TRY(feed.sg.init(dev));
+    return build_model(dev, c, feed, out);
+}
+
+extern "C" int htr_text_model_config(htr_text_model *m, htr_text_config *out) {
+    if (!m || !out) return htr_fail("htr_text_model_config: null argument");
+    *out = m->cfg;
     return 0;
 }
 

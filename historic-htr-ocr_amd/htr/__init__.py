@@ -29,7 +29,10 @@ SYMBOLS = [
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
     "htr_choose_many", "htr_matmul_q8_0", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
-    "htr_vision_out_shape", "htr_vision_encode", "htr_text_model_create", "htr_text_model_free", "htr_session_create", "htr_session_free",
+    "htr_vision_out_shape", "htr_vision_encode", "htr_gguf_open", "htr_gguf_open_source", "htr_gguf_close",
+    "htr_gguf_header", "htr_gguf_tensor", "htr_gguf_u32", "htr_gguf_f32", "htr_gguf_str", "htr_gguf_f32_array",
+    "htr_gguf_read_small", "htr_text_model_create", "htr_text_model_free", "htr_text_model_load_gguf",
+    "htr_text_model_config", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
 ]
@@ -52,6 +55,15 @@ class TextConfigC(C.Structure):
 class LayerTensorsC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "attn_norm", "q_norm", "k_norm",
                                           "ffn_norm")]
+
+
+class GgufTensorC(C.Structure):
+    _fields_ = [("name", C.c_char * 128), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("shape", C.c_uint64 * 4),
+                ("n_elements", C.c_uint64), ("n_bytes", C.c_uint64), ("offset", C.c_uint64),
+                ("file_offset", C.c_uint64)]
+
+
+READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint64, C.c_void_p, C.c_size_t)
 
 
 class PresetC(C.Structure):
@@ -125,8 +137,21 @@ def lib() -> C.CDLL:
             "htr_vision_free": (i32, [vp]),
             "htr_vision_out_shape": (i32, [vp, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)]),
             "htr_vision_encode": (i32, [vp, vp, i32, i32, i32, vp]),
+            "htr_gguf_open": (i32, [C.c_char_p, pp]),
+            "htr_gguf_open_source": (i32, [C.c_uint64, READ_FN, vp, pp]),
+            "htr_gguf_close": (i32, [vp]),
+            "htr_gguf_header": (i32, [vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                      C.POINTER(sz)]),
+            "htr_gguf_tensor": (i32, [vp, C.c_char_p, sz, C.POINTER(GgufTensorC)]),
+            "htr_gguf_u32": (i32, [vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+            "htr_gguf_f32": (i32, [vp, C.c_char_p, C.POINTER(f32)]),
+            "htr_gguf_str": (i32, [vp, C.c_char_p, C.c_char_p, sz, C.POINTER(sz)]),
+            "htr_gguf_f32_array": (i32, [vp, C.c_char_p, vp, sz, C.POINTER(sz)]),
+            "htr_gguf_read_small": (i32, [vp, C.c_char_p, vp, sz]),
             "htr_text_model_create": (i32, [vp, C.POINTER(TextConfigC), vp, vp, C.POINTER(LayerTensorsC), pp]),
             "htr_text_model_free": (i32, [vp]),
+            "htr_text_model_load_gguf": (i32, [vp, vp, pp]),
+            "htr_text_model_config": (i32, [vp, C.POINTER(TextConfigC)]),
             "htr_session_create": (i32, [vp, sz, pp]),
             "htr_session_free": (i32, [vp]),
             "htr_session_n_past": (i32, [vp, C.POINTER(sz)]),
@@ -406,9 +431,99 @@ class Preset:
                        self.repetition_window, self.max_new_tokens)
 
 
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+
+
+class Gguf:
+    """ocr-gguf Gguf (lib.rs:1-401): the parsed header of a GGUF file (or of bytes in memory, read through the
+    TensorSource callback); the tensors' bytes are read on demand."""
+
+    def __init__(self, path=None, data: bytes | None = None):
+        h = C.c_void_p()
+        if data is not None:
+            self._data = bytes(data)
+
+            def read(_user, off, buf, n):
+                if off + n > len(self._data):
+                    return 1
+                C.memmove(buf, self._data[off:off + n], n)
+                return 0
+
+            self._read = READ_FN(read)
+            _check(lib().htr_gguf_open_source(len(self._data), self._read, None, C.byref(h)))
+        else:
+            _check(lib().htr_gguf_open(str(path).encode(), C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().htr_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def header(self) -> dict:
+        v, al, off, n = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_size_t()
+        _check(lib().htr_gguf_header(self.h, C.byref(v), C.byref(al), C.byref(off), C.byref(n)))
+        return {"version": v.value, "alignment": al.value, "data_offset": off.value, "n_tensors": n.value}
+
+    def info(self, name: str | None = None, index: int = 0) -> dict:
+        t = GgufTensorC()
+        _check(lib().htr_gguf_tensor(self.h, None if name is None else name.encode(), index, C.byref(t)))
+        return {"name": t.name.decode(), "type": t.type, "shape": list(t.shape[: t.n_dims]), "n_bytes": t.n_bytes,
+                "offset": t.offset, "file_offset": t.file_offset}
+
+    def u32(self, key: str) -> int:
+        v = C.c_uint32()
+        _check(lib().htr_gguf_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def f32(self, key: str) -> float:
+        v = C.c_float()
+        _check(lib().htr_gguf_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def str(self, key: str) -> str:
+        n = C.c_size_t()
+        _check(lib().htr_gguf_str(self.h, key.encode(), None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        _check(lib().htr_gguf_str(self.h, key.encode(), buf, n.value + 1, None))
+        return buf.raw[: n.value].decode()
+
+    def f32_array(self, key: str) -> np.ndarray:
+        n = C.c_size_t()
+        _check(lib().htr_gguf_f32_array(self.h, key.encode(), None, 0, C.byref(n)))
+        out = np.empty(n.value, np.float32)
+        _check(lib().htr_gguf_f32_array(self.h, key.encode(), _ptr(out), n.value, None))
+        return out
+
+    def read_small(self, name: str) -> np.ndarray:
+        nb = self.info(name)["n_bytes"]
+        out = np.empty(nb, np.uint8)
+        _check(lib().htr_gguf_read_small(self.h, name.encode(), _ptr(out), nb))
+        return out
+
+
 class TextModel:
     """TextModel::load (text.rs:332-375) from host tensors: ``layers`` is a list of dicts with the q8_0 block bytes
-    (q, k, v, o, gate, up, down) and f32 norms (attn_norm, q_norm, k_norm, ffn_norm)."""
+    (q, k, v, o, gate, up, down) and f32 norms (attn_norm, q_norm, k_norm, ffn_norm). ``TextModel.from_gguf`` loads
+    one from a GGUF file instead."""
+
+    @classmethod
+    def from_gguf(cls, dev: Device, g: Gguf) -> "TextModel":
+        self = cls.__new__(cls)
+        h = C.c_void_p()
+        _check(lib().htr_text_model_load_gguf(dev.h, g.h, C.byref(h)))
+        self.dev, self.h = dev, h.value
+        c = TextConfigC()
+        _check(lib().htr_text_model_config(self.h, C.byref(c)))
+        self.cfg = TextConfig(c.n_layer, c.dim, c.n_head, c.n_kv, c.d_head, c.n_ff, c.n_vocab, c.n_ctx_train, c.eps,
+                              c.rope_base)
+        return self
 
     def __init__(self, dev: Device, cfg: TextConfig, tok_embd: np.ndarray, output_norm: np.ndarray,
                  layers: list[dict]):

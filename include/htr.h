@@ -175,6 +175,40 @@ int htr_vision_out_shape(htr_vision *v, int width, int height, int n_layers, siz
 /* Vision::encode_gpu (vision.rs:258-263): RGB bytes [height][width][3] → d_out (device memory of the shape above) */
 int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width, int height, int n_layers, float *d_out);
 
+/* ---- GGUF files (ocr-gguf lib.rs:1-401: Gguf / TensorSource / TensorInfo) --------------------------------------- */
+typedef struct htr_gguf htr_gguf;
+/* ggml types the reader accepts (lib.rs:98-130); any other is an error */
+enum { HTR_GGML_F32 = 0, HTR_GGML_F16 = 1, HTR_GGML_Q8_0 = 8, HTR_GGML_BF16 = 30 };
+typedef struct {
+    char name[128];
+    uint32_t type;         /* HTR_GGML_* */
+    uint32_t n_dims;       /* 1 … 4 */
+    uint64_t shape[4];     /* ggml order: shape[0] is the contiguous (innermost) dimension */
+    uint64_t n_elements, n_bytes;
+    uint64_t offset;       /* from the start of the data section */
+    uint64_t file_offset;  /* absolute */
+} htr_gguf_tensor_info;
+/* TensorSource::read_at: fill buf with the len bytes at off; 0, or nonzero on failure */
+typedef int (*htr_read_fn)(void *user, uint64_t off, void *buf, size_t len);
+/* Gguf::open / Gguf::from_source (lib.rs:316-346): the header (GGUF v2 / v3) parsed from a prefix of the source
+ * (1 MiB, doubled while the header is longer); every tensor must end inside the source. The tensors' bytes are read
+ * on demand. The file is read with pread (no mapping). */
+int htr_gguf_open(const char *path, htr_gguf **out);
+int htr_gguf_open_source(uint64_t len, htr_read_fn read, void *user, htr_gguf **out);
+int htr_gguf_close(htr_gguf *g);
+/* version, general.alignment (default 32), the data section's offset, the tensor count */
+int htr_gguf_header(htr_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset, size_t *n_tensors);
+/* TensorInfo by name (Gguf::info), or by file order when name is NULL */
+int htr_gguf_tensor(htr_gguf *g, const char *name, size_t index, htr_gguf_tensor_info *out);
+/* metadata (Gguf::u32 — a non-negative i32 reads too —, Gguf::f32, Gguf::str, Gguf::f32_array): the length of a
+ * string / array is written to *len; a string is cut to cap − 1 bytes and terminated */
+int htr_gguf_u32(htr_gguf *g, const char *key, uint32_t *out);
+int htr_gguf_f32(htr_gguf *g, const char *key, float *out);
+int htr_gguf_str(htr_gguf *g, const char *key, char *buf, size_t cap, size_t *len);
+int htr_gguf_f32_array(htr_gguf *g, const char *key, float *out, size_t cap, size_t *len);
+/* Gguf::read_small (lib.rs:484-493): a tensor of at most 1 MiB, raw bytes */
+int htr_gguf_read_small(htr_gguf *g, const char *name, void *buf, size_t cap);
+
 /* ---- the text decoder (text.rs:30-130 TextConfig / TextModel, text.rs:332-375 load) ------------------------------ */
 typedef struct {
     int n_layer, dim, n_head, n_kv, d_head, n_ff, n_vocab, n_ctx_train;
@@ -191,6 +225,12 @@ typedef struct {
 int htr_text_model_create(htr_device *dev, const htr_text_config *cfg, const void *tok_embd, const float *output_norm,
                           const htr_layer_tensors *layers, htr_text_model **out);
 int htr_text_model_free(htr_text_model *m);
+/* TextModel::load from a GGUF (text.rs:43-76 TextConfig::from_gguf, text.rs:101-118 weight / vector, text.rs:332-375):
+ * the qwen3.* metadata, the same shape / type / absent-tensor checks, the q8_0 projections streamed file → device
+ * through two pinned 32 MiB buffers and repacked on the device (never a whole tensor in host memory) */
+int htr_text_model_load_gguf(htr_device *dev, htr_gguf *g, htr_text_model **out);
+/* the configuration a model was built with */
+int htr_text_model_config(htr_text_model *m, htr_text_config *out);
 
 /* TextModel::session (text.rs:378-434): n_ctx positions (prompt + new tokens); the KV cache is sized once to n_ctx */
 int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out);
