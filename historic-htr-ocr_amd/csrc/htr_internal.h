@@ -173,6 +173,9 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
 int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
                         const htr_weight *wk, const htr_weight *wv, float *q, float *k, float *v);
 
+// the vocabulary of a session's model (text_model.hip)
+int session_n_vocab(const htr_session *s);
+
 // GGUF (gguf.hip): tensor lookup, metadata, the streaming upload through two pinned buffers
 typedef htr_gguf_tensor_info GgufTensor;
 enum { GGUF_F32 = HTR_GGML_F32, GGUF_F16 = HTR_GGML_F16, GGUF_Q8_0 = HTR_GGML_Q8_0, GGUF_BF16 = HTR_GGML_BF16 };

@@ -469,6 +469,8 @@ extern "C" int htr_session_logits(htr_session *s, float *h_logits) {
     return htr_download(s->dev, h_logits, s->logits, (size_t)s->m->cfg.n_vocab * 4);
 }
 
+int session_n_vocab(const htr_session *s) { return s->m->cfg.n_vocab; }
+
 extern "C" int htr_session_rewind(htr_session *s, size_t n_past) {
     if (!s) return htr_fail("htr_session_rewind: null session");
     if (n_past > (size_t)s->n_past) return htr_fail("rewind to %zu: the session is at %d", n_past, s->n_past);

@@ -34,7 +34,7 @@ SYMBOLS = [
     "htr_gguf_read_small", "htr_text_model_create", "htr_text_model_free", "htr_text_model_load_gguf",
     "htr_text_model_config", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
-    "htr_decode_gpu", "htr_synth_q8_0", "htr_synth_normal",
+    "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
 ]
 
 
@@ -164,6 +164,9 @@ def lib() -> C.CDLL:
             "htr_decode_gpu": (i32, [vp, vp, sz, TOKEN_CB, vp]),
             "htr_synth_q8_0": (i32, [C.c_uint64, sz, sz, vp]),
             "htr_synth_normal": (i32, [C.c_uint64, sz, f32, f32, vp]),
+            "htr_choose_host": (i32, [vp, sz, C.POINTER(PresetC), vp, sz, vp, vp, sz, C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_int32)]),
+            "htr_generate": (i32, [vp, C.POINTER(PresetC), C.c_uint64, vp, sz, TOKEN_CB, vp, C.POINTER(sz)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -383,6 +386,24 @@ def choose_many(dev: Device, logits: Buffer, n_vocab: int, n: int, hist: Buffer,
 def matmul_q8_0(dev: Device, x: Buffer, m: int, w: Weight, y: Buffer, acc: bool = False) -> None:
     """y[m][N] (+)= x·Wᵀ (x f32 [m][K], w q8_0) on the device's compute path: F32 exact, F16 operands rounded to f16"""
     _check(lib().htr_matmul_q8_0(dev.h, x.ptr, m, w.h, y.ptr, int(acc)))
+
+
+def choose_host(logits: np.ndarray, preset: Preset, history, counts: dict | None, rng_state: list) -> int:
+    """sampling.rs:38-89 choose on host logits (penalised IN PLACE); rng_state is a one-element list holding the
+    SplitMix64 state, advanced when the preset samples"""
+    assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+    hist = np.ascontiguousarray(history, dtype=np.int32)
+    counts = counts or {}
+    ct = np.array(list(counts.keys()), dtype=np.int32)
+    cn = np.array(list(counts.values()), dtype=np.uint32)
+    st = C.c_uint64(rng_state[0])
+    out = C.c_int32()
+    p = preset.c()
+    _check(lib().htr_choose_host(_ptr(logits), logits.size, C.byref(p), _ptr(hist) if hist.size else None, hist.size,
+                                 _ptr(ct) if ct.size else None, _ptr(cn) if cn.size else None, ct.size, C.byref(st),
+                                 C.byref(out)))
+    rng_state[0] = st.value
+    return out.value
 
 
 def gemm_f16(dev: Device, x16: Buffer, m: int, w: Weight, y: Buffer, acc: bool = False) -> None:
@@ -607,6 +628,24 @@ class Session:
 
         fn = TOKEN_CB(cb)
         _check(lib().htr_decode_gpu(self.h, ch.h, max_tokens, fn, None))
+        return toks
+
+    def generate(self, preset: Preset, seed: int, history, on_token=None) -> list[int]:
+        """sampling.rs:252-278 generate: the CPU-choice read (any preset, sampled ones included), each token stepped
+        on the device; on_token returning False ends the read before the token is stepped"""
+        toks: list[int] = []
+
+        def cb(t, _u):
+            toks.append(int(t))
+            return 1 if on_token is None else int(bool(on_token(int(t))))
+
+        fn = TOKEN_CB(cb)
+        hist = np.ascontiguousarray(history, dtype=np.int32)
+        p = preset.c()
+        n = C.c_size_t()
+        _check(lib().htr_generate(self.h, C.byref(p), seed, _ptr(hist) if hist.size else None, hist.size, fn, None,
+                                  C.byref(n)))
+        assert n.value == len(toks)
         return toks
 
 

@@ -266,6 +266,22 @@ typedef int (*htr_token_cb)(int32_t tok, void *user);
  * launch, `depth` launches in flight; 4 bytes per token come back. on_token returning 0 ends the read. */
 int htr_decode_gpu(htr_session *s, htr_choice *c, size_t max, htr_token_cb on_token, void *user);
 
+/* ---- the CPU-choice decode (ocr-decode sampling.rs:23-89, 252-278) ------------------------------------------------ */
+/* choose (sampling.rs:38-89) on host logits, penalised in place: the repetition penalty over the distinct ids of the
+ * history's last repetition_window (< 0: × rp, else ÷ rp), the frequency penalty fp · count over (count_ids, counts),
+ * then the first maximum (temperature 0) or temperature + top-p sampling with the SplitMix64 state *rng (Rng,
+ * sampling.rs:23-35; advanced once per sampled choice) → *out. The preset is checked as Preset::validate does
+ * (presets.rs:35-55: temperature ≥ 0, 0 < top_p ≤ 1 and 1 when greedy, rp > 0, window ≥ 1, fp ≥ 0, max ≥ 1). */
+int htr_choose_host(float *logits, size_t n_vocab, const htr_preset *p, const int32_t *history, size_t n_history,
+                    const int32_t *count_ids, const uint32_t *counts, size_t n_counts, uint64_t *rng, int32_t *out);
+/* generate (sampling.rs:252-278) over TextModel::step (text.rs:524-537): up to max_new_tokens choices on the CPU, the
+ * first from the session's logits, each chosen token passed to on_token and then stepped on the device (htr_step).
+ * history seeds the repetition window, seed the Rng; the frequency counts start empty. on_token returning 0 ends the
+ * read before the token is stepped (the engine's end of generation or cancel). *n_out = the tokens passed to
+ * on_token. */
+int htr_generate(htr_session *s, const htr_preset *p, uint64_t seed, const int32_t *history, size_t n_history,
+                 htr_token_cb on_token, void *user, size_t *n_out);
+
 /* ---- seeded synthetic inputs (host-side data generation for tests and benches; not on the decode path) ------- */
 /* q8_0 GGUF blocks: quants uniform in [−127, 127], d = f16(|N(0,1)|·0.002), from (seed, block index) */
 int htr_synth_q8_0(uint64_t seed, size_t rows, size_t cols, void *h_blocks);

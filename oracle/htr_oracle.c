@@ -654,6 +654,84 @@ int32_t or_choose(float *logits, size_t n_vocab, double rp, size_t window, doubl
     return (int32_t)best;
 }
 
+/* sampling.rs:23-35 Rng: SplitMix64 (Steele, Lea, Flood 2014); the next double in [0, 1) from the top 53 bits */
+double or_rng_next_f64(uint64_t *state) {
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) / 9007199254740992.0; /* 2^53 */
+}
+
+typedef struct {
+    size_t i;
+    double p;
+} or_prob;
+
+/* probability descending, index ascending on ties: the order of a stable sort of the vocabulary by probability */
+static int prob_order(const void *a, const void *b) {
+    const or_prob *x = (const or_prob *)a, *y = (const or_prob *)b;
+    if (x->p != y->p) {
+        return x->p > y->p ? -1 : 1;
+    }
+    return x->i < y->i ? -1 : (x->i > y->i);
+}
+
+/* sampling.rs:38-89 choose with a sampled preset: the penalties as or_choose, then e^((l − max)/T) in f64 from the
+ * f32 (l − max)/T, normalised by their sum over the vocabulary in index order; the smallest prefix of the descending
+ * order whose running sum reaches top_p (all of it when top_p ≥ 1); r = next_f64 · Σ kept; the first kept token where
+ * r minus the running sum falls to ≤ 0 (the last kept one if none does). temperature 0 → or_choose. */
+int32_t or_choose_sampled(float *logits, size_t n_vocab, double temperature, double top_p, double rp, size_t window,
+                          double fp, const int32_t *history, size_t n_hist, const int32_t *count_tok,
+                          const uint32_t *count_n, size_t n_counts, uint64_t *rng) {
+    if (temperature == 0.0) {
+        return or_choose(logits, n_vocab, rp, window, fp, history, n_hist, count_tok, count_n, n_counts);
+    }
+    /* the penalties alone: or_choose with no vocabulary to scan (its argmax over 0 tokens) */
+    or_choose(logits, 0, rp, window, fp, history, n_hist, count_tok, count_n, n_counts);
+    float t = (float)temperature, mx = -INFINITY;
+    for (size_t i = 0; i < n_vocab; i++) {
+        mx = logits[i] > mx ? logits[i] : mx;
+    }
+    or_prob *pr = (or_prob *)malloc(n_vocab * sizeof(or_prob));
+    double sum = 0.0;
+    for (size_t i = 0; i < n_vocab; i++) {
+        pr[i].i = i;
+        pr[i].p = exp((double)((logits[i] - mx) / t));
+        sum += pr[i].p;
+    }
+    for (size_t i = 0; i < n_vocab; i++) {
+        pr[i].p /= sum;
+    }
+    qsort(pr, n_vocab, sizeof(or_prob), prob_order);
+    size_t keep = n_vocab;
+    if (top_p < 1.0) {
+        double acc = 0.0;
+        for (size_t k = 0; k < n_vocab; k++) {
+            acc += pr[k].p;
+            if (acc >= top_p) {
+                keep = k + 1;
+                break;
+            }
+        }
+    }
+    double total = 0.0;
+    for (size_t k = 0; k < keep; k++) {
+        total += pr[k].p;
+    }
+    double r = or_rng_next_f64(rng) * total;
+    int32_t tok = (int32_t)pr[keep - 1].i;
+    for (size_t k = 0; k < keep; k++) {
+        r -= pr[k].p;
+        if (r <= 0.0) {
+            tok = (int32_t)pr[k].i;
+            break;
+        }
+    }
+    free(pr);
+    return tok;
+}
+
 /* ---------------------------------------------------------------------------------------------------------- */
 /* the text decoder                                                                                           */
 

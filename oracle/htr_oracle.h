@@ -99,6 +99,12 @@ void or_attn_f64(const float *q, const uint16_t *k, const uint16_t *v, size_t kv
  * are −inf / NaN) */
 int32_t or_choose(float *logits, size_t n_vocab, double rp, size_t window, double fp, const int32_t *history,
                   size_t n_hist, const int32_t *count_tok, const uint32_t *count_n, size_t n_counts);
+/* sampling.rs:23-35 Rng (SplitMix64): the next f64 in [0, 1) */
+double or_rng_next_f64(uint64_t *state);
+/* sampling.rs:38-89 choose for any preset: temperature 0 → or_choose; else T + top-p sampling with *rng */
+int32_t or_choose_sampled(float *logits, size_t n_vocab, double temperature, double top_p, double rp, size_t window,
+                          double fp, const int32_t *history, size_t n_hist, const int32_t *count_tok,
+                          const uint32_t *count_n, size_t n_counts, uint64_t *rng);
 
 /* ---- the text decoder (text.rs:437-658) -------------------------------------------------------------------- */
 typedef struct {

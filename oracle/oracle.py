@@ -43,6 +43,9 @@ def lib() -> C.CDLL:
             "or_attn_causal": (None, [vp, vp, vp, sz, i32, i32, i32, i32, f32, vp]),
             "or_attn_f64": (None, [vp, vp, vp, sz, i32, i32, i32, f64, vp]),
             "or_choose": (C.c_int32, [vp, sz, f64, sz, f64, vp, sz, vp, vp, sz]),
+            "or_rng_next_f64": (f64, [C.POINTER(C.c_uint64)]),
+            "or_choose_sampled": (C.c_int32, [vp, sz, f64, f64, f64, sz, f64, vp, sz, vp, vp, sz,
+                                              C.POINTER(C.c_uint64)]),
             "or_session_new": (vp, [vp, vp, vp, vp, i32]),
             "or_session_free": (None, [vp]),
             "or_session_n_past": (i32, [vp]),
@@ -215,6 +218,29 @@ def choose(logits: np.ndarray, rp: float, window: int, fp: float, history, count
     cn = np.array(list(counts.values()), dtype=np.uint32)
     return int(lib().or_choose(_p(logits), logits.size, rp, window, fp, _p(hist) if hist.size else None, hist.size,
                                _p(ct) if ct.size else None, _p(cn) if cn.size else None, ct.size))
+
+
+class Rng:
+    """sampling.rs:23-35 Rng (SplitMix64), the oracle's"""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed)
+
+    def next_f64(self) -> float:
+        return lib().or_rng_next_f64(C.byref(self.state))
+
+
+def choose_sampled(logits: np.ndarray, temperature: float, top_p: float, rp: float, window: int, fp: float, history,
+                   counts: dict | None, rng: Rng) -> int:
+    """sampling.rs:38-89 for any preset (logits penalised IN PLACE); rng advances when the preset samples"""
+    assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+    hist = np.ascontiguousarray(history, dtype=np.int32)
+    counts = counts or {}
+    ct = np.array(list(counts.keys()), dtype=np.int32)
+    cn = np.array(list(counts.values()), dtype=np.uint32)
+    return int(lib().or_choose_sampled(_p(logits), logits.size, temperature, top_p, rp, window, fp,
+                                       _p(hist) if hist.size else None, hist.size, _p(ct) if ct.size else None,
+                                       _p(cn) if cn.size else None, ct.size, C.byref(rng.state)))
 
 
 class TextCfg(C.Structure):

@@ -123,6 +123,49 @@ def test_tiny_decode_gpu_matches_oracle_and_is_chunk_invariant(dev, tiny):
     print(f"\n[tiny decode] {n_new} tokens, near-ties: {ties}")
 
 
+def test_generate_is_the_cpu_choice_read(dev, tiny):
+    """sampling.rs:252-278 generate over TextModel::step with a sampled preset (T 0.7, top-p 0.9, rp 1.1 / 20,
+    fp 0.1, seed 1234): the tokens of a step-by-step loop that chooses with the oracle's choose on the GPU's own logits,
+    the history, counts and Rng advanced as generate does (every token is stepped, the last one too); an early stop
+    from the callback; and with a greedy preset the tokens of the GPU choice (decode_gpu)"""
+    cfg, te, on, layers, m = tiny
+    prompt = tiny_prompt()
+    n = 40
+    p = htr.Preset(repetition_penalty=1.1, repetition_window=20, frequency_penalty=0.1, max_new_tokens=n,
+                   temperature=0.7, top_p=0.9)
+    s = m.session(prompt.size + n)
+    s.prefill(prompt)
+    toks = s.generate(p, 1234, prompt)
+    assert len(toks) == n and s.n_past == prompt.size + n
+    s2 = m.session(prompt.size + n)
+    lg = s2.prefill(prompt)
+    hist, counts, r, want = [int(t) for t in prompt], {}, orc.Rng(1234), []
+    for i in range(n):
+        t = orc.choose_sampled(lg.copy(), 0.7, 0.9, 1.1, 20, 0.1, hist, counts, r)
+        want.append(t)
+        hist.append(t)
+        counts[t] = counts.get(t, 0) + 1
+        lg = s2.step(t)
+    assert toks == want
+    print(f"\n[generate, sampled] {toks[:12]}…")
+    s3 = m.session(prompt.size + n)
+    s3.prefill(prompt)
+    seen = []
+    got = s3.generate(p, 1234, prompt, on_token=lambda t: (seen.append(t), len(seen) < 7)[1])
+    assert got == want[:7] and s3.n_past == prompt.size + 6
+    greedy = htr.Preset(repetition_penalty=1.1, repetition_window=20, max_new_tokens=30)
+    s4 = m.session(prompt.size + 30)
+    s4.prefill(prompt)
+    g_cpu = s4.generate(greedy, 0, prompt)
+    s5 = m.session(prompt.size + 30)
+    s5.prefill(prompt)
+    ch = s5.choice(greedy, prompt, 4, 2)
+    assert g_cpu == s5.decode_gpu(ch, 30)
+    ch.free()
+    for x in (s, s2, s3, s4, s5):
+        x.free()
+
+
 def test_decode_gpu_stops_when_the_callback_says_so(dev, tiny):
     cfg, te, on, layers, m = tiny
     prompt = tiny_prompt()
