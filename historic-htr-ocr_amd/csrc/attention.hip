@@ -439,118 +439,213 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
 
 // ---- prefill causal attention ----------------------------------------------------------------------------------------
 //
-// attention_causal.wgsl's arithmetic (text.rs:484-499, the F32 path): q·scale, f32 scores, an online softmax in f32,
-// out = O / l — on the f32 matrix cores (v_mfma_f32_16x16x4f32: f32 products and sums in the matrix unit's order).
-// grid (⌈n_q/32⌉, n_kv), 256 threads = 4 waves: wave w takes q head 2·kvh + (w & 1) (GQA group 2) and the 16 queries
-// 32·x + 16·(w >> 1) …; both heads share the KV head's keys. Keys in stages of 32 through LDS (K [32][128 + 8] f16,
-// Vᵀ [128][32 + 4] f16: padded rows, so 16 lanes' reads fall on distinct banks), each stage as two blocks of 16.
-// Per block, Sᵀ (16 keys × 16 queries) = K·(q·scale)ᵀ is 32 MFMAs over the 128 dims (lane group g = ℓ/16 takes dims
-// 32g …), leaving lane ℓ = 16g + c the scores of keys 4g … 4g + 3 for query c (its partners across lane bits 4 and 5
-// hold the rest); masked keys (after the query) are −inf, the running max starts at −3e38. Oᵀ (128 dims × 16 queries)
-// += Vᵀ·Pᵀ is 32 more, lane ℓ accumulating dims 16t + 4g … of query c, so the rescale stays in the lane.
-constexpr int PQ = 32, PK = 32, KS = D + 8, VS = PK + 4;
+// attention_causal.wgsl's arithmetic (text.rs:484-499; the same on every compute path): q·scale in f32, scores as
+// f32 dot products with the f16 keys, an online softmax in f32 from a running max of −3e38 over the keys each query
+// sees (0 … its position), out = acc · (1 / l). Here on the f16 matrix cores (v_mfma_f32_16x16x32_f16) with f32-grade
+// operands: q·scale = qh + ql and p·2^14 = ph + pl, each half rounded to f16 (the pair holds 22 bits; K and V are f16
+// already), so every product is exact and every sum f32; the 2^14 (exact) keeps small p out of f16's subnormals and
+// comes off with 1/l at the end.
+//
+//   blocks   a pre-pass (k_kv_blocks) copies the keys 0 … n_keys − 1 of each KV head into blocks of 32 keys, 16 KB each,
+//            laid out as LDS holds them: K [32 keys][128 dims] with row r's 16-byte chunk c at 16r + (c ^ r%16), then
+//            Vᵀ [128 dims][32 keys] with row d's chunk g at 512 + 4d + (g ^ (d/4)%4), the keys of chunk g in the order
+//            the P·V MFMA consumes them: 4g … 4g+3, 16 + 4g … 16 + 4g + 3 (the keys lane group g holds in its two
+//            score tiles) — so 16 lanes' fragment reads fall on 16 bank groups and a stage is a plain copy;
+//   work     a workgroup takes 16 queries (one query block) of both q heads of a KV head: 4 waves = 2 heads × 2 halves
+//            of the key blocks (even / odd), the two halves merged through LDS at the end. Stages of 2 blocks go
+//            global → LDS by direct loads, the next stage in flight while one is used. Workgroup j takes query block
+//            n_qb − 1 − j/n_kv for the first half of the grid and j/n_kv − half for the second, so the two workgroups
+//            a CU holds have complementary lengths;
+//   scores   Sᵀ (16 keys × 16 queries) = K·(qh + ql)ᵀ: lane ℓ = 16g + c holds query c's scores of keys 4g … 4g + 3 of
+//            each 16-key tile; the max and the sum over a query's keys are one swap across lane bits 4 and 5 each;
+//   values   Oᵀ (128 dims × 16 queries) += Vᵀ·(ph + pl)ᵀ, the P operand straight from the lane's score registers,
+//            lane ℓ accumulating dims 16t + 4g … of query c, so the rescale by the query's correction stays in the lane.
+constexpr int CQ = 16, CK = 32, CB_CHUNKS = 1024;  // queries a block, keys a block, 16-byte chunks a key block
+constexpr float P_SCALE = 16384.0f, P_UNSCALE = 1.0f / 16384.0f;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
+__device__ __forceinline__ int kb_kslot(int r, int c) { return 16 * r + (c ^ (r & 15)); }
+__device__ __forceinline__ int kb_vslot(int d, int g) { return 512 + 4 * d + (g ^ ((d >> 2) & 3)); }
+// the key of chunk slot j (0 … 7) of Vᵀ chunk g
+__device__ __forceinline__ int kb_vkey(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4); }
+
+// grid (n_blk, n_kv), 256 threads, 4 chunks a thread; keys ≥ n_keys are zeros (masked wherever they are read)
+__global__ __launch_bounds__(256) void k_kv_blocks(const _Float16 *kc, const _Float16 *vc, int n_ctx, int n_keys,
+                                                   int4 *out) {
+    const int kb = blockIdx.x, kvh = blockIdx.y, n_blk = gridDim.x;
+    const _Float16 *kh = kc + (size_t)kvh * n_ctx * D, *vh = vc + (size_t)kvh * n_ctx * D;
+    int4 *ob = out + ((size_t)kvh * n_blk + kb) * CB_CHUNKS;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int u = threadIdx.x + 256 * i;
+        int4 v = make_int4(0, 0, 0, 0);
+        if (u < 512) {
+            const int r = u >> 4, c = (u & 15) ^ (r & 15), key = CK * kb + r;
+            if (key < n_keys) v = *reinterpret_cast<const int4 *>(kh + (size_t)key * D + 8 * c);
+        } else {
+            const int w = u - 512, d = w >> 2, g = (w & 3) ^ ((d >> 2) & 3);
+            _Float16 e[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int key = CK * kb + kb_vkey(g, j);
+                e[j] = key < n_keys ? vh[(size_t)key * D + d] : (_Float16)0.0f;
+            }
+            __builtin_memcpy(&v, e, 16);
+        }
+        ob[u] = v;
+    }
+}
+
 // OT: the output's type — f32, or f16 (rounded to nearest even: the value the f16 path's o-projection tile holds)
 template <typename OT>
-__global__ __launch_bounds__(256) void k_attn_causal(const float *q, const _Float16 *kc, const _Float16 *vc, int n_q,
-                                                     int pos0, int n_head, int n_kv, int n_ctx, float scale,
-                                                     OT *out) {
-    __shared__ __attribute__((aligned(16))) _Float16 s_k[PK * KS];
-    __shared__ __attribute__((aligned(16))) _Float16 s_vt[D * VS];
-    const int kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = 2 * kvh + (wave & 1);
-    const int q0 = blockIdx.x * PQ + 16 * (wave >> 1);
+__global__ __launch_bounds__(256) void k_attn_causal(const float *q, const int4 *kvb, int n_blk, int n_q, int pos0,
+                                                     int n_head, int n_kv, float scale, OT *out) {
+    __shared__ __attribute__((aligned(16))) int4 s_kv[2][2][CB_CHUNKS];  // [buffer][half][chunk]
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
-    const int qi = min(q0 + c, n_q - 1);
-    const int qpos = pos0 + qi;
-    const int wlast = pos0 + min(q0 + 15, n_q - 1);                  // the wave's last query position
-    const int glast = pos0 + min((int)blockIdx.x * PQ + PQ - 1, n_q - 1);  // the workgroup's
-    // the B operand of Sᵀ at MFMA step s: q[query c][dim 32g + s]·scale
-    float qf[32];
-    {
-        const float4 *qr = reinterpret_cast<const float4 *>(q + ((size_t)qi * n_head + h) * D + 32 * g);
+    const int n_qb = (n_q + CQ - 1) / CQ, half_grid = (n_qb + 1) / 2;
+    const int kvh = blockIdx.x % n_kv, rank = blockIdx.x / n_kv;
+    const int qb = rank < half_grid ? n_qb - 1 - rank : rank - half_grid;
+    const int hh = wave & 1, kh = wave >> 1, h = 2 * kvh + hh;
+    const int q_first = CQ * qb, q_last = min(q_first + CQ - 1, n_q - 1);
+    const int qi = min(q_first + c, n_q - 1), qpos = pos0 + qi;
+    const int nkb = (pos0 + q_last + 1 + CK - 1) / CK;  // key blocks the last query of the block sees
+    const int n_stage = (nkb + 1) / 2;
+    const int4 *src = kvb + (size_t)kvh * n_blk * CB_CHUNKS;
+
+    // stage st → buffer: blocks 2st, 2st + 1 (clamped to the last: loaded, not used), 8 direct loads a wave
+    auto issue = [&](int st, int buf) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float4 v = qr[i];
-            qf[4 * i] = v.x * scale, qf[4 * i + 1] = v.y * scale, qf[4 * i + 2] = v.z * scale, qf[4 * i + 3] = v.w * scale;
+            const int u = 64 * (wave + 4 * i);  // the wave's 64 chunks of the stage's 2048
+            const int blk = min(2 * st + (u >> 10), nkb - 1);
+            __builtin_amdgcn_global_load_lds((const void *)(src + (size_t)blk * CB_CHUNKS + (u & 1023) + lane),
+                                             (void __attribute__((address_space(3))) *)&s_kv[buf][u >> 10][u & 1023],
+                                             16, 0, 0);
+        }
+    };
+    issue(0, 0);
+
+    // q·scale as f16 pairs: B operand of step ks = dims 32ks + 8g … + 7 of query c
+    half8 qh[4], ql[4];
+    {
+        const float *qrow = q + ((size_t)qi * n_head + h) * D;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * g);
+            const float4 a1 = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * g + 4);
+            const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float qs = x[e] * scale;
+                const _Float16 hi = (_Float16)qs;
+                qh[ks][e] = hi;
+                ql[ks][e] = (_Float16)(qs - (float)hi);
+            }
         }
     }
     f32x4 o[8];
 #pragma unroll
     for (int t = 0; t < 8; t++) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -3.0e38f, l = 0.0f;
-    const _Float16 *kb = kc + (size_t)kvh * n_ctx * D, *vb = vc + (size_t)kvh * n_ctx * D;
-    const int n_stage = glast / PK + 1;
+
     for (int st = 0; st < n_stage; st++) {
-        const int k0 = st * PK;
-        __syncthreads();  // the previous stage is no longer read
-        // K and V of keys k0 … k0 + 31 (past the workgroup's last query: its row, masked): 512 chunks of 16 bytes
+        const int buf = st & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage st
+        __builtin_amdgcn_s_barrier();                       // everyone's; and stage st − 1 is read by all
+        asm volatile("" ::: "memory");
+        if (st + 1 < n_stage) issue(st + 1, buf ^ 1);
+        const int kb = 2 * st + kh;
+        if (kb >= nkb) continue;
+        const int4 *blk = s_kv[buf][kh];
+        f32x4 s[2];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int ch = tid + 256 * i, r = ch >> 4, cc = ch & 15;
-            const size_t key = (size_t)min(k0 + r, glast);
-            const int4 kv = *reinterpret_cast<const int4 *>(kb + key * D + 8 * cc);
-            const half8 vv = *reinterpret_cast<const half8 *>(vb + key * D + 8 * cc);
-            *reinterpret_cast<int4 *>(s_k + r * KS + 8 * cc) = kv;
+        for (int t = 0; t < 2; t++) {
+            s[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int e = 0; e < 8; e++) s_vt[(8 * cc + e) * VS + r] = vv[e];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++) {
-            const int kb0 = k0 + 16 * sb;
-            if (kb0 > wlast) break;  // no key of this block is visible to the wave's queries (uniform)
-            f32x4 sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            const _Float16 *krow = s_k + (16 * sb + c) * KS + 32 * g;
-#pragma unroll
-            for (int s4 = 0; s4 < 4; s4++) {
-                const half8 kh = *reinterpret_cast<const half8 *>(krow + 8 * s4);
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kh[e], qf[8 * s4 + e], sacc, 0, 0, 0);
-            }
-            float sv[4], mx = m;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                sv[i] = kb0 + 4 * g + i <= qpos ? sacc[i] : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
-            }
-            mx = pair_max<32>(pair_max<16>(mx));
-            const float corr = expf(m - mx);
-            float p[4], ps = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                p[i] = expf(sv[i] - mx);  // masked: e^(−inf) = 0
-                ps += p[i];
-            }
-            l = l * corr + pair_sum<32>(pair_sum<16>(ps));
-            m = mx;
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const half4 vt = *reinterpret_cast<const half4 *>(s_vt + (16 * t + c) * VS + 16 * sb + 4 * g);
-                o[t] *= corr;
-#pragma unroll
-                for (int s = 0; s < 4; s++) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vt[s], p[s], o[t], 0, 0, 0);
+            for (int ks = 0; ks < 4; ks++) {
+                const half8 a = *reinterpret_cast<const half8 *>(blk + kb_kslot(16 * t + c, 4 * ks + g));
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[t], 0, 0, 0);
             }
         }
-    }
-    if (q0 + c < n_q) {
-        const float inv = 1.0f / l;
-        OT *orow = out + ((size_t)(q0 + c) * n_head + h) * D + 4 * g;
+        // keys after the query (only in the block that holds the query block's positions) take no part
+        const bool diag = CK * kb + CK - 1 > pos0 + q_first;
+        float mx = m;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (diag && CK * kb + 16 * t + 4 * g + r > qpos) s[t][r] = -INFINITY;
+                mx = fmaxf(mx, s[t][r]);
+            }
+        mx = pair_max<32>(pair_max<16>(mx));
+        const float corr = expf(m - mx);
+        float p[2][4], ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[t][r] = expf(s[t][r] - mx);  // masked: e^(−inf) = 0
+                ps += p[t][r];
+            }
+        l = l * corr + pair_sum<32>(pair_sum<16>(ps));
+        m = mx;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[t] *= corr;
+        }
+        half8 ph, pl;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float ps2 = p[t][r] * P_SCALE;
+                const _Float16 hi = (_Float16)ps2;
+                ph[4 * t + r] = hi;
+                pl[4 * t + r] = (_Float16)(ps2 - (float)hi);
+            }
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            if constexpr (sizeof(OT) == 4) {
-                *reinterpret_cast<float4 *>(orow + 16 * t) =
-                    make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
-            } else {
-                const half4 hv = {(_Float16)(o[t][0] * inv), (_Float16)(o[t][1] * inv), (_Float16)(o[t][2] * inv),
-                                  (_Float16)(o[t][3] * inv)};
-                *reinterpret_cast<half4 *>(orow + 16 * t) = hv;
-            }
+            const half8 a = *reinterpret_cast<const half8 *>(blk + kb_vslot(16 * t + c, g));
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[t], 0, 0, 0);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS load in flight past this point
+    // merge the two key halves of each head through LDS (the stage buffers are free after this barrier)
+    __syncthreads();
+    float *s_o = reinterpret_cast<float *>(&s_kv[0][0][0]);  // [head][128 dims][16 queries] + [head][2][16]
+    float *s_ml = s_o + 2 * D * CQ;
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) s_o[(hh * D + 16 * t + 4 * g + r) * CQ + c] = o[t][r];
+        if (g == 0) {
+            s_ml[(hh * 2) * CQ + c] = m;
+            s_ml[(hh * 2 + 1) * CQ + c] = l;
+        }
+    }
+    __syncthreads();
+    if (kh == 1 || q_first + c >= n_q) return;
+    const float m1 = s_ml[(hh * 2) * CQ + c], l1 = s_ml[(hh * 2 + 1) * CQ + c];
+    const float mm = fmaxf(m, m1), a0 = expf(m - mm), a1 = expf(m1 - mm);
+    const float inv = (1.0f / (l * a0 + l1 * a1)) * P_UNSCALE;
+    OT *orow = out + ((size_t)(q_first + c) * n_head + h) * D + 4 * g;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = (o[t][r] * a0 + s_o[(hh * D + 16 * t + 4 * g + r) * CQ + c] * a1) * inv;
+        if constexpr (sizeof(OT) == 4) {
+            *reinterpret_cast<float4 *>(orow + 16 * t) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            const half4 hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            *reinterpret_cast<half4 *>(orow + 16 * t) = hv;
         }
     }
 }
@@ -622,20 +717,30 @@ int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k
     return htr_launched(dev, "k_qk_rows");
 }
 
+size_t attn_causal_block_bytes(int n_kv, int n_keys) {
+    return (size_t)n_kv * ((n_keys + CK - 1) / CK) * CB_CHUNKS * 16;
+}
+
 int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
-                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out, _Float16 *out16) {
+                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, void *blocks, float *out,
+                       _Float16 *out16) {
     if (n_head != 2 * n_kv) return htr_fail("causal attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
     if (n_q < 1 || pos0 < 0 || pos0 + n_q > n_ctx)
         return htr_fail("causal attention: %d queries from position %d in a %d-row cache", n_q, pos0, n_ctx);
     if (!out == !out16) return htr_fail("causal attention: one output, f32 or f16");
-    const dim3 grid((n_q + PQ - 1) / PQ, n_kv);
+    if (!blocks) return htr_fail("causal attention: no key-block buffer");
+    const int n_keys = pos0 + n_q, n_blk = (n_keys + CK - 1) / CK;
+    hipLaunchKernelGGL(k_kv_blocks, dim3(n_blk, n_kv), dim3(256), 0, st, (const _Float16 *)kc, (const _Float16 *)vc,
+                       n_ctx, n_keys, (int4 *)blocks);
+    HTR_TRY(htr_launched(dev, "k_kv_blocks"));
+    const dim3 grid(((n_q + CQ - 1) / CQ) * n_kv);
     if (out) {
-        hipLaunchKernelGGL(k_attn_causal<float>, grid, dim3(256), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc,
-                           n_q, pos0, n_head, n_kv, n_ctx, scale, out);
+        hipLaunchKernelGGL(k_attn_causal<float>, grid, dim3(256), 0, st, q, (const int4 *)blocks, n_blk, n_q, pos0,
+                           n_head, n_kv, scale, out);
         return htr_launched(dev, "k_attn_causal");
     }
-    hipLaunchKernelGGL(k_attn_causal<_Float16>, grid, dim3(256), 0, st, q, (const _Float16 *)kc, (const _Float16 *)vc,
-                       n_q, pos0, n_head, n_kv, n_ctx, scale, out16);
+    hipLaunchKernelGGL(k_attn_causal<_Float16>, grid, dim3(256), 0, st, q, (const int4 *)blocks, n_blk, n_q, pos0,
+                       n_head, n_kv, scale, out16);
     return htr_launched(dev, "k_attn_causal<f16>");
 }
 
@@ -650,6 +755,17 @@ extern "C" int htr_qkv_post(htr_device *dev, float *d_qkv, const float *d_q_norm
         return htr_fail("htr_qkv_post: position %d of a %d-row cache, %d / %d heads", pos, n_ctx, n_head, n_kv);
     return launch_qkv_post(dev, dev->stream, d_qkv, d_q_norm, d_k_norm, d_rope, n_head, n_kv, nullptr, pos, n_ctx, eps,
                            d_k, d_v);
+}
+
+extern "C" int htr_causal_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v,
+                                    int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *d_out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!d_q || !d_k || !d_v || !d_out) return htr_fail("htr_causal_attention: null argument");
+    if (n_q < 1 || pos0 < 0 || n_ctx < 1 || pos0 > n_ctx - n_q)
+        return htr_fail("htr_causal_attention: %d queries from position %d in a %d-row cache", n_q, pos0, n_ctx);
+    void *blocks;
+    HTR_TRY(htr_scratch(dev, SCR_CAUSAL_BLOCKS, attn_causal_block_bytes(n_kv, pos0 + n_q), &blocks));
+    return launch_attn_causal(dev, dev->stream, d_q, d_k, d_v, n_q, pos0, n_head, n_kv, n_ctx, scale, blocks, d_out);
 }
 
 extern "C" int htr_decode_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v,

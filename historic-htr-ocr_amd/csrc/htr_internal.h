@@ -42,7 +42,7 @@ struct htr_device {
     int compute = HTR_COMPUTE_F16;
 };
 
-enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3 };
+enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3, SCR_CAUSAL_BLOCKS = 4 };
 // the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it, zero-filled)
 int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out);
 
@@ -123,9 +123,12 @@ int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const ui
 int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k, const float *v, const float *qn,
                              const float *kn, const float *rope, int n_tok, int n_head, int n_kv, int pos0, int n_ctx,
                              float eps, uint16_t *kc, uint16_t *vc);
-// out [n_q][n_head·128] f32, or f16 into out16 (the f16 path's o-projection input) when out is NULL
+// the causal prefill attention: q [n_q][n_head·128] f32 (normed, roped), the head-major f16 caches [n_kv][n_ctx][128]
+// holding keys 0 … pos0 + n_q − 1; blocks: attn_causal_block_bytes(n_kv, pos0 + n_q) of device scratch (the key
+// blocks' copy); out [n_q][n_head·128] f32, or f16 into out16 (the f16 path's o-projection input) when out is NULL
+size_t attn_causal_block_bytes(int n_kv, int n_keys);
 int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
-                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, float *out,
+                       int n_q, int pos0, int n_head, int n_kv, int n_ctx, float scale, void *blocks, float *out,
                        _Float16 *out16 = nullptr);
 
 // token choice (choose.hip)

@@ -65,6 +65,9 @@ struct htr_session {
     hipGraphExec_t step_graph = nullptr;  // the CPU-choice step (no token choice)
     // the prefill's row buffers (ids, x, h, q, k, v, attention, g, u) for up to pre_cap rows, kept across calls
     void *pre = nullptr;
+    // the causal attention's key blocks (a copy of the cache's keys 0 … pos0 + n − 1 in its LDS layout), grown on demand
+    void *kvb = nullptr;
+    size_t kvb_bytes = 0;
     size_t pre_cap = 0;
 };
 
@@ -408,7 +411,7 @@ extern "C" int htr_session_free(htr_session *s) {
     if (s->step_graph) hipGraphExecDestroy(s->step_graph);
     for (void *p : {(void *)s->kc, (void *)s->vc, (void *)s->rope, (void *)s->x, (void *)s->qkv, (void *)s->attn,
                     (void *)s->g, (void *)s->logits, (void *)s->tok, (void *)s->state, (void *)s->asc.part,
-                    (void *)s->asc.counters, s->pre})
+                    (void *)s->asc.counters, s->pre, s->kvb})
         if (p) htr_dev_free(dev, p);
     delete s;
     return 0;
@@ -506,6 +509,14 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         rc = htr_dev_alloc(dev, n * per_row, HTR_MEM_WORK, &s->pre);
         if (rc == 0) s->pre_cap = n;
     }
+    const size_t kvb_need = attn_causal_block_bytes(c.n_kv, pos0 + l);
+    if (rc == 0 && kvb_need > s->kvb_bytes) {
+        if (s->kvb) htr_dev_free(dev, s->kvb);
+        s->kvb = nullptr;
+        s->kvb_bytes = 0;
+        rc = htr_dev_alloc(dev, kvb_need, HTR_MEM_WORK, &s->kvb);
+        if (rc == 0) s->kvb_bytes = kvb_need;
+    }
     uint32_t *d_tok = nullptr;
     float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *a = nullptr, *g = nullptr,
           *u = nullptr;
@@ -537,7 +548,8 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
                                           s->n_ctx, c.eps, kc, vc);
         if (rc == 0)
-            rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, nullptr, a16);
+            rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, s->kvb, nullptr,
+                                    a16);
         if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_ACC, a16, l, ly.o, nullptr, x, nullptr, 1.0f);
         if (rc == 0) rc = launch_rms_norm_f16(dev, st, x, ly.ffn_norm, h16, l, d, c.eps);
         if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_FFN, h16, l, ly.gate, ly.up, nullptr, g16, 1.0f);
@@ -555,7 +567,7 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         if (rc == 0)
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
                                           s->n_ctx, c.eps, kc, vc);
-        if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, a);
+        if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, s->kvb, a);
         if (rc == 0) rc = gemm(dev, st, a, ly.o, x, l, 1);
         if (rc == 0) rc = launch_rms_norm(dev, st, x, ly.ffn_norm, h, l, d, c.eps);
         if (rc == 0) rc = gemm(dev, st, h, ly.gate, g, l, 0);

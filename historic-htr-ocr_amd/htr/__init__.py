@@ -27,7 +27,7 @@ SYMBOLS = [
     "htr_sync", "htr_device_set_compute", "htr_device_compute", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free",
     "htr_upload", "htr_download", "htr_copy", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
-    "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_choose",
+    "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_causal_attention", "htr_choose",
     "htr_choose_many", "htr_matmul_q8_0", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
     "htr_vision_out_shape", "htr_vision_encode", "htr_gguf_open", "htr_gguf_open_source", "htr_gguf_close",
     "htr_gguf_header", "htr_gguf_tensor", "htr_gguf_u32", "htr_gguf_f32", "htr_gguf_str", "htr_gguf_f32_array",
@@ -127,6 +127,7 @@ def lib() -> C.CDLL:
             "htr_matvec_ffn": (i32, [vp, vp, vp, vp, vp, f32, vp]),
             "htr_qkv_post": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, vp, vp]),
             "htr_decode_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
+            "htr_causal_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp]),
             "htr_choose": (i32, [vp, vp, i32, vp, i32, i32, f32, f32, vp, vp, vp]),
             "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),
             "htr_matmul_q8_0": (i32, [vp, vp, sz, vp, vp, i32]),
@@ -370,6 +371,11 @@ def qkv_post(dev: Device, qkv: Buffer, q_norm: Buffer, k_norm: Buffer, rope: Buf
 def decode_attention(dev: Device, q: Buffer, kc: Buffer, vc: Buffer, n_head: int, n_kv: int, n_ctx: int, n_keys: int,
                      scale: float, out: Buffer) -> None:
     _check(lib().htr_decode_attention(dev.h, q.ptr, kc.ptr, vc.ptr, n_head, n_kv, n_ctx, n_keys, scale, out.ptr))
+
+
+def causal_attention(dev: Device, q: Buffer, kc: Buffer, vc: Buffer, n_q: int, pos0: int, n_head: int, n_kv: int,
+                     n_ctx: int, scale: float, out: Buffer) -> None:
+    _check(lib().htr_causal_attention(dev.h, q.ptr, kc.ptr, vc.ptr, n_q, pos0, n_head, n_kv, n_ctx, scale, out.ptr))
 
 
 def choose(dev: Device, logits: Buffer, n_vocab: int, hist: Buffer, length: int, window: int, rp: float, tok: Buffer,

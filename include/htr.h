@@ -121,6 +121,11 @@ int htr_qkv_post(htr_device *dev, float *d_qkv, const float *d_q_norm, const flo
  * head-major f16 caches [n_kv][n_ctx][128], n_keys keys, scale → out [n_head·128] f32. GQA group 2. */
 int htr_decode_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v, int n_head,
                          int n_kv, int n_ctx, int n_keys, float scale, float *d_out);
+/* causal GQA prefill attention (attention_causal.wgsl, text.rs:484-499): q [n_q][n_head·128] f32 (normed and roped)
+ * at positions pos0 …, the head-major f16 caches [n_kv][n_ctx][128] holding the keys 0 … pos0 + n_q − 1 → out
+ * [n_q][n_head·128] f32 = softmax(q·scale·Kᵀ over the keys ≤ each query's position)·V. GQA group 2. */
+int htr_causal_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v, int n_q,
+                         int pos0, int n_head, int n_kv, int n_ctx, float scale, float *d_out);
 /* the GPU token choice of a greedy preset on n_vocab logits (choose_pen → choose_max → choose_pick,
  * text.rs:222-231; semantics of ocr-decode sampling.rs:38-62, bit-exact): the repetition penalty rp over the distinct
  * ids of d_hist[len − window … len) applied in place (< 0: × rp, else ÷ rp, IEEE round-to-nearest), the frequency

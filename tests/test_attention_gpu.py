@@ -89,3 +89,40 @@ def test_config2_attention(dev, L):
     want = orc.attn_f64(q_gpu, k, v, n_kv * 128, L, n_head, n_kv, 1 / np.sqrt(128))
     assert rel_l2(got, want) < 1e-3
     assert rel_l2(got, want) < 1e-5  # what the kernel actually reaches (f32 throughout)
+
+
+@pytest.mark.parametrize("n_q,pos0,n_head,n_kv,n_ctx", [(1, 0, 4, 2, 8), (17, 0, 4, 2, 40), (33, 5, 4, 2, 64),
+                                                      (100, 37, 16, 8, 160), (1023, 0, 16, 8, 1536),
+                                                      (200, 1000, 16, 8, 1536)])
+def test_causal_attention_matches_oracle(dev, n_q, pos0, n_head, n_kv, n_ctx):
+    """attention_causal.wgsl (text.rs:484-499): queries at positions pos0 … over the keys 0 … each one's position —
+    against the oracle's f32 restatement and, for sampled queries, fp64 softmax attention (bar 1e-5: f32-grade
+    products and sums on both sides). The cache rows past the last key hold large values: reading them would show."""
+    n_keys = pos0 + n_q
+    g = orc.Lcg(n_q * 7 + pos0)
+    k = orc.f16_bits(g.f32(n_keys * n_kv * 128, 2.0)).reshape(n_keys, -1)
+    v = orc.f16_bits(g.f32(n_keys * n_kv * 128)).reshape(n_keys, -1)
+    q = g.f32(n_q * n_head * 128, 2.0)
+    big = np.full((n_ctx - n_keys, n_kv * 128), np.float16(3.0e4).view(np.uint16), np.uint16)
+    kc = dev.upload(kv_head_major(np.concatenate([k, big]), n_kv))
+    vc = dev.upload(kv_head_major(np.concatenate([v, big]), n_kv))
+    out = dev.alloc(n_q * n_head * 128 * 4)
+    sc = float(np.float32(1 / np.sqrt(128)))
+    htr.causal_attention(dev, dev.upload(q), kc, vc, n_q, pos0, n_head, n_kv, n_ctx, sc, out)
+    got = out.download(np.float32).reshape(n_q, n_head * 128)
+    want = orc.attn_causal(q, k, v, n_kv * 128, n_q, pos0, n_head, n_kv, sc).reshape(n_q, n_head * 128)
+    e = rel_l2(got, want)
+    print(f"\n[causal {n_q} queries from {pos0}] rel-L2 vs the oracle {e:.2e}")
+    assert e < 1e-5
+    for t in sorted({0, n_q // 2, n_q - 1}):
+        row = orc.attn_f64(q[t * n_head * 128:(t + 1) * n_head * 128], k, v, n_kv * 128, pos0 + t + 1, n_head, n_kv,
+                           1 / np.sqrt(128))
+        assert rel_l2(got[t], row) < 1e-5, t
+
+
+def test_causal_attention_rejects_bad_ranges(dev):
+    q, kc, vc, out = dev.alloc(4 * 128 * 4), dev.alloc(2 * 8 * 128 * 2), dev.alloc(2 * 8 * 128 * 2), dev.alloc(4 * 128 * 4)
+    with pytest.raises(htr.HtrError, match="queries from position"):
+        htr.causal_attention(dev, q, kc, vc, 2, 7, 4, 2, 8, 0.1, out)
+    with pytest.raises(htr.HtrError, match="groups of 2"):
+        htr.causal_attention(dev, q, kc, vc, 1, 0, 6, 2, 8, 0.1, out)
