@@ -42,7 +42,14 @@ struct htr_device {
     int compute = HTR_COMPUTE_F16;
 };
 
-enum { SCR_CHOOSE_PART = 0, SCR_CHOOSE_CNT = 1, SCR_ATTN_PART = 2, SCR_ATTN_CNT = 3, SCR_CAUSAL_BLOCKS = 4 };
+enum {
+    SCR_CHOOSE_PART = 0,
+    SCR_CHOOSE_CNT = 1,
+    SCR_ATTN_PART = 2,
+    SCR_ATTN_CNT = 3,
+    SCR_CAUSAL_BLOCKS = 4,
+    SCR_GEMM_PART = 5,  // split-K products [split][M][N]
+};
 // the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it, zero-filled)
 int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out);
 

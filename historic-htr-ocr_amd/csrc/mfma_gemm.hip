@@ -65,14 +65,36 @@ struct GemmK {
     int m, k;
     float scale;                // FFN output scale
     int tiles_m, tiles_n;
+    // K split over `split` workgroups a tile (F32 / ACC, one weight): each takes k_per of K and stores its product
+    // into part [split][M][N]; k_split_reduce then adds the slices in split order (onto y with ACC)
+    int split, k_per;
+    float *part;
 };
+
+// y (+)= ((p_0 + p_1) + p_2) + …: the split slices of a GEMM in split order, 4 values a thread
+__global__ __launch_bounds__(256) void k_split_reduce(const float *part, int split, size_t n4, float *y, int acc) {
+    const size_t stride = n4 * 4;
+    for (size_t i = blockIdx.x * (size_t)256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        float4 s = *reinterpret_cast<const float4 *>(part + 4 * i);
+        for (int q = 1; q < split; q++) {
+            const float4 v = *reinterpret_cast<const float4 *>(part + q * stride + 4 * i);
+            s.x += v.x, s.y += v.y, s.z += v.z, s.w += v.w;
+        }
+        float4 *o = reinterpret_cast<float4 *>(y + 4 * i);
+        if (acc) {
+            const float4 b = *o;
+            s = make_float4(b.x + s.x, b.y + s.y, b.z + s.z, b.w + s.w);
+        }
+        *o = s;
+    }
+}
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // the 16-byte chunk slot of (row r, chunk c) in a stage region
 __device__ __forceinline__ int chunk_slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
 
-template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(const GemmK a) {
+template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void k_gemm_f16(const GemmK a) {
     constexpr int BM = T::BM, BN = T::BN, WN = T::WN, NW = T::NW, TM = T::TM, TN = T::TN;
     constexpr int ACH = T::ACH, SCH = T::SCH, AI = T::AI, BI = T::BI;
     static_assert(EPI != GEMM_FFN || TN == 2, "the FFN pairs one gate and one up tile a wave");
@@ -81,15 +103,18 @@ template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(
     const int wm = wave / WN, wn = wave % WN;
     // tile: XCD band, then groups of GROUP tile rows walked column by column
     int tm, tn;
+    const int sp = SPLIT ? (int)blockIdx.x % a.split : 0;  // this workgroup's part of K
+    const int tile = SPLIT ? (int)blockIdx.x / a.split : (int)blockIdx.x;
     {
-        const int total = a.tiles_m * a.tiles_n, b = blockIdx.x, xcd = b % XCDS, i = b / XCDS;
+        const int total = a.tiles_m * a.tiles_n, b = tile, xcd = b % XCDS, i = b / XCDS;
         const int per = total / XCDS, extra = total % XCDS;
         const int t = xcd * per + min(xcd, extra) + i;
         const int gsz = GROUP * a.tiles_n, g = t / gsz, gr = t % gsz, gm = min(GROUP, a.tiles_m - g * GROUP);
         tm = g * GROUP + gr % gm;
         tn = gr / gm;
     }
-    const int row0 = tm * BM, k = a.k, nk = k / 32, m = a.m;
+    const int row0 = tm * BM, k = a.k, m = a.m;
+    const int nk = (SPLIT ? a.k_per : k) / 32, kbeg = SPLIT ? sp * a.k_per : 0;
     // the W rows of tile row r (0 … BN−1): F32 / ACC the tile's rows of the stacked weights (one weight a tile, rows
     // past its end clamped); FFN blocks of 32 alternating gate / up rows of the tile's BN/2 outputs
     int wsel = 0;
@@ -107,7 +132,7 @@ template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(
         return min(wrow0 + r, wrows - 1);
     };
     auto issue = [&](int ks, int buf) {
-        const size_t kk = (size_t)min(ks, nk - 1) * 32;
+        const size_t kk = (size_t)kbeg + (size_t)min(ks, nk - 1) * 32;
 #pragma unroll
         for (int i = 0; i < AI; i++) {
             const int s = 64 * (wave + NW * i) + lane, r = s >> 2, c = (s & 3) ^ ((r >> 2) & 3);
@@ -203,7 +228,8 @@ template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(
             }
         return;
     }
-    float *y = a.y[wsel];
+    // SPLIT: this part of K's product into its own slice [sp][M][N] (k_split_reduce adds the slices)
+    float *y = SPLIT ? a.part + (size_t)sp * m * wrows : a.y[wsel];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int col = wrow0 + wn * TN * 32 + 32 * j + (lane & 31);
@@ -215,7 +241,7 @@ template <int EPI, class T> __global__ __launch_bounds__(T::GW) void k_gemm_f16(
                 const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (row >= m) continue;
                 float *o = y + (size_t)row * wrows + col;
-                *o = EPI == GEMM_ACC ? *o + acc[i][j][r] : acc[i][j][r];
+                *o = EPI == GEMM_ACC && !SPLIT ? *o + acc[i][j][r] : acc[i][j][r];
             }
     }
 }
@@ -234,12 +260,18 @@ template <class T> int tiles_for(const GemmK &a, int epi, int &tm, int &tn) {
 }
 
 template <class T> void launch_tile(hipStream_t st, int epi, const GemmK &a) {
-    const dim3 grid(a.tiles_m * a.tiles_n);
+    const dim3 grid(a.tiles_m * a.tiles_n * (a.split > 1 ? a.split : 1));
     switch (epi) {
-    case GEMM_F32: hipLaunchKernelGGL((k_gemm_f16<GEMM_F32, T>), grid, dim3(T::GW), 0, st, a); break;
-    case GEMM_ACC: hipLaunchKernelGGL((k_gemm_f16<GEMM_ACC, T>), grid, dim3(T::GW), 0, st, a); break;
+    case GEMM_F32:
+        if (a.split > 1) hipLaunchKernelGGL((k_gemm_f16<GEMM_F32, T, true>), grid, dim3(T::GW), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_f16<GEMM_F32, T, false>), grid, dim3(T::GW), 0, st, a);
+        break;
+    case GEMM_ACC:
+        if (a.split > 1) hipLaunchKernelGGL((k_gemm_f16<GEMM_ACC, T, true>), grid, dim3(T::GW), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_f16<GEMM_ACC, T, false>), grid, dim3(T::GW), 0, st, a);
+        break;
     default:
-        if constexpr (T::TN == 2) hipLaunchKernelGGL((k_gemm_f16<GEMM_FFN, T>), grid, dim3(T::GW), 0, st, a);
+        if constexpr (T::TN == 2) hipLaunchKernelGGL((k_gemm_f16<GEMM_FFN, T, false>), grid, dim3(T::GW), 0, st, a);
         break;
     }
 }
@@ -255,6 +287,29 @@ int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
     int pick = -1;
     for (int i = 0; i < 3 && pick < 0; i++)
         if (n_tiles[i] >= want) pick = i;
+    // too few 256 / 128 tiles and a long K (one weight; N a multiple of 4): 128 × 128 tiles with K split over up to 4
+    // workgroups (a multiple of 32 each), the products summed in split order by k_split_reduce
+    a.split = 1;
+    if (pick != 0 && epi != GEMM_FFN && a.n_w == 1 && a.rows[0] % 4 == 0 && n_tiles[1] > 0 && n_tiles[1] < want &&
+        a.k >= 1024) {
+        int sp = std::min(4, (dev->n_cu + n_tiles[1] - 1) / n_tiles[1]);
+        while (sp > 1 && a.k % (32 * sp)) sp--;
+        if (sp > 1) {
+            void *part = nullptr;
+            HTR_TRY(htr_scratch(dev, SCR_GEMM_PART, (size_t)sp * a.m * a.rows[0] * 4, &part));
+            a.split = sp;
+            a.k_per = a.k / sp;
+            a.part = (float *)part;
+            tiles_for<T128>(a, epi, a.tiles_m, a.tiles_n);
+            launch_tile<T128>(st, epi, a);
+            HTR_TRY(htr_launched(dev, "k_gemm_f16<128, split K>"));
+            const size_t n4 = (size_t)a.m * a.rows[0] / 4;
+            const int grid = (int)std::min<size_t>((n4 + 255) / 256, (size_t)dev->n_cu * 8);
+            hipLaunchKernelGGL(k_split_reduce, dim3(grid), dim3(256), 0, st, a.part, sp, n4, a.y[0],
+                               epi == GEMM_ACC ? 1 : 0);
+            return htr_launched(dev, "k_split_reduce");
+        }
+    }
     for (int i = 0; i < 3 && pick < 0; i++)
         if (n_tiles[i] >= 0 && (pick < 0 || n_tiles[i] > n_tiles[pick])) pick = i;
     if (pick < 0) return htr_fail("gemm_f16: no tile shape fits weights of %d rows", a.rows[0]);

@@ -219,3 +219,25 @@ def test_compute_path_setting(dev):
     with pytest.raises(htr.HtrError, match="compute path"):
         dev.compute = 7
     assert dev.compute == keep
+
+
+@pytest.mark.parametrize("m,n,k", [(1023, 1024, 2048), (1023, 1024, 3072), (40, 256, 1024)])
+def test_split_k_is_exact_and_deterministic(dev, m, n, k):
+    """prompt-sized GEMMs with few tiles split K over workgroups; the last of a tile's splits adds the partials in split
+    order, so repeated runs (any arrival order) are bit-identical; accumulate mode onto a residual, against fp64"""
+    blocks, w16 = f16_weight(m * 3 + n + k, n, k)
+    x = x16(m + 11 * k, m, k, 0.5)
+    w = htr.Weight(dev, blocks, n, k, f16=True)
+    xb = dev.upload(x)
+    base = htr.synth_normal(m + n, m * n).reshape(m, n)
+    outs = []
+    for _ in range(3):
+        y = dev.upload(base)
+        htr.gemm_f16(dev, xb, m, w, y, acc=True)
+        outs.append(y.download(np.float32).reshape(m, n))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    want = base.astype(np.float64) + x.astype(np.float64) @ w16.astype(np.float64).T
+    e = rel_l2(outs[0], want)
+    print(f"\n[split-K {m}x{n}x{k}] rel-L2 vs fp64 {e:.2e}")
+    assert e < 1e-5
+    w.free()
