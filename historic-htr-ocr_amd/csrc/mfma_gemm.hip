@@ -9,8 +9,9 @@
 //   tile      a workgroup owns a BM × BN tile of X rows × W rows, split over a WM × WN grid of waves, each wave
 //             TM × TN v_mfma_f32_32x32x16_f16 tiles (lane layouts checked on the GPU: A lane ℓ holds
 //             A[ℓ%32][8(ℓ/32) …+7], B lane ℓ holds B[8(ℓ/32) …+7][ℓ%32], D lane ℓ register r is row 8(r/4) + 4(ℓ/32)
-//             + r%4, column ℓ%32). Three tile shapes: 256 × 256 (8 waves of 128 × 64), 128 × 128 and 64 × 64 (4
-//             waves of 64 × 64 / 32 × 32); the launch takes the largest that still gives half a workgroup per CU.
+//             + r%4, column ℓ%32). Tile shapes: 256 × 256 and 192 × 256 (8 waves of 128 × 64 / 96 × 64), 128 × 128
+//             and 64 × 64 (4 waves of 64 × 64 / 32 × 32); the launch takes the largest that still gives half a
+//             workgroup per CU, 192 rows where that takes fewer rows × rounds, and splits K for prompt-sized M.
 //             The FFN's W tile is BN/2 gate rows and the same BN/2 up rows in alternating blocks of 32, so a wave's
 //             two column tiles are one gate and one up tile of the same outputs;
 //   K         in stages of 32 through a ring of 4 LDS stages filled by direct-to-LDS loads (global_load_lds_dwordx4):
@@ -37,15 +38,18 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM_, int BN_, int WM_, int WN_> struct Tile {
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;  // tile: X rows × W rows; wave grid
+// AM: X rows a stage loads (≥ BM; the rows past BM are the next tile's, loaded so that every wave issues the same
+// direct loads, and not used)
+template <int BM_, int BN_, int WM_, int WN_, int AM_ = BM_> struct Tile {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, AM = AM_;  // tile: X rows × W rows; wave grid
     static constexpr int NW = WM * WN, GW = 64 * NW;                // waves, threads
     static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles a wave
-    static constexpr int ACH = BM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
+    static constexpr int ACH = AM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
     static constexpr int AI = ACH / GW, BI = BCH / GW;              // direct-to-LDS loads a wave a stage
-    static_assert(TM >= 1 && TN >= 1 && AI * GW == ACH && BI * GW == BCH, "tile shape");
+    static_assert(TM >= 1 && TN >= 1 && AI * GW == ACH && BI * GW == BCH && AM >= BM, "tile shape");
 };
 using T256 = Tile<256, 256, 2, 4>;
+using T192 = Tile<192, 256, 2, 4, 256>;
 using T128 = Tile<128, 128, 2, 2>;
 using T64 = Tile<64, 64, 2, 2>;
 
@@ -287,6 +291,18 @@ int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
     int pick = -1;
     for (int i = 0; i < 3 && pick < 0; i++)
         if (n_tiles[i] >= want) pick = i;
+    // large M: 192-row tiles when they take fewer rows × rounds of one workgroup a CU (M = 12100 at N = 1024: 256
+    // tiles in one round against 192 of 256 rows; at N = 3072 three full rounds against 2¼)
+    if (pick == 0) {
+        const int t192 = tiles_for<T192>(a, epi, tm, tn);
+        const long c256 = (long)((n_tiles[0] + dev->n_cu - 1) / dev->n_cu) * 256;
+        const long c192 = (long)((t192 + dev->n_cu - 1) / dev->n_cu) * 192;
+        if (t192 > 0 && c192 < c256) {
+            tiles_for<T192>(a, epi, a.tiles_m, a.tiles_n);
+            launch_tile<T192>(st, epi, a);
+            return htr_launched(dev, "k_gemm_f16<192>");
+        }
+    }
     // too few 256 / 128 tiles and a long K (one weight; N a multiple of 4): 128 × 128 tiles with K split over up to 4
     // workgroups (a multiple of 32 each), the products summed in split order by k_split_reduce
     a.split = 1;

@@ -206,6 +206,10 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         // (v_cvt_pk_f16_f32, round to nearest even) and summed as f32 by v_dot2 against (1, 1)
         constexpr float LOG2E = 1.4426950408889634f;
         const float corr = __builtin_amdgcn_exp2f((m - mx) * LOG2E), nml = -mx * LOG2E;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) o[t] *= corr;
+        }
         half8 pb[2];
         float ps = 0.0f;
 #pragma unroll
@@ -223,34 +227,38 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         }
         l = l * corr + pair_sum<32>(ps);
         m = mx;
-        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < 2; t++) o[t] *= corr;
-        }
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int st = 0; st < 2; st++)
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fv[2 * t + st], pb[st], o[t], 0, 0, 0);
     };
-    const int n_stage = (n_blk + AST - 1) / AST;
+    // stages 0 … n_full − 1 hold full blocks only: the loop body has one path, so O stays in the same registers
+    // through every iteration (a masked path inside the loop makes the compiler copy it each block)
+    const int n_stage = (n_blk + AST - 1) / AST, n_full = n_tok / (AST * FB);
     gload(0);
     lstore(0);
     __syncthreads();
-    for (int sg = 0; sg < n_stage; sg++) {
+    for (int sg = 0; sg < n_full; sg++) {
         const int buf = sg & 1;
         if (sg + 1 < n_stage) gload(sg + 1);
 #pragma unroll
+        for (int j = 0; j < AST; j++) block(s_kv[buf] + j * (KVB / 16), (sg * AST + j) * FB, std::false_type{});
+        // the other buffer was last read in the previous stage, before the barrier that ended it
+        if (sg + 1 < n_stage) lstore(buf ^ 1);
+        __syncthreads();
+    }
+    // the last stage, when it holds keys ≥ n_tok (copied to buffer n_full % 2 by the loop's last iteration, or
+    // before the loop when n_full is 0)
+    if (n_full < n_stage) {
+        const int buf = n_full & 1;
         for (int j = 0; j < AST; j++) {
-            const int k0 = (sg * AST + j) * FB;
+            const int k0 = (n_full * AST + j) * FB;
             if (k0 + FB <= n_tok)
                 block(s_kv[buf] + j * (KVB / 16), k0, std::false_type{});
             else if (k0 < n_tok)
                 block(s_kv[buf] + j * (KVB / 16), k0, std::true_type{});
         }
-        // the other buffer was last read in the previous stage, before the barrier that ended it
-        if (sg + 1 < n_stage) lstore(buf ^ 1);
-        __syncthreads();
     }
     if (q0 + c < n_tok) {
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));

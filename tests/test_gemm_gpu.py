@@ -137,9 +137,10 @@ def test_ffn_config4_shape(dev):
 
 # the tile shapes the launch picks (the largest with ≥ 128 workgroups on 256 CUs, else the one with the most):
 # (1, 1024, 2048) 64 × 64; (1023, 1024, 3072) 64 × 64 (the prefill's down); (512, 4096, 1024) 128 × 128;
-# (1024, 4032, 64) 128 × 128 with a last tile half past N; (50, 192, 64) 64 × 64 over 3 column tiles
+# (1024, 4032, 64) 128 × 128 with a last tile half past N; (50, 192, 64) 64 × 64 over 3 column tiles; (2000, 4096,
+# 256) 192 × 256 (176 tiles in one round against 128 of 256 rows), its last tile row 80 rows past M
 @pytest.mark.parametrize("m,n,k", [(1, 1024, 2048), (1023, 1024, 3072), (512, 4096, 1024), (1024, 4032, 64),
-                                   (50, 192, 64)])
+                                   (50, 192, 64), (2000, 4096, 256)])
 def test_gemm_f16_tile_shapes(dev, m, n, k):
     blocks, w16 = f16_weight(m + 3 * n + k, n, k)
     x = x16(5 * m + k, m, k, 0.5)
