@@ -7,12 +7,12 @@ HIP graphs. Each step rewinds the session to 1023 positions, runs one decode ste
 decodes 512 tokens (so every step is the same read).
 
 Also measured in the same run (one JSON line):
-  roofline      the q8_0 matvec kernel at config 0's shape (W [3072 × 1024], x f32[1024], y f32[3072]) over a rotation
+  roofline      the q8_0 matvec kernel at the 3072 × 1024 projection (W [3072 × 1024], x f32[1024], y f32[3072]) over a rotation
                 of 128 distinct W copies (428 MB > the 256 MB Infinity Cache), 128 matvecs per launch; algorithmic
                 bytes 3,358,720 per matvec; HIP events on the library's stream
   matvec        the same kernel one matvec per launch over the rotation (and the 64-copy figure)
-  choose        config 1: windowed penalty + argmax over 151936 logits, 10k seeded steps over 512 rotating buffers
-  attention     config 2: GQA decode attention at 512 / 2048 / 8192 keys over ≥ 256 MB of rotating caches
+  choose        windowed penalty + argmax over 151936 logits, 10k seeded steps over 512 rotating buffers
+  attention     GQA decode attention (16 q / 8 kv heads × 128) at 512 / 2048 / 8192 keys over ≥ 256 MB of rotating caches
   cpu_baseline  the oracle (oracle/, a C restatement of the reference path, OpenMP) decoding on the host cores
 """
 from __future__ import annotations
@@ -239,7 +239,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
 def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
-    """config 4's encoder-layer GEMMs on the matrix cores at one page's 12100 patch rows: q, k, v, o [1024 x 1024],
+    """the vision encoder layer's GEMMs on the matrix cores at one page's 12100 patch rows: q, k, v, o [1024 x 1024],
     gate + up fused with SwiGLU [4096 x 1024] x 2, down [1024 x 4096] (q8_0 weights dequantised to f16 at load)"""
     x16 = dev.upload(synth_normal_f16(71, m * ff))
     y = dev.alloc(m * dim * 4)
@@ -279,7 +279,7 @@ def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
 
 
 def bench_vision_encode(dev, reps=2):
-    """config 4 end to end: one 1540 x 1540 page (12100 patches) through the 24-layer encoder and the projector
+    """the vision encoder end to end: one 1540 x 1540 page (12100 patches) through the 24-layer encoder and the projector
     (3025 x 1024 embeddings left on the device), random-init q8_0 weights"""
     from htr import synth
 
@@ -326,7 +326,7 @@ def bench_copy(dev, mib=512, reps=5):
 def load_traffic():
     """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE
     per dispatch, scaled by what the same counters read for a copy of known size), or None"""
-    f = os.path.join(ROOT, "profiles", "k_dmv_many_cfg0_traffic.json")
+    f = os.path.join(ROOT, "profiles", "k_dmv_many_w3072x1024_traffic.json")
     if not os.path.exists(f):
         return None
     with open(f) as fh:

@@ -238,15 +238,37 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
     for (int j = 0; j < TN; j++) {
         const int col = wrow0 + wn * TN * 32 + 32 * j + (lane & 31);
         if (col >= wrows) continue;  // the part of a last tile past the weight's end
+        if constexpr (EPI == GEMM_ACC && !SPLIT) {
+            // the residual values of two row tiles are loaded before the first of their sums is stored (rows past M
+            // read row M − 1), so 32 loads are in flight together instead of one load, wait and store after another
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+            for (int i0 = 0; i0 < TM; i0 += 2) {
+                constexpr int NB = TM >= 2 ? 2 : 1;
+                float prev[NB][16];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= m) continue;
-                float *o = y + (size_t)row * wrows + col;
-                *o = EPI == GEMM_ACC && !SPLIT ? *o + acc[i][j][r] : acc[i][j][r];
+                for (int i = i0; i < i0 + NB && i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        prev[i - i0][r] = y[(size_t)min(row, m - 1) * wrows + col];
+                    }
+#pragma unroll
+                for (int i = i0; i < i0 + NB && i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < m) y[(size_t)row * wrows + col] = prev[i - i0][r] + acc[i][j][r];
+                    }
             }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < m) y[(size_t)row * wrows + col] = acc[i][j][r];
+                }
+        }
     }
 }
 

@@ -66,7 +66,7 @@ def test_decode_attention_edge_lengths(dev, n_keys):
 
 @pytest.mark.parametrize("L", [512, 2048, 8192])
 def test_config2_attention(dev, L):
-    """config 2: 16 q / 8 kv heads × 128, K / V ~ N(0,1) f16, q ~ N(0,1) → per-head RMSNorm (ε 1e-6, weights
+    """16 q / 8 kv heads × 128, K / V ~ N(0,1) f16, q ~ N(0,1) → per-head RMSNorm (ε 1e-6, weights
     1 + N(0, 0.02)) → RoPE θ = 1e6 at position L; n_keys = L; scale 1/√128; rel-L2 ≤ 1e-3 against fp64"""
     n_head, n_kv, eps = 16, 8, 1e-6
     k = orc.f16_bits(htr.synth_normal(10 + L, L * n_kv * 128)).reshape(L, -1)

@@ -62,7 +62,7 @@ def test_choose_penalty_is_ieee_exact(dev):
 
 
 def config1_inputs(seed: int, rows: int, n_vocab: int = 151936, window: int = 64):
-    """config 1: logits N(0, 3) + 8 planted equal maxima (3 of them on window ids, so the penalty reverses them),
+    """151936 logits N(0, 3) + 8 planted equal maxima (3 of them on window ids, so the penalty reverses them),
     history = 64 ids uniform over the vocabulary with 25 % repeats"""
     logits = np.empty((rows, n_vocab), np.float32)
     hist = np.empty((rows, window), np.int32)
@@ -84,7 +84,7 @@ def config1_inputs(seed: int, rows: int, n_vocab: int = 151936, window: int = 64
 
 
 def test_config1_choice_bit_exact(dev):
-    """config 1 at full size: 64 independent rows in one launch and 16 single launches, each against the oracle"""
+    """the 151936-logit vocabulary: 64 independent rows in one launch and 16 single launches, each against the oracle"""
     rows, n_vocab, window, rp = 64, 151936, 64, 1.1
     logits, hist = config1_inputs(1, rows)
     hb = dev.upload(np.concatenate([hist, np.zeros((rows, 1), np.int32)], axis=1).astype(np.uint32))

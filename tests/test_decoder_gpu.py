@@ -8,8 +8,8 @@ Both compute paths: the F32 path (exact q8_0 values in the prefill GEMMs) is pin
 (the default; X and q·d rounded to f16 in the prefill GEMMs, as the reference on a device with f16) is pinned tightly
 per GEMM (test_gemm_gpu); end to end its logits are only defined to the sensitivity of f16 rounding: on the tiny model
 a 1e-7 relative nudge of the embeddings moves the fp64 forward with f16-rounded GEMM operands by 1.0e-3 rel-L2 (the
-f32 forward: 3.7e-6), on config 3's shape a 2e-7 nudge of one norm moves the oracle's f16 prefill by 1.9e-3 — two
-correct f16-path results in different summation orders differ by that much. Bars: 5e-3 (tiny), 1e-2 (config 3)."""
+f32 forward: 3.7e-6), on the 28-layer decoder's shape a 2e-7 nudge of one norm moves the oracle's f16 prefill by 1.9e-3 — two
+correct f16-path results in different summation orders differ by that much. Bars: 5e-3 (tiny), 1e-2 (28 layers)."""
 import numpy as np
 import pytest
 
@@ -205,7 +205,7 @@ def test_model_and_session_errors(dev, tiny):
 
 
 def test_full_size_decoder_matches_oracle(dev):
-    """config 3's model shape (28 layers, dim 1024, 16 / 8 heads, ffn 3072, vocab 151936, tied head) with a 64-token
+    """the full model shape (28 layers, dim 1024, 16 / 8 heads, ffn 3072, vocab 151936, tied head) with a 64-token
     prompt and 24 greedy tokens (rp 1.1, window 64): prefill logits and the decode teacher-forced against the oracle"""
     cfg, te, on, layers = synth_text_model()
     m = model_on(dev, htr.COMPUTE_F32, cfg, te, on, layers)
@@ -309,7 +309,7 @@ def test_f16_path_other_shapes_use_the_rounding_tiled_kernel(dev):
 
 
 def test_full_size_decoder_f16_path_matches_oracle(dev):
-    """config 3's shape on the f16 path: prefill logits against the oracle's f16-path prefill (bar 1e-2, the path's
+    """the full model shape on the f16 path: prefill logits against the oracle's f16-path prefill (bar 1e-2, the path's
     sensitivity), then 16 greedy tokens teacher-forced against the oracle"""
     cfg, te, on, layers = synth_text_model()
     m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)

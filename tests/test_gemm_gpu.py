@@ -96,8 +96,8 @@ def test_gemm_rejects_bad_shapes(dev):
 
 
 @pytest.mark.parametrize("n,k", [(1024, 1024), (1024, 4096)])
-def test_gemm_config4_shapes(dev, n, k):
-    """config 4's GEMMs: 12100 patch rows (q / k / v / o: 1024 × 1024; down: 1024 × 4096, weights × 64)"""
+def test_gemm_page_shapes(dev, n, k):
+    """the vision page's GEMMs: 12100 patch rows (q / k / v / o: 1024 × 1024; down: 1024 × 4096, weights × 64)"""
     m = 12100
     scale = 64.0 if k == 4096 else 1.0
     blocks, w16 = f16_weight(n + k, n, k, scale)
@@ -111,10 +111,12 @@ def test_gemm_config4_shapes(dev, n, k):
     e = rel_l2(got, want)
     print(f"\n[gemm {m}x{n}x{k}] rel-L2 vs fp64 {e:.2e}")
     assert e < 1e-5
+    htr.gemm_f16(dev, xb, m, w, y, acc=True)  # onto itself: every element doubles exactly
+    assert np.array_equal(y.download(np.float32).reshape(m, n), 2 * got)
     w.free()
 
 
-def test_ffn_config4_shape(dev):
+def test_ffn_page_shape(dev):
     m, n, k = 12100, 4096, 1024
     bg, wg16 = f16_weight(31, n, k)
     bu, wu16 = f16_weight(32, n, k)
@@ -138,21 +140,28 @@ def test_ffn_config4_shape(dev):
 # the tile shapes the launch picks (the largest with ≥ 128 workgroups on 256 CUs, else the one with the most):
 # (1, 1024, 2048) 64 × 64; (1023, 1024, 3072) 64 × 64 (the prefill's down); (512, 4096, 1024) 128 × 128;
 # (1024, 4032, 64) 128 × 128 with a last tile half past N; (50, 192, 64) 64 × 64 over 3 column tiles; (2000, 4096,
-# 256) 192 × 256 (176 tiles in one round against 128 of 256 rows), its last tile row 80 rows past M
+# 256) 192 × 256 (176 tiles in one round against 128 of 256 rows), its last tile row 80 rows past M; (4096, 4096, 64)
+# 256 × 256 (256 tiles in one round against 352 of 192 rows in two)
 @pytest.mark.parametrize("m,n,k", [(1, 1024, 2048), (1023, 1024, 3072), (512, 4096, 1024), (1024, 4032, 64),
-                                   (50, 192, 64), (2000, 4096, 256)])
+                                   (50, 192, 64), (2000, 4096, 256), (4096, 4096, 64)])
 def test_gemm_f16_tile_shapes(dev, m, n, k):
     blocks, w16 = f16_weight(m + 3 * n + k, n, k)
     x = x16(5 * m + k, m, k, 0.5)
     w = htr.Weight(dev, blocks, n, k, f16=True)
+    xb = dev.upload(x)
     y = dev.upload(np.full((m + 3) * n, np.nan, np.float32))
-    htr.gemm_f16(dev, dev.upload(x), m, w, y)
+    htr.gemm_f16(dev, xb, m, w, y)
     got = y.download(np.float32)
     want = x.astype(np.float64) @ w16.astype(np.float64).T
     e = rel_l2(got[: m * n].reshape(m, n), want)
     print(f"\n[gemm f16 {m}x{n}x{k}] rel-L2 vs fp64 {e:.2e}")
     assert e < 1e-5
     assert np.all(np.isnan(got[m * n:]))  # rows past M untouched
+    # the same product accumulated onto itself: p + p is exact in f32, so every element doubles bit for bit
+    htr.gemm_f16(dev, xb, m, w, y, acc=True)
+    got2 = y.download(np.float32)
+    assert np.array_equal(got2[: m * n], 2 * got[: m * n])
+    assert np.all(np.isnan(got2[m * n:]))
     w.free()
 
 

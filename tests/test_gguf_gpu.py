@@ -96,7 +96,7 @@ def test_architecture_and_head_dim_checks(dev):
 
 
 def test_full_size_model_from_a_file(dev, tmp_path):
-    """config 3's shape (633 MB of q8_0) written to a GGUF file and streamed onto the device: the same logits as the
+    """the 28-layer decoder shape (633 MB of q8_0) written to a GGUF file and streamed onto the device: the same logits as the
     host-array model after a 16-token prompt and 4 steps"""
     cfg, te, on, layers = synth_text_model()
     p = tmp_path / "text-q8_0.gguf"

@@ -65,7 +65,7 @@ def test_fused_matvecs_reference_shapes(dev):
 
 @pytest.mark.parametrize("rows,k", [(3072, 1024), (1024, 2048), (1024, 3072), (4096, 1024), (151936, 1024)])
 def test_matvec_decoder_shapes_vs_fp64(dev, rows, k):
-    """config 0's W [3072 × 1024] and every decoder projection shape, including the 151936-row LM head"""
+    """the W [3072 × 1024] projection and every decoder projection shape, including the 151936-row LM head"""
     blocks = htr.synth_q8_0(100 + rows + k, rows, k)
     x = htr.synth_normal(7, k)
     w = htr.Weight(dev, blocks, rows, k)

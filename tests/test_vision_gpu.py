@@ -3,7 +3,7 @@
 Bars: rel-L2 ≤ 2e-3 against the oracle for every output (the stated bar for the vision path; the reference's own
 kernel bars, text.rs:1123-1293, are 1e-3 … 5e-3 against fp64). Tiny encoders at two page sizes (24 and 80 patches:
 one and three key blocks, ragged GEMM tiles), every depth (after the patch embedding, after one layer, the whole
-encoder with the projector); config 4's page (1540 × 1540, 12100 patches) through its first layer."""
+encoder with the projector); a 1540 × 1540 page (12100 patches) through its first layer."""
 import numpy as np
 import pytest
 
@@ -47,8 +47,8 @@ def test_encoder_rejects_unbaked_pages(tiny):
         v.encode(tiny_page(cfg, 56, 56), 3)
 
 
-def test_config4_first_layer_matches_oracle(dev):
-    """config 4's page and encoder shape: 12100 patches, hidden 1024, 16 heads, SwiGLU 4096 — the residual after the
+def test_page_first_layer_matches_oracle(dev):
+    """a page at the encoder's shape: 12100 patches, hidden 1024, 16 heads, SwiGLU 4096 — the residual after the
     patch embedding and after the first layer; then the whole 24-layer encode with the projector (3025 × 1024, finite)"""
     from htr import synth
 
