@@ -214,16 +214,14 @@ int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const f
                     int side, float *P);
 int launch_rms_norm_f16(htr_device *dev, hipStream_t st, const float *x, const float *w, _Float16 *y, int rows, int dim,
                         float eps);
-int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, int n_tok, int n_head, int d_head, int px,
-                  int max_pos);
 // K / V of the vision attention as f16 key blocks of 8 KB per head (vision_kv_bytes in all)
 int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kv, int n_tok,
-                     int n_head);
+                     int n_head, const float *cs, int px, int max_pos);
 size_t vision_kv_bytes(int n_tok, int n_head);
 int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kv, _Float16 *o, int n_tok,
-                       int n_head, float scale);
+                       int n_head, float scale, const float *cs, int px, int max_pos);
 int launch_unfold2x2(htr_device *dev, hipStream_t st, const float *x, float *z, int px, int py, int dim);
 int launch_gelu(htr_device *dev, hipStream_t st, float *x, size_t n);
-// Y[M,N] (+)= X[M,K]·Wᵀ, f32 X, W f32 or f16 (w_f16), any K
-int launch_gemm_f32w(htr_device *dev, hipStream_t st, const float *x, const void *w, bool w_f16, float *y, int m, int n,
-                     int k, int acc);
+// x f32 [m][k] → f16 rows of nseg segments of kp values: hi = f16(x), or lo = f16(x − hi) in the segments of lo_mask
+int launch_split_f16(htr_device *dev, hipStream_t st, const float *x, int m, int k, int kp, int nseg, int lo_mask,
+                     _Float16 *out);

@@ -1,9 +1,11 @@
-// The vision encoder's non-GEMM kernels for gfx950 and the f32 GEMM of its patch embedding and projector.
+// The vision encoder's non-GEMM kernels for gfx950, and the f16 pieces of the f32 operands that its patch embedding
+// and projector multiply on the matrix cores.
 //
 // Reference semantics (the f16 compute path, vision.rs:328-423): patchify.wgsl (normalise + im2col), rms_norm.wgsl /
-// rms_norm_h (gpu.rs:268-275), rope2d.wgsl (+ vision.rs:159-175), heads_f16.wgsl, attention_coop.wgsl (flash attention
-// with q·scale, K, V and P rounded to f16, f32 sums, the output rounded to f16), unfold2x2.wgsl, gelu.wgsl, and the
-// f32 matmul of the patch embedding (K = 588) and the projector (f32 activations, f16-valued weights).
+// rms_norm_h (gpu.rs:268-275), rope2d.wgsl (+ vision.rs:159-175; applied as K and q are read), heads_f16.wgsl,
+// attention_coop.wgsl (flash attention with q·scale, K, V and P rounded to f16, f32 sums, the output rounded to f16),
+// unfold2x2.wgsl, gelu.wgsl; the f32 matmuls of the patch embedding (K = 588) and the projector (f32 activations,
+// f16-valued weights) run as f16 GEMMs over split operands (k_split_f16).
 #include <cmath>
 #include <type_traits>
 
@@ -45,21 +47,19 @@ __global__ __launch_bounds__(VW) void k_rms_norm_rows(const float *x, const floa
     for (int i = tid; i < dim; i += VW) y[base + i] = (T)((x[base + i] * scale) * w[i]);
 }
 
-// rope2d.wgsl in place: pairs (2k, 2k+1) of each half of a head; half 0 at the row t / px, half 1 at the column
-__global__ __launch_bounds__(VW) void k_rope2d(float *Q, const float *cs, int n_tok, int n_head, int d_head, int px,
-                                               int max_pos) {
-    const int nk = d_head / 4;
-    const size_t total = (size_t)n_tok * n_head * 2 * nk;
-    for (size_t i = gid(); i < total; i += gsize()) {
-        const int k = (int)(i % nk), half = (int)((i / nk) % 2), h = (int)((i / (2 * nk)) % n_head);
-        const int t = (int)(i / (2 * nk * n_head));
-        const int pos = half == 0 ? t / px : t % px;
-        const float c = cs[2 * (((size_t)half * max_pos + pos) * nk + k)];
-        const float s = cs[2 * (((size_t)half * max_pos + pos) * nk + k) + 1];
-        float *x = Q + (size_t)t * n_head * d_head + h * d_head + half * (d_head / 2) + 2 * k;
-        const float x0 = x[0], x1 = x[1];
-        x[0] = x0 * c - x1 * s;
-        x[1] = x0 * s + x1 * c;
+// rope2d.wgsl on 8 consecutive dims d0 … d0 + 7 of a head (d0 a multiple of 8, head dim 64), in registers: the
+// pairs (2k, 2k + 1) of each 32-dim half, half 0 turned by the row t / px, half 1 by the column t % px;
+// cs = [half][pos][k] × (cos, sin), 16 pairs a half
+__device__ __forceinline__ void rope8(float (&x)[8], const float *cs, int t, int px, int max_pos, int d0) {
+    const int half = d0 >> 5, k0 = (d0 & 31) >> 1, pos = half == 0 ? t / px : t % px;
+    const float4 *c4 = reinterpret_cast<const float4 *>(cs + 2 * (((size_t)half * max_pos + pos) * 16 + k0));
+    const float4 a = c4[0], b = c4[1];
+    const float c[4] = {a.x, a.z, b.x, b.z}, sn[4] = {a.y, a.w, b.y, b.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float x0 = x[2 * e], x1 = x[2 * e + 1];
+        x[2 * e] = x0 * c[e] - x1 * sn[e];
+        x[2 * e + 1] = x0 * sn[e] + x1 * c[e];
     }
 }
 
@@ -85,10 +85,10 @@ constexpr int KVB = 8192;
 __device__ __forceinline__ int kv_kchunk(int r, int j) { return r * 8 + (j ^ ((r >> 1) & 7)); }
 __device__ __forceinline__ int kv_vchunk(int d, int q) { return 256 + d * 4 + (q ^ ((d >> 2) & 3)); }
 
-// heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16 blocks as above, keys n … ⌈n/32⌉·32 − 1 zero. grid (blocks, H),
-// one block of one head per workgroup; V goes through LDS for the transposition.
+// rope2d.wgsl on K, then heads_f16.wgsl's rounding: K, V f32 [n][H·64] → f16 blocks as above, keys n … ⌈n/32⌉·32 − 1
+// zero. grid (blocks, H), one block of one head per workgroup; V goes through LDS for the transposition.
 __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V, _Float16 *KV, int n_tok, int n_head,
-                                                  int n_blk) {
+                                                  int n_blk, const float *cs, int px, int max_pos) {
     __shared__ _Float16 s_v[32][64 + 2];
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int r = tid >> 3, j8 = tid & 7, t = 32 * b + r;
@@ -99,6 +99,7 @@ __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V
         const float4 k0 = ks[0], k1 = ks[1], v0 = vs[0], v1 = vs[1];
         kv[0] = k0.x, kv[1] = k0.y, kv[2] = k0.z, kv[3] = k0.w, kv[4] = k1.x, kv[5] = k1.y, kv[6] = k1.z, kv[7] = k1.w;
         vv[0] = v0.x, vv[1] = v0.y, vv[2] = v0.z, vv[3] = v0.w, vv[4] = v1.x, vv[5] = v1.y, vv[6] = v1.z, vv[7] = v1.w;
+        rope8(kv, cs, t, px, max_pos, 8 * j8);
     }
     half8 kh;
 #pragma unroll
@@ -129,7 +130,8 @@ __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V
 constexpr int FQ = 32, FB = 32, FWAVES = VW / 64, AST = 2;
 
 __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *KV, _Float16 *O, int n_tok,
-                                                    int n_head, int n_blk, int n_qt, float scale) {
+                                                    int n_head, int n_blk, int n_qt, float scale, const float *cs,
+                                                    int px, int max_pos) {
     __shared__ __attribute__((aligned(16))) half8 s_kv[2][AST * KVB / 16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5, c = lane & 31;
     // workgroup b runs on XCD b % 8: with H a multiple of 8, XCD x takes heads x·H/8 … (x + 1)·H/8 − 1
@@ -144,15 +146,15 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
     }
     const int row = n_head * 64, q0 = (qt * FWAVES + wave) * FQ;
     const int qi = min(q0 + c, n_tok - 1);
-    half8 qf[4];  // B operand of step ks: q16[query c][dims 16ks + 8h … + 7]
+    half8 qf[4];  // B operand of step ks: q16[query c][dims 16ks + 8h … + 7], q turned by rope2d first
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const float4 *src = reinterpret_cast<const float4 *>(Q + (size_t)qi * row + h * 64 + 16 * ks + 8 * hf);
         const float4 x0 = src[0], x1 = src[1];
-        qf[ks][0] = (_Float16)(x0.x * scale), qf[ks][1] = (_Float16)(x0.y * scale);
-        qf[ks][2] = (_Float16)(x0.z * scale), qf[ks][3] = (_Float16)(x0.w * scale);
-        qf[ks][4] = (_Float16)(x1.x * scale), qf[ks][5] = (_Float16)(x1.y * scale);
-        qf[ks][6] = (_Float16)(x1.z * scale), qf[ks][7] = (_Float16)(x1.w * scale);
+        float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        rope8(x, cs, qi, px, max_pos, 16 * ks + 8 * hf);
+#pragma unroll
+        for (int e = 0; e < 8; e++) qf[ks][e] = (_Float16)(x[e] * scale);
     }
     // the lane's fragment chunks within a block: K step ks (key c, dims 16ks + 8h …), Vᵀ tile t step st (dim 32t + c,
     // slots 16st + 8h …)
@@ -295,50 +297,19 @@ __global__ __launch_bounds__(VW) void k_gelu(float *X, size_t n) {
     }
 }
 
-// Y[M,N] (+)= X[M,K]·Wᵀ with f32 X and W of type WT (f32, or f16 read as f32), f32 fma in k order per output;
-// 64 × 64 tiles, K in steps of 16 through LDS, 4 × 4 outputs a thread
-template <typename WT>
-__global__ __launch_bounds__(VW) void k_gemm_f32w(const float *X, const WT *W, float *Y, int m, int n, int k, int acc) {
-    __shared__ float s_x[16][64 + 4];
-    __shared__ float s_w[16][64 + 4];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int row0 = blockIdx.y * 64, col0 = blockIdx.x * 64;
-    float c[4][4] = {};
-    for (int k0 = 0; k0 < k; k0 += 16) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + VW * i, r = e >> 4, kk = e & 15;
-            const int gr = row0 + r, gc = col0 + r, gk = k0 + kk;
-            s_x[kk][r] = gr < m && gk < k ? X[(size_t)gr * k + gk] : 0.0f;
-            s_w[kk][r] = gc < n && gk < k ? (float)W[(size_t)gc * k + gk] : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 16; kk++) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                a[i] = s_x[kk][ty + 16 * i];
-                b[i] = s_w[kk][tx + 16 * i];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) c[i][j] = fmaf(a[i], b[j], c[i][j]);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = row0 + ty + 16 * i;
-        if (r >= m) continue;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int cc = col0 + tx + 16 * j;
-            if (cc >= n) continue;
-            float *o = Y + (size_t)r * n + cc;
-            *o = acc ? *o + c[i][j] : c[i][j];
-        }
+// f32 values as f16 pieces for f32-grade products on the f16 matrix cores: x [m][k] → rows of nseg segments of kp
+// values (kp ≥ k, a multiple of 32, the values past k zero); segment s holds hi = f16(x), or lo = f16(x − hi) where bit
+// s of lo_mask is set. x − hi is exact in f32 and hi + lo is x within 2^-22·|x| (|x| < 65504). With X as [hi, hi, lo]
+// and W as [hi, lo, hi] one f16 GEMM over 3·kp sums xh·wh + xh·wl + xl·wh in f32; f16-valued W: X [hi, lo], W [w, w].
+__global__ __launch_bounds__(VW) void k_split_f16(const float *x, int m, int k, int kp, int nseg, int lo_mask,
+                                                  _Float16 *out) {
+    const size_t total = (size_t)m * kp;
+    for (size_t i = gid(); i < total; i += gsize()) {
+        const int c = (int)(i % kp);
+        const size_t r = i / kp;
+        const float v = c < k ? x[r * k + c] : 0.0f;
+        const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
+        for (int s = 0; s < nseg; s++) out[(r * nseg + s) * kp + c] = (lo_mask >> s) & 1 ? lo : hi;
     }
 }
 
@@ -359,27 +330,26 @@ int launch_rms_norm_f16(htr_device *dev, hipStream_t st, const float *x, const f
     return htr_launched(dev, "k_rms_norm_rows<f16>");
 }
 
-int launch_rope2d(htr_device *dev, hipStream_t st, float *q, const float *cs, int n_tok, int n_head, int d_head, int px,
-                  int max_pos) {
-    hipLaunchKernelGGL(k_rope2d, dim3(grid_for((size_t)n_tok * n_head * d_head / 2)), dim3(VW), 0, st, q, cs, n_tok,
-                       n_head, d_head, px, max_pos);
-    return htr_launched(dev, "k_rope2d");
-}
-
 int launch_heads_f16(htr_device *dev, hipStream_t st, const float *k, const float *v, _Float16 *kv, int n_tok,
-                     int n_head) {
+                     int n_head, const float *cs, int px, int max_pos) {
+    if (px < 1 || (n_tok + px - 1) / px > max_pos || px > max_pos)
+        return htr_fail("vision heads: %d tokens on %d columns, rope table of %d positions", n_tok, px, max_pos);
     const int n_blk = (n_tok + FB - 1) / FB;
-    hipLaunchKernelGGL(k_heads_f16, dim3(n_blk, n_head), dim3(VW), 0, st, k, v, kv, n_tok, n_head, n_blk);
+    hipLaunchKernelGGL(k_heads_f16, dim3(n_blk, n_head), dim3(VW), 0, st, k, v, kv, n_tok, n_head, n_blk, cs, px,
+                       max_pos);
     return htr_launched(dev, "k_heads_f16");
 }
 
 size_t vision_kv_bytes(int n_tok, int n_head) { return (size_t)n_head * ((n_tok + FB - 1) / FB) * KVB; }
 
 int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _Float16 *kv, _Float16 *o, int n_tok,
-                       int n_head, float scale) {
+                       int n_head, float scale, const float *cs, int px, int max_pos) {
     if (n_tok < 1) return htr_fail("vision attention: %d tokens", n_tok);
+    if (px < 1 || (n_tok + px - 1) / px > max_pos || px > max_pos)
+        return htr_fail("vision attention: %d tokens on %d columns, rope table of %d positions", n_tok, px, max_pos);
     const int n_qt = (n_tok + FQ * FWAVES - 1) / (FQ * FWAVES), n_blk = (n_tok + FB - 1) / FB;
-    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kv, o, n_tok, n_head, n_blk, n_qt, scale);
+    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kv, o, n_tok, n_head, n_blk, n_qt, scale,
+                       cs, px, max_pos);
     return htr_launched(dev, "k_attn_vision");
 }
 
@@ -393,12 +363,10 @@ int launch_gelu(htr_device *dev, hipStream_t st, float *x, size_t n) {
     return htr_launched(dev, "k_gelu");
 }
 
-int launch_gemm_f32w(htr_device *dev, hipStream_t st, const float *x, const void *w, bool w_f16, float *y, int m, int n,
-                     int k, int acc) {
-    const dim3 grid((n + 63) / 64, (m + 63) / 64);
-    if (w_f16)
-        hipLaunchKernelGGL(k_gemm_f32w<_Float16>, grid, dim3(VW), 0, st, x, (const _Float16 *)w, y, m, n, k, acc);
-    else
-        hipLaunchKernelGGL(k_gemm_f32w<float>, grid, dim3(VW), 0, st, x, (const float *)w, y, m, n, k, acc);
-    return htr_launched(dev, "k_gemm_f32w");
+int launch_split_f16(htr_device *dev, hipStream_t st, const float *x, int m, int k, int kp, int nseg, int lo_mask,
+                     _Float16 *out) {
+    if (m < 1 || k < 1 || kp < k || kp % 32 || nseg < 1 || nseg > 3)
+        return htr_fail("split_f16: [%d x %d] into %d segments of %d", m, k, nseg, kp);
+    hipLaunchKernelGGL(k_split_f16, dim3(grid_for((size_t)m * kp)), dim3(VW), 0, st, x, m, k, kp, nseg, lo_mask, out);
+    return htr_launched(dev, "k_split_f16");
 }

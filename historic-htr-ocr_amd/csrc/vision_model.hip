@@ -51,6 +51,12 @@ struct htr_vision {
     size_t rgb_cap = 0;
     float *P = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *tmp = nullptr, *cs = nullptr;
     _Float16 *h16 = nullptr, *a16 = nullptr, *g16 = nullptr, *kv = nullptr;
+    // the f32 operands of the patch embedding and the projector as f16 pieces (k_split_f16): the patch embedding
+    // weight [dim][hi | lo | hi] in segments of pe_kp (the patch's 3·p² values padded to a multiple of 32); the
+    // projector weights are stored [w | w]; xs holds an activation's pieces
+    htr_weight *pe = nullptr;
+    int pe_kp = 0;
+    _Float16 *xs = nullptr;
 };
 
 namespace {
@@ -67,13 +73,51 @@ int up_w16(htr_device *dev, const void *h, size_t rows, size_t cols, float scale
     return 0;
 }
 
+// W [N][K] f16 → [N][2K] = [w | w]: the projector's f32 activations go in as [hi | lo] (k_split_f16)
+int widen_w16(htr_device *dev, htr_weight *w) {
+    _Float16 *h2 = nullptr;
+    const size_t n = w->rows, k = w->cols;
+    HTR_TRY(htr_dev_alloc(dev, n * 2 * k * 2, HTR_MEM_WEIGHTS, (void **)&h2));
+    int rc = 0;
+    for (int s = 0; s < 2 && rc == 0; s++)
+        rc = htr_hip(dev, hipMemcpy2DAsync(h2 + s * k, 2 * k * 2, w->h, k * 2, k * 2, n, hipMemcpyDeviceToDevice,
+                                           dev->stream), "widen a projector weight");
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc < 0) {
+        htr_dev_free(dev, h2);
+        return -1;
+    }
+    htr_dev_free(dev, w->h);
+    w->h = h2;
+    w->cols = 2 * k;
+    return 0;
+}
+
+// the f32 patch embedding [dim][3·p²] → the f16 weight [dim][hi | lo | hi] (segments of pe_kp); the f32 copy is freed
+int split_patch_embd(htr_vision *v, size_t pp) {
+    htr_device *dev = v->dev;
+    const int d = v->cfg.dim, kp = (int)((pp + 31) / 32 * 32);
+    auto *w = new htr_weight;
+    w->dev = dev;
+    w->rows = d;
+    w->cols = (size_t)3 * kp;
+    v->pe = w;
+    v->pe_kp = kp;
+    HTR_TRY(htr_dev_alloc(dev, w->rows * w->cols * 2, HTR_MEM_WEIGHTS, (void **)&w->h));
+    HTR_TRY(launch_split_f16(dev, dev->stream, v->patch_embd, d, (int)pp, kp, 3, 0b010, w->h));
+    HTR_TRY(htr_sync(dev));
+    htr_dev_free(dev, v->patch_embd);
+    v->patch_embd = nullptr;
+    return 0;
+}
+
 void free_bufs(htr_vision *v) {
     for (void *p : {(void *)v->rgb, (void *)v->P, (void *)v->x, (void *)v->q, (void *)v->k, (void *)v->v, (void *)v->tmp,
-                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kv})
+                    (void *)v->cs, (void *)v->h16, (void *)v->a16, (void *)v->g16, (void *)v->kv, (void *)v->xs})
         if (p) htr_dev_free(v->dev, p);
     v->rgb = nullptr;
     v->P = v->x = v->q = v->k = v->v = v->tmp = v->cs = nullptr;
-    v->h16 = v->a16 = v->g16 = v->kv = nullptr;
+    v->h16 = v->a16 = v->g16 = v->kv = v->xs = nullptr;
     v->n_cap = v->pos_cap = 0;
     v->rgb_cap = 0;
 }
@@ -98,6 +142,10 @@ int ensure_bufs(htr_vision *v, int n, int max_pos, size_t rgb_bytes) {
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * d * 2, HTR_MEM_WORK, (void **)&v->a16);
         if (rc == 0) rc = htr_dev_alloc(dev, (size_t)n * f * 2, HTR_MEM_WORK, (void **)&v->g16);
         if (rc == 0) rc = htr_dev_alloc(dev, vision_kv_bytes((int)n, c.n_head), HTR_MEM_WORK, (void **)&v->kv);
+        // the split activations: patches [n][3·pe_kp], the merger's input [n/4][2·4d], mm.1 / mm.2's [n/4][2·width]
+        const size_t xs = std::max({(size_t)n * 3 * v->pe_kp, (size_t)(n / 4) * 2 * 4 * d,
+                                    (size_t)(n / 4) * 2 * std::max<size_t>(d, (size_t)c.proj_dim)});
+        if (rc == 0) rc = htr_dev_alloc(dev, xs * 2, HTR_MEM_WORK, (void **)&v->xs);
         if (rc < 0) {
             std::string keep = htr_last_error();
             free_bufs(v);
@@ -121,7 +169,7 @@ extern "C" int htr_vision_free(htr_vision *v) {
         for (float *p : {l.ln1, l.ln2})
             if (p) htr_dev_free(dev, p);
     }
-    for (htr_weight *w : {v->merger, v->mm1, v->mm2}) htr_weight_free(w);
+    for (htr_weight *w : {v->merger, v->mm1, v->mm2, v->pe}) htr_weight_free(w);
     for (float *p : {v->lut, v->patch_embd, v->pre_ln, v->input_norm})
         if (p) htr_dev_free(dev, p);
     delete v;
@@ -142,8 +190,9 @@ extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, 
         return htr_fail("head dim %d (dim %d / %d heads): the attention kernel is written for 64", c.d_head, c.dim,
                         c.n_head);
     if (c.merge != 2 || c.n_ff < 4 * c.dim) return htr_fail("merge %d / n_ff %d: the unfold kernel is 2×2", c.merge, c.n_ff);
-    if (c.dim % 128 || c.n_ff % 128 || c.proj_dim % 32)
-        return htr_fail("dims %d / %d: the matrix-core GEMMs take widths that are multiples of 128", c.dim, c.n_ff);
+    if (c.dim % 128 || c.n_ff % 128 || c.proj_dim % 64)
+        return htr_fail("dims %d / %d / projection %d: the matrix-core GEMMs take widths that are multiples of 128 (the "
+                        "projection: of 64)", c.dim, c.n_ff, c.proj_dim);
     auto *v = new htr_vision;
     v->dev = dev;
     v->cfg = c;
@@ -174,6 +223,9 @@ extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, 
     if (rc == 0) rc = up_w16(dev, merger, d, 4 * d, 1.0f, "mm.patch_merger.weight", &v->merger);
     if (rc == 0) rc = up_w16(dev, mm1, c.proj_dim, d, 1.0f, "mm.1.weight", &v->mm1);
     if (rc == 0) rc = up_w16(dev, mm2, c.proj_dim, c.proj_dim, 1.0f, "mm.2.weight", &v->mm2);
+    for (htr_weight *w : {v->merger, v->mm1, v->mm2})
+        if (rc == 0) rc = widen_w16(dev, w);
+    if (rc == 0) rc = split_patch_embd(v, pp);
     if (rc < 0) {
         std::string keep = htr_last_error();
         htr_vision_free(v);
@@ -217,7 +269,9 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
     const float scale = 1.0f / sqrtf((float)c.d_head);
     const int nl = n_layers < 0 ? c.n_layer : n_layers;
     HTR_TRY(launch_patchify(dev, st, v->rgb, v->lut, width, px, n, c.patch, v->P));
-    HTR_TRY(launch_gemm_f32w(dev, st, v->P, v->patch_embd, false, v->tmp, n, d, pp, 0));
+    // the patch embedding in f32 grade: [xh | xh | xl]·[wh | wl | wh]ᵀ
+    HTR_TRY(launch_split_f16(dev, st, v->P, n, pp, v->pe_kp, 3, 0b100, v->xs));
+    HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->xs, n, v->pe, nullptr, v->tmp, nullptr, 1.0f));
     HTR_TRY(launch_rms_norm(dev, st, v->tmp, v->pre_ln, v->x, n, d, c.eps));
     for (int li = 0; li < nl; li++) {
         const VLayer &l = v->layers[li];
@@ -229,10 +283,9 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
             HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.k, nullptr, v->k, nullptr, 1.0f));
             HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->h16, n, l.v, nullptr, v->v, nullptr, 1.0f));
         }
-        HTR_TRY(launch_rope2d(dev, st, v->q, v->cs, n, c.n_head, c.d_head, px, max_pos));
-        HTR_TRY(launch_rope2d(dev, st, v->k, v->cs, n, c.n_head, c.d_head, px, max_pos));
-        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kv, n, c.n_head));
-        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kv, v->a16, n, c.n_head, scale));
+        // rope2d is applied as K is rounded into its blocks and as the attention reads q
+        HTR_TRY(launch_heads_f16(dev, st, v->k, v->v, v->kv, n, c.n_head, v->cs, px, max_pos));
+        HTR_TRY(launch_attn_vision(dev, st, v->q, v->kv, v->a16, n, c.n_head, scale, v->cs, px, max_pos));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_ACC, v->a16, n, l.o, nullptr, v->x, nullptr, 1.0f));
         HTR_TRY(launch_rms_norm_f16(dev, st, v->x, l.ln2, v->h16, n, d, c.eps));
         HTR_TRY(launch_gemm_f16(dev, st, GEMM_FFN, v->h16, n, l.gate, l.up, nullptr, v->g16, 1.0f / FFN_DOWN_SCALE));
@@ -246,9 +299,13 @@ extern "C" int htr_vision_encode(htr_vision *v, const uint8_t *h_rgb, int width,
     const int n_out = n / 4;
     HTR_TRY(launch_rms_norm(dev, st, v->x, v->input_norm, v->tmp, n, d, c.eps));
     HTR_TRY(launch_unfold2x2(dev, st, v->tmp, v->q, px, py, d));
-    HTR_TRY(launch_gemm_f32w(dev, st, v->q, v->merger->h, true, v->k, n_out, d, 4 * d, 0));
-    HTR_TRY(launch_gemm_f32w(dev, st, v->k, v->mm1->h, true, v->v, n_out, c.proj_dim, d, 0));
+    // the projector's f32 activations as [hi | lo] against its weights [w | w]
+    HTR_TRY(launch_split_f16(dev, st, v->q, n_out, 4 * d, 4 * d, 2, 0b10, v->xs));
+    HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->xs, n_out, v->merger, nullptr, v->k, nullptr, 1.0f));
+    HTR_TRY(launch_split_f16(dev, st, v->k, n_out, d, d, 2, 0b10, v->xs));
+    HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->xs, n_out, v->mm1, nullptr, v->v, nullptr, 1.0f));
     HTR_TRY(launch_gelu(dev, st, v->v, (size_t)n_out * c.proj_dim));
-    HTR_TRY(launch_gemm_f32w(dev, st, v->v, v->mm2->h, true, d_out, n_out, c.proj_dim, c.proj_dim, 0));
+    HTR_TRY(launch_split_f16(dev, st, v->v, n_out, c.proj_dim, c.proj_dim, 2, 0b10, v->xs));
+    HTR_TRY(launch_gemm_f16(dev, st, GEMM_F32, v->xs, n_out, v->mm2, nullptr, d_out, nullptr, 1.0f));
     return htr_sync(dev);
 }

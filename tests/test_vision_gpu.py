@@ -1,9 +1,12 @@
 """The vision encoder on the GPU (vision.rs:328-423, the f16 compute path) against the vision oracle.
 
-Bars: rel-L2 ≤ 2e-3 against the oracle for every output (the stated bar for the vision path; the reference's own
-kernel bars, text.rs:1123-1293, are 1e-3 … 5e-3 against fp64). Tiny encoders at two page sizes (24 and 80 patches:
-one and three key blocks, ragged GEMM tiles), every depth (after the patch embedding, after one layer, the whole
-encoder with the projector); a 1540 × 1540 page (12100 patches) through its first layer."""
+Bars. The stated bar for the vision path is rel-L2 ≤ 2e-3 against the oracle (the reference's own kernel bars,
+text.rs:1123-1293, are 1e-3 … 5e-3 against fp64). It is the bar for a 12100-patch page after one layer: there the f16
+path is chaotic at 1e-3 — the oracle's own output moves by 1.1e-3 when the patch embedding weight is scaled by
+1 + 1e-6·N(0, 1) (7e-4 for 1e-7), so two correct implementations that sum in different orders differ by that much.
+Where the output is not chaotic the bars are tight: 1e-5 after the patch embedding (f32-grade products from f16
+pieces), 2e-4 for the tiny encoders after one layer and through the projector. Tiny encoders at two page sizes (24 and
+80 patches: one and three key blocks, ragged GEMM tiles); a 1540 × 1540 page (12100 patches) through its first layer."""
 import numpy as np
 import pytest
 
@@ -34,7 +37,7 @@ def test_tiny_encoder_matches_oracle(tiny, w, h):
         assert got.shape == want.shape, nl
         e = rel_l2(got, want)
         print(f"\n[vision {w}x{h} layers {nl}] rel-L2 vs oracle {e:.2e}")
-        assert e < 2e-3, nl
+        assert e < (1e-5 if nl == 0 else 2e-4), nl
 
 
 def test_encoder_rejects_unbaked_pages(tiny):
@@ -62,7 +65,7 @@ def test_page_first_layer_matches_oracle(dev):
         want = orc.vision_encode(one, t1, rgb, nl)
         e = rel_l2(got, want)
         print(f"\n[vision 1540x1540 layers {nl}] rel-L2 vs oracle {e:.2e}")
-        assert e < 2e-3, nl
+        assert e < (1e-5 if nl == 0 else 2e-3), nl
     out = v.encode(rgb)
     assert out.shape == (3025, 1024)
     assert np.all(np.isfinite(out))
