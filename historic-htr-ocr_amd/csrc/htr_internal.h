@@ -180,6 +180,9 @@ enum { GEMM_F32 = 0, GEMM_ACC = 1, GEMM_FFN = 2 };
 int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x, int m, const htr_weight *w,
                     const htr_weight *w2, float *y, _Float16 *y16, float scale);
 // Q / K / V of one input as one GEMM over the three stacked weights (rows each a multiple of 64), three f32 outputs
+// y += x·Wᵀ (the residual), then h16 = f16(rmsnorm(y)·norm_w) — in the K-split reduction when the GEMM splits K
+int launch_gemm_f16_acc_norm(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *w, float *y,
+                             const float *norm_w, float eps, _Float16 *h16);
 int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,
                         const htr_weight *wk, const htr_weight *wv, float *q, float *k, float *v);
 

@@ -27,11 +27,14 @@
 //             their X rows and their W rows in its L2;
 //   edges     rows past M read row M − 1 and are not stored; W rows past a weight's end (a last tile that runs over)
 //             are read clamped and not stored. Stacked weights start on tile boundaries. K/32 may be odd.
-// Measured at M = 12100 on one MI355X (256 × 256 tiles): 886 TFLOP/s at N = 8192, K = 1024 and 898 at N = 1024,
-// K = 4096, against ≈ 2.0 PFLOP/s sustained by MFMAs from registers.
+// Measured at M = 12100 on one MI355X: 857 TFLOP/s at N = 8192, K = 1024 (256 × 256 tiles) and 997 at N = 1024,
+// K = 4096 (192 × 256), against ≈ 2.0 PFLOP/s sustained by MFMAs from registers; the clock under this load is about
+// 1.7 GHz, and the LDS traffic of a stage (its fragment reads and the direct loads' writes) is close to what the LDS
+// serves in the stage's MFMA time.
 #include <algorithm>
 
 #include "htr_internal.h"
+#include "wave.h"
 
 namespace {
 
@@ -73,7 +76,53 @@ struct GemmK {
     // into part [split][M][N]; k_split_reduce then adds the slices in split order (onto y with ACC)
     int split, k_per;
     float *part;
+    // ACC with K split: the reduction also writes h16 = f16(rmsnorm(y)·norm_w) when norm_w is set (rows of 1024·NV)
+    const float *norm_w;
+    float eps;
+    _Float16 *norm_out;
 };
+
+// y += ((p_0 + p_1) + p_2) + …, then h = f16(y·1/sqrt(mean(y²) + eps)·w): one row of 1024·NV a workgroup, the sums
+// in k_split_reduce's order and the norm in k_rms_norm_rows4's (a thread's 4·NV values, then the wave and the 4
+// waves), so the result is the two kernels' one after the other
+template <int NV>
+__global__ __launch_bounds__(256) void k_split_reduce_norm(const float *part, int split, size_t stride, float *y,
+                                                           const float *w, float eps, _Float16 *h) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, n = 1024 * NV;
+    const size_t row = blockIdx.x * (size_t)n;
+    float4 v[NV];
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const size_t off = row + 4 * (size_t)(tid + 256 * j);
+        float4 s = *reinterpret_cast<const float4 *>(part + off);
+        for (int q = 1; q < split; q++) {
+            const float4 p = *reinterpret_cast<const float4 *>(part + q * stride + off);
+            s.x += p.x, s.y += p.y, s.z += p.z, s.w += p.w;
+        }
+        const float4 b = *reinterpret_cast<const float4 *>(y + off);
+        s = make_float4(b.x + s.x, b.y + s.y, b.z + s.z, b.w + s.w);
+        *reinterpret_cast<float4 *>(y + off) = s;
+        v[j] = s;
+        s2 = fmaf(s.x, s.x, s2);
+        s2 = fmaf(s.y, s.y, s2);
+        s2 = fmaf(s.z, s.z, s2);
+        s2 = fmaf(s.w, s.w, s2);
+    }
+    s2 = wave_sum(s2, lane);
+    if (lane == 0) red[tid >> 6] = s2;
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)n + eps);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const float4 ww = reinterpret_cast<const float4 *>(w)[tid + 256 * j];
+        const h4 o = {(_Float16)((v[j].x * scale) * ww.x), (_Float16)((v[j].y * scale) * ww.y),
+                      (_Float16)((v[j].z * scale) * ww.z), (_Float16)((v[j].w * scale) * ww.w)};
+        *reinterpret_cast<h4 *>(h + row + 4 * (tid + 256 * j)) = o;
+    }
+}
 
 // y (+)= ((p_0 + p_1) + p_2) + …: the split slices of a GEMM in split order, 4 values a thread
 __global__ __launch_bounds__(256) void k_split_reduce(const float *part, int split, size_t n4, float *y, int acc) {
@@ -304,7 +353,8 @@ template <class T> void launch_tile(hipStream_t st, int epi, const GemmK &a) {
 
 // the largest tile shape that gives at least half a workgroup per CU; else the one with the most tiles (the FFN: 256
 // or 128 — a wave pairs one gate and one up tile)
-int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
+int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a, bool *normed = nullptr) {
+    if (normed) *normed = false;
     if (epi != GEMM_F32 && epi != GEMM_ACC && epi != GEMM_FFN) return htr_fail("gemm_f16: epilogue %d", epi);
     const int want = std::max(1, dev->n_cu / 2);
     int tm, tn;
@@ -342,6 +392,21 @@ int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a) {
             launch_tile<T128>(st, epi, a);
             HTR_TRY(htr_launched(dev, "k_gemm_f16<128, split K>"));
             const size_t n4 = (size_t)a.m * a.rows[0] / 4;
+            const int nv = a.rows[0] % 1024 ? 0 : a.rows[0] / 1024;
+            if (epi == GEMM_ACC && a.norm_w && normed && (nv == 1 || nv == 2 || nv == 4)) {
+                const size_t stride = n4 * 4;
+                if (nv == 1)
+                    hipLaunchKernelGGL(k_split_reduce_norm<1>, dim3(a.m), dim3(256), 0, st, a.part, sp, stride, a.y[0],
+                                       a.norm_w, a.eps, a.norm_out);
+                else if (nv == 2)
+                    hipLaunchKernelGGL(k_split_reduce_norm<2>, dim3(a.m), dim3(256), 0, st, a.part, sp, stride, a.y[0],
+                                       a.norm_w, a.eps, a.norm_out);
+                else
+                    hipLaunchKernelGGL(k_split_reduce_norm<4>, dim3(a.m), dim3(256), 0, st, a.part, sp, stride, a.y[0],
+                                       a.norm_w, a.eps, a.norm_out);
+                *normed = true;
+                return htr_launched(dev, "k_split_reduce_norm");
+            }
             const int grid = (int)std::min<size_t>((n4 + 255) / 256, (size_t)dev->n_cu * 8);
             hipLaunchKernelGGL(k_split_reduce, dim3(grid), dim3(256), 0, st, a.part, sp, n4, a.y[0],
                                epi == GEMM_ACC ? 1 : 0);
@@ -391,6 +456,31 @@ int launch_gemm_f16(htr_device *dev, hipStream_t st, int epi, const _Float16 *x,
     a.k = k;
     a.scale = scale;
     return launch(dev, st, epi, a);
+}
+
+int launch_gemm_f16_acc_norm(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *w, float *y,
+                             const float *norm_w, float eps, _Float16 *h16) {
+    if (!w || !w->h) return htr_fail("gemm_f16: the weight has no f16 plane (htr_weight_q8_0_f16)");
+    const int n = (int)w->rows, k = (int)w->cols;
+    if (m < 1) return htr_fail("gemm_f16: %d rows", m);
+    if (n % 64 || k % 32) return htr_fail("gemm_f16: W [%d x %d]: rows a multiple of 64, columns a multiple of 32", n, k);
+    if (!norm_w || !h16) return htr_fail("gemm_f16: the norm weight and output are required");
+    GemmK a{};
+    a.x = x;
+    a.w[0] = a.w[1] = a.w[2] = w->h;
+    a.n_w = 1;
+    a.rows[0] = a.rows[1] = a.rows[2] = n;
+    a.y[0] = a.y[1] = a.y[2] = y;
+    a.m = m;
+    a.k = k;
+    a.scale = 1.0f;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.norm_out = h16;
+    bool normed = false;
+    HTR_TRY(launch(dev, st, GEMM_ACC, a, &normed));
+    if (!normed) HTR_TRY(launch_rms_norm_f16(dev, st, y, norm_w, h16, m, n, eps));
+    return 0;
 }
 
 int launch_gemm_f16_qkv(htr_device *dev, hipStream_t st, const _Float16 *x, int m, const htr_weight *wq,

@@ -539,21 +539,24 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
     // (h, the attention output and g in the first halves of their f32 rows' space); the FFN's first GEMM fuses SwiGLU
     _Float16 *h16 = (_Float16 *)h, *a16 = (_Float16 *)a, *g16 = (_Float16 *)g;
     if (rc == 0) rc = launch_embed(dev, st, m->tok_embd, d_tok, l, x);
+    // each residual GEMM also writes the next RMS norm's f16 rows (inside its K-split reduction where it splits)
+    if (rc == 0 && m->mfma16) rc = launch_rms_norm_f16(dev, st, x, m->layers[0].attn_norm, h16, l, d, c.eps);
     for (int li = 0; li < c.n_layer && rc == 0 && m->mfma16; li++) {
         const Layer &ly = m->layers[li];
         uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
-        rc = launch_rms_norm_f16(dev, st, x, ly.attn_norm, h16, l, d, c.eps);
-        if (rc == 0) rc = launch_gemm_f16_qkv(dev, st, h16, l, ly.q, ly.k, ly.v, q, k, v);
+        rc = launch_gemm_f16_qkv(dev, st, h16, l, ly.q, ly.k, ly.v, q, k, v);
         if (rc == 0)
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
                                           s->n_ctx, c.eps, kc, vc);
         if (rc == 0)
             rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, s->kvb, nullptr,
                                     a16);
-        if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_ACC, a16, l, ly.o, nullptr, x, nullptr, 1.0f);
-        if (rc == 0) rc = launch_rms_norm_f16(dev, st, x, ly.ffn_norm, h16, l, d, c.eps);
+        if (rc == 0) rc = launch_gemm_f16_acc_norm(dev, st, a16, l, ly.o, x, ly.ffn_norm, c.eps, h16);
         if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_FFN, h16, l, ly.gate, ly.up, nullptr, g16, 1.0f);
-        if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_ACC, g16, l, ly.down, nullptr, x, nullptr, 1.0f);
+        if (rc == 0 && li + 1 < c.n_layer)
+            rc = launch_gemm_f16_acc_norm(dev, st, g16, l, ly.down, x, m->layers[li + 1].attn_norm, c.eps, h16);
+        else if (rc == 0)
+            rc = launch_gemm_f16(dev, st, GEMM_ACC, g16, l, ly.down, nullptr, x, nullptr, 1.0f);
     }
     // the F32 path (exact q8_0 values, f32 sums), or the f16 path's rounding on the tiled kernel for other shapes
     auto gemm = m->compute == HTR_COMPUTE_F32 ? launch_gemm_q8_0_f32 : launch_gemm_q8_0_r16;

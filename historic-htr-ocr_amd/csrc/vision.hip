@@ -47,6 +47,37 @@ __global__ __launch_bounds__(VW) void k_rms_norm_rows(const float *x, const floa
     for (int i = tid; i < dim; i += VW) y[base + i] = (T)((x[base + i] * scale) * w[i]);
 }
 
+// the same for dim = 1024·NV: a thread holds NV float4 of the row, so x is read once, in 16-byte loads
+template <typename T, int NV>
+__global__ __launch_bounds__(VW) void k_rms_norm_rows4(const float *x, const float *w, T *y, int dim, float eps) {
+    __shared__ float red[VW / 64];
+    const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)blockIdx.x * dim);
+    const int tid = threadIdx.x, lane = tid & 63;
+    float4 v[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        v[j] = xr[tid + VW * j];
+        s = fmaf(v[j].x, v[j].x, s);
+        s = fmaf(v[j].y, v[j].y, s);
+        s = fmaf(v[j].z, v[j].z, s);
+        s = fmaf(v[j].w, v[j].w, s);
+    }
+    s = wave_sum(s, lane);
+    if (lane == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)dim + eps);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    typedef T t4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const float4 ww = w4[tid + VW * j];
+        const t4 o = {(T)((v[j].x * scale) * ww.x), (T)((v[j].y * scale) * ww.y), (T)((v[j].z * scale) * ww.z),
+                      (T)((v[j].w * scale) * ww.w)};
+        *reinterpret_cast<t4 *>(y + (size_t)blockIdx.x * dim + 4 * (tid + VW * j)) = o;
+    }
+}
+
 // rope2d.wgsl on 8 consecutive dims d0 … d0 + 7 of a head (d0 a multiple of 8, head dim 64), in registers: the
 // pairs (2k, 2k + 1) of each 32-dim half, half 0 turned by the row t / px, half 1 by the column t % px;
 // cs = [half][pos][k] × (cos, sin), 16 pairs a half
@@ -326,7 +357,12 @@ int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const f
 
 int launch_rms_norm_f16(htr_device *dev, hipStream_t st, const float *x, const float *w, _Float16 *y, int rows, int dim,
                         float eps) {
-    hipLaunchKernelGGL(k_rms_norm_rows<_Float16>, dim3(rows), dim3(VW), 0, st, x, w, y, dim, eps);
+    switch (dim % (4 * VW) ? 0 : dim / (4 * VW)) {
+    case 1: hipLaunchKernelGGL((k_rms_norm_rows4<_Float16, 1>), dim3(rows), dim3(VW), 0, st, x, w, y, dim, eps); break;
+    case 2: hipLaunchKernelGGL((k_rms_norm_rows4<_Float16, 2>), dim3(rows), dim3(VW), 0, st, x, w, y, dim, eps); break;
+    case 4: hipLaunchKernelGGL((k_rms_norm_rows4<_Float16, 4>), dim3(rows), dim3(VW), 0, st, x, w, y, dim, eps); break;
+    default: hipLaunchKernelGGL(k_rms_norm_rows<_Float16>, dim3(rows), dim3(VW), 0, st, x, w, y, dim, eps); break;
+    }
     return htr_launched(dev, "k_rms_norm_rows<f16>");
 }
 
