@@ -443,6 +443,14 @@ class TextConfig:
                            self.n_ctx_train, self.eps, self.rope_base)
 
 
+def seed_for_stem(stem: str) -> int:
+    """presets.rs:114-117 seed_for_stem: a page's sampled-read seed, the first 4 bytes of md5(stem) big-endian (the
+    presets' seedRule int(md5(stem).hexdigest()[:8], 16)); it is the seed Session.generate takes"""
+    import hashlib
+
+    return int.from_bytes(hashlib.md5(stem.encode()).digest()[:4], "big")
+
+
 @dataclass
 class Preset:
     """ocr-decode presets.rs:17-29 (the fields the token choice reads)."""

@@ -1,8 +1,9 @@
 """The CPU choice (ocr-decode sampling.rs:23-89): the oracle's restatement pinned, and the library's htr_choose_host
 against it, bit-exact. Host code only.
 
-Pins of the oracle: SplitMix64's published outputs for state 0 (Steele, Lea, Flood; Vigna's splitmix64.c: 0xe220a8397b1dcdaf,
-0x6e789e6aa1b965f4, 0x06c45d188009454f); the reference's own choose cases (sampling.rs:297-321); and for the sampled
+Pins of the oracle: the presets' seed rule (presets.rs:139-143, md5("abc") → 0x90015098); SplitMix64's published
+outputs for state 0 (Steele, Lea, Flood; Vigna's splitmix64.c: 0xe220a8397b1dcdaf, 0x6e789e6aa1b965f4,
+0x06c45d188009454f); the reference's own choose cases (sampling.rs:297-321); and for the sampled
 branch what the mathematics fixes: a top_p below every probability keeps only the most likely token; the sampled
 frequencies match the top-p kept set renormalised (T = 1: the softmax, T = 2: its square root renormalised), and
 tokens outside the kept set never come."""
@@ -13,6 +14,12 @@ import htr
 import oracle as orc
 
 KAT = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+def test_seed_rule_known_answer():
+    # presets.rs:139-143: int(hashlib.md5(b"abc").hexdigest()[:8], 16) = 0x90015098
+    assert htr.seed_for_stem("abc") == 0x90015098
+    assert htr.seed_for_stem("") == 0xD41D8CD9  # md5("") = d41d8cd9 8f00b204 … (RFC 1321 A.5)
 
 
 def test_rng_known_answers():
