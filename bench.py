@@ -278,7 +278,7 @@ def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
     return res
 
 
-def bench_vision_encode(dev, reps=2):
+def bench_vision_encode(dev, reps=5):
     """the vision encoder end to end: one 1540 x 1540 page (12100 patches) through the 24-layer encoder and the projector
     (3025 x 1024 embeddings left on the device), random-init q8_0 weights"""
     from htr import synth

@@ -27,7 +27,7 @@
 //             their X rows and their W rows in its L2;
 //   edges     rows past M read row M − 1 and are not stored; W rows past a weight's end (a last tile that runs over)
 //             are read clamped and not stored. Stacked weights start on tile boundaries. K/32 may be odd.
-// Measured at M = 12100 on one MI355X: 857 TFLOP/s at N = 8192, K = 1024 (256 × 256 tiles) and 997 at N = 1024,
+// Measured at M = 12100 on one MI355X: 851 TFLOP/s at N = 8192, K = 1024 (256 × 256 tiles) and 1034 at N = 1024,
 // K = 4096 (192 × 256), against ≈ 2.0 PFLOP/s sustained by MFMAs from registers; the clock under this load is about
 // 1.7 GHz, and the LDS traffic of a stage (its fragment reads and the direct loads' writes) is close to what the LDS
 // serves in the stage's MFMA time.
@@ -249,16 +249,15 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
     // one stage: cur holds its fragments; nxt receives stage kt + 1's. The stages in flight at the wait are kt + 1 …
     // kt + ST − 2 (the one to wait for and ST − 3 later ones); the buffer refilled after the barrier held stage kt − 1,
     // which every wave finished reading in the stage before
+    // (no scheduling fences: the memory clobbers keep the loads and LDS reads after the wait and the barrier, and the
+    // compiler interleaves the register-only MFMAs with them — 2–10 % faster than issuing each group as a block)
     auto step = [&](Frag &cur, Frag &nxt, int kt) {
-        __builtin_amdgcn_sched_barrier(0);
         mfma_half(cur, 0);
-        __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((ST - 3) * (AI + BI)) : "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         issue(kt + ST - 1, (kt + ST - 1) % ST);
         read(nxt, kt + 1);
-        __builtin_amdgcn_sched_barrier(0);
         mfma_half(cur, 1);
     };
     int kt = 0;
