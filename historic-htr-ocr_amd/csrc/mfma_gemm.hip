@@ -269,7 +269,7 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS load left in flight when the wave ends
 
     // epilogue: lane ℓ, register r → row 8(r/4) + 4(ℓ/32) + r%4, column ℓ%32 of each 32 × 32 tile
-    if (EPI == GEMM_FFN) {
+    if constexpr (EPI == GEMM_FFN) {
         const int col = tn * (BN / 2) + wn * 32 + (lane & 31);  // gate tile j = 0, up tile j = 1
 #pragma unroll
         for (int i = 0; i < TM; i++)
