@@ -336,7 +336,7 @@ def load_traffic():
 
 def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
     """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores"""
-    # the oracle is the checker: imported here, for the CPU baseline leg only
+    # the oracle (test infrastructure): imported here, for the CPU baseline leg only
     import importlib.util
 
     spec = importlib.util.spec_from_file_location("htr_oracle_py", os.path.join(ROOT, "oracle", "oracle.py"))

@@ -1,7 +1,7 @@
 /*
  * htr_oracle.h — CPU restatement of the reference engine's LightOnOCR decode path (test infrastructure only).
  *
- * This library is the checker, never the product: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * This library checks the product and is never part of it: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it. Every function names the reference file:line it restates (paths relative to the reference
  * repository root; the engine lives in app/crates/ocr-wgpu/src, the decoding policy in app/crates/ocr-decode/src).
  *

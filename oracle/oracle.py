@@ -1,6 +1,6 @@
 """ctypes wrapper of liboracle.so — the CPU restatement of the reference decode path (htr_oracle.h).
 
-TEST INFRASTRUCTURE ONLY. This module is the checker: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+TEST INFRASTRUCTURE ONLY. This module checks the product and is never part of it: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
 import it; the product (historic-htr-ocr_amd/) never does. Each function names the reference lines it restates in
 htr_oracle.h. Built by oracle/Makefile (`make -C oracle`).
 """

@@ -10,7 +10,7 @@ for p in (ROOT, os.path.join(ROOT, "historic-htr-ocr_amd"), os.path.join(ROOT, "
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu on the GPU box")
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu where one is present")
 
 
 @pytest.fixture(scope="session")
