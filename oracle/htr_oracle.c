@@ -1,6 +1,6 @@
 /*
- * htr_oracle.c — CPU restatement of the reference engine's LightOnOCR decode path. TEST INFRASTRUCTURE ONLY: the
- * checker for the HIP library, never linked into it. See htr_oracle.h for the function list, the reference lines each
+ * htr_oracle.c — CPU restatement of the reference engine's LightOnOCR decode path. TEST INFRASTRUCTURE ONLY: it
+ * checks the HIP library and is never linked into it. See htr_oracle.h for the function list, the reference lines each
  * one restates and what pins it.
  *
  * Build: oracle/Makefile (gcc -O2 -fopenmp -ffp-contract=off). f32 arithmetic in the reference kernels' order; every
