@@ -370,6 +370,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, vision")
+    ap.add_argument("--choose-steps", type=int, default=10000,
+                    help="single-launch steps of the choose leg (a counter run takes fewer: every launch is sampled)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this path has no multi-GPU sharding (asked for {args.gpus})", file=sys.stderr)
@@ -417,7 +419,7 @@ def main():
                               "algorithmic_bytes_per_launch": mv["batched_bytes_per_launch"],
                               "avg_launch_us": mv["batched_launch_us"]}
     if want("choose"):
-        result["choose"] = bench_choose(dev)
+        result["choose"] = bench_choose(dev, n_steps=args.choose_steps)
     if want("attention"):
         result["attention"] = bench_attention(dev)
     if want("copy"):
