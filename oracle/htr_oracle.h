@@ -21,7 +21,7 @@
  *   or_session_prefill / or_session_step
  *                                     an independent numpy float64 forward of the same graph (tiny model shape)
  *   or_pixel_lut / or_patchify, or_rope2d_table / or_rope2d, or_unfold2x2, or_gelu, or_rms_norm_h, or_matmul_f16,
- *   or_ffn_f16, or_attention_coop, or_vision_encode
+ *   or_ffn_f16, or_attention_coop, or_vision_encode, or_vision_encode_w16
  *                                     numpy restatements (fp64 closed forms, ggml's rope cache by its own recurrence,
  *                                     torch-unfold index order by brute force), tests/test_vision_oracle.py
  */
@@ -167,6 +167,16 @@ typedef struct {
 int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
                      const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
                      const uint8_t *rgb, int w, int h, int n_layers, float *out);
+/* the same with f16 weight planes (an mmproj's bf16 weights as vision.rs:124-142 converts them at load:
+ * f16(w · scale), the down projection × 64) */
+typedef struct {
+    const float *ln1, *ln2;
+    const uint16_t *q, *k, *v, *o, *gate, *up, *down;
+} or_vision_layer16;
+int or_vision_encode_w16(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln,
+                         const or_vision_layer16 *layers, const float *input_norm, const uint16_t *merger,
+                         const uint16_t *mm1, const uint16_t *mm2, const uint8_t *rgb, int w, int h, int n_layers,
+                         float *out);
 
 #ifdef __cplusplus
 }

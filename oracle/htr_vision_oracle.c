@@ -219,9 +219,17 @@ void or_gelu(float *x, size_t n) {
 
 /* vision.rs:328-423 run_f16 + project on a baked image: n_layers < 0 → every layer and the projector → out
  * [n/4][proj_dim]; n_layers ≥ 0 → the residual after that many layers → out [n][dim]. Returns 0, −1 on bad sizes. */
-int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
-                     const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
-                     const uint8_t *rgb, int w, int h, int n_layers, float *out) {
+/* a weight as the f16 plane its matmul reads: q8_0 blocks dequantised to f16 (× scale: the down projection's 64,
+ * vision.rs:31-35), or (W16) an f16 plane as given — the mmproj's bf16 weights, converted at load with the scale
+ * already applied (f16_from_bf16.wgsl, vision.rs:124-142) */
+static void vision_w(const uint8_t *src, int w16, size_t n, float scale, uint16_t *dst) {
+    if (w16) memcpy(dst, src, n * 2);
+    else or_q8_0_to_f16(src, n, scale, dst);
+}
+
+static int vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
+                         const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
+                         const uint8_t *rgb, int w, int h, int n_layers, float *out, int w16src) {
     const int grid = c->patch * c->merge;
     if (w % grid || h % grid || w <= 0 || h <= 0 || c->d_head != 64 || c->merge != 2) return -1;
     if (n_layers > c->n_layer) return -1;
@@ -243,22 +251,22 @@ int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const floa
     for (int li = 0; li < nl; li++) {
         const or_vision_layer *L = &layers[li];
         or_rms_norm_h(x, L->ln1, h16, n, d, c->eps);
-        or_q8_0_to_f16(L->q, (size_t)d * d, 1.0f, w16);
+        vision_w(L->q, w16src, (size_t)d * d, 1.0f, w16);
         or_matmul_f16(h16, w16, qb, n, d, d, 0);
-        or_q8_0_to_f16(L->k, (size_t)d * d, 1.0f, w16);
+        vision_w(L->k, w16src, (size_t)d * d, 1.0f, w16);
         or_matmul_f16(h16, w16, kb, n, d, d, 0);
-        or_q8_0_to_f16(L->v, (size_t)d * d, 1.0f, w16);
+        vision_w(L->v, w16src, (size_t)d * d, 1.0f, w16);
         or_matmul_f16(h16, w16, vb, n, d, d, 0);
         or_rope2d(qb, n, c->n_head, c->d_head, px, max_pos, cs);
         or_rope2d(kb, n, c->n_head, c->d_head, px, max_pos, cs);
         or_attention_coop(qb, kb, vb, a16, n, c->n_head, scale);
-        or_q8_0_to_f16(L->o, (size_t)d * d, 1.0f, w16);
+        vision_w(L->o, w16src, (size_t)d * d, 1.0f, w16);
         or_matmul_f16(a16, w16, x, n, d, d, 1);
         or_rms_norm_h(x, L->ln2, h16, n, d, c->eps);
-        or_q8_0_to_f16(L->gate, (size_t)f * d, 1.0f, w16);
-        or_q8_0_to_f16(L->up, (size_t)f * d, 1.0f, w16b);
+        vision_w(L->gate, w16src, (size_t)f * d, 1.0f, w16);
+        vision_w(L->up, w16src, (size_t)f * d, 1.0f, w16b);
         or_ffn_f16(h16, w16, w16b, g16, n, f, d, 1.0f / 64.0f);
-        or_q8_0_to_f16(L->down, (size_t)d * f, 64.0f, w16);
+        vision_w(L->down, w16src, (size_t)d * f, 64.0f, w16);
         or_matmul_f16(g16, w16, x, n, d, f, 1);
     }
     int rc = 0;
@@ -273,14 +281,14 @@ int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const floa
         uint16_t *wh = malloc((size_t)d * 4 * d * 2);
         or_rms_norm(x, input_norm, tmp, n, d, c->eps);
         or_unfold2x2(tmp, z, px, py, d);
-        or_q8_0_to_f16(merger, (size_t)d * 4 * d, 1.0f, wh);
+        vision_w(merger, w16src, (size_t)d * 4 * d, 1.0f, wh);
         for (size_t i = 0; i < (size_t)d * 4 * d; i++) wf[i] = or_f32_from_f16(wh[i]);
         or_matmul_f32(z, wf, mg, n_out, d, 4 * d, 0);
-        or_q8_0_to_f16(mm1, (size_t)pd * d, 1.0f, wh);
+        vision_w(mm1, w16src, (size_t)pd * d, 1.0f, wh);
         for (size_t i = 0; i < (size_t)pd * d; i++) wf[i] = or_f32_from_f16(wh[i]);
         or_matmul_f32(mg, wf, m1, n_out, pd, d, 0);
         or_gelu(m1, (size_t)n_out * pd);
-        or_q8_0_to_f16(mm2, (size_t)pd * pd, 1.0f, wh);
+        vision_w(mm2, w16src, (size_t)pd * pd, 1.0f, wh);
         for (size_t i = 0; i < (size_t)pd * pd; i++) wf[i] = or_f32_from_f16(wh[i]);
         or_matmul_f32(m1, wf, out, n_out, pd, pd, 0);
         free(z);
@@ -301,5 +309,30 @@ int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const floa
     free(w16);
     free(w16b);
     free(cs);
+    return rc;
+}
+
+int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
+                     const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
+                     const uint8_t *rgb, int w, int h, int n_layers, float *out) {
+    return vision_encode(c, patch_embd, pre_ln, layers, input_norm, merger, mm1, mm2, rgb, w, h, n_layers, out, 0);
+}
+
+int or_vision_encode_w16(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln,
+                         const or_vision_layer16 *layers, const float *input_norm, const uint16_t *merger,
+                         const uint16_t *mm1, const uint16_t *mm2, const uint8_t *rgb, int w, int h, int n_layers,
+                         float *out) {
+    or_vision_layer *l8 = malloc((size_t)c->n_layer * sizeof(or_vision_layer));
+    if (!l8) return -1;
+    for (int i = 0; i < c->n_layer; i++) {
+        const or_vision_layer16 *s = &layers[i];
+        or_vision_layer t = {s->ln1, s->ln2, (const uint8_t *)s->q, (const uint8_t *)s->k, (const uint8_t *)s->v,
+                             (const uint8_t *)s->o, (const uint8_t *)s->gate, (const uint8_t *)s->up,
+                             (const uint8_t *)s->down};
+        l8[i] = t;
+    }
+    const int rc = vision_encode(c, patch_embd, pre_ln, l8, input_norm, (const uint8_t *)merger, (const uint8_t *)mm1,
+                                 (const uint8_t *)mm2, rgb, w, h, n_layers, out, 1);
+    free(l8);
     return rc;
 }

@@ -67,6 +67,7 @@ def lib() -> C.CDLL:
             "or_unfold2x2": (None, [vp, vp, i32, i32, i32]),
             "or_gelu": (None, [vp, sz]),
             "or_vision_encode": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+            "or_vision_encode_w16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -423,9 +424,11 @@ class VisionLayerC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")]
 
 
-def vision_encode(cfg: dict, t: dict, rgb: np.ndarray, n_layers: int = -1) -> np.ndarray:
+def vision_encode(cfg: dict, t: dict, rgb: np.ndarray, n_layers: int = -1, w16: bool = False) -> np.ndarray:
     """vision.rs run_f16 + project on the host tensors `t` (q8_0 blocks / f32): n_layers < 0 → the projected
-    embeddings [n/4][proj_dim]; else the residual after n_layers layers [n][dim]"""
+    embeddings [n/4][proj_dim]; else the residual after n_layers layers [n][dim]. w16: the layer and projector
+    weights are f16 planes (uint16 [rows][cols], the down projection already × 64), as an mmproj's bf16 weights are
+    converted at load (vision.rs:124-142)"""
     c = VisionCfg(cfg["n_layer"], cfg["dim"], cfg["n_head"], 64, cfg["n_ff"], cfg["patch"], 2, cfg["proj_dim"],
                   cfg["eps"], cfg["rope_theta"], (C.c_float * 3)(*cfg["mean"]), (C.c_float * 3)(*cfg["std"]))
     arr = (VisionLayerC * cfg["n_layer"])()
@@ -435,8 +438,9 @@ def vision_encode(cfg: dict, t: dict, rgb: np.ndarray, n_layers: int = -1) -> np
     n = (h // cfg["patch"]) * (w // cfg["patch"])
     out = np.empty((n, cfg["dim"]) if n_layers >= 0 else (n // 4, cfg["proj_dim"]), np.float32)
     rgb = np.ascontiguousarray(rgb, np.uint8)
-    rc = lib().or_vision_encode(C.byref(c), _p(t["patch_embd"]), _p(t["pre_ln"]), arr, _p(t["input_norm"]),
-                                _p(t["merger"]), _p(t["mm1"]), _p(t["mm2"]), _p(rgb), w, h, n_layers, _p(out))
+    fn = lib().or_vision_encode_w16 if w16 else lib().or_vision_encode
+    rc = fn(C.byref(c), _p(t["patch_embd"]), _p(t["pre_ln"]), arr, _p(t["input_norm"]),
+            _p(t["merger"]), _p(t["mm1"]), _p(t["mm2"]), _p(rgb), w, h, n_layers, _p(out))
     if rc != 0:
         raise ValueError("oracle vision_encode: unsupported size")
     return out

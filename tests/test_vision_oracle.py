@@ -228,3 +228,32 @@ def test_vision_encode_matches_numpy_forward():
         assert e < 2e-3, (nl, e)
     with pytest.raises(ValueError):
         orc.vision_encode(cfg, t, rgb[:70], -1)  # 70 rows: not on the 28-pixel grid
+
+
+def f16_planes(cfg, t):
+    """the f16 weight planes an mmproj load would hold for the q8_0 tensors of `t` (f16 of the exact dequant; the
+    down projection × 64, as vision.rs:124-142 and 31-35 scale it)"""
+    d, f, pd = cfg["dim"], cfg["n_ff"], cfg["proj_dim"]
+    shapes = dict(q=(d, d), k=(d, d), v=(d, d), o=(d, d), gate=(f, d), up=(f, d), down=(d, f))
+    layers = []
+    for ly in t["layers"]:
+        p = dict(ln1=ly["ln1"], ln2=ly["ln2"])
+        for name, (r, c) in shapes.items():
+            p[name] = orc.q8_0_to_f16(ly[name], r, c, 64.0 if name == "down" else 1.0)
+        layers.append(p)
+    return dict(patch_embd=t["patch_embd"], pre_ln=t["pre_ln"], layers=layers, input_norm=t["input_norm"],
+                merger=orc.q8_0_to_f16(t["merger"], d, 4 * d), mm1=orc.q8_0_to_f16(t["mm1"], pd, d),
+                mm2=orc.q8_0_to_f16(t["mm2"], pd, pd))
+
+
+def test_vision_encode_on_f16_planes_is_the_q8_0_encode():
+    """the oracle's f16-plane entry (weights converted at load) on the planes the q8_0 path converts to inside: the
+    same output bit for bit at every depth"""
+    cfg = tiny_vision_cfg()
+    t = tiny_vision_tensors(cfg)
+    t16 = f16_planes(cfg, t)
+    rgb = tiny_page(cfg)
+    for nl in (0, 1, -1):
+        a = orc.vision_encode(cfg, t, rgb, nl)
+        b = orc.vision_encode(cfg, t16, rgb, nl, w16=True)
+        assert np.array_equal(a, b), nl
