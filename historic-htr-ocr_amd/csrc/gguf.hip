@@ -256,7 +256,63 @@ __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t *blk, size_t 
     }
 }
 
+// a vision weight's values (BF16 or F32, n of them, starting on an even element of the tensor) × scale → f16 (OUT_F32:
+// the f16 values widened to f32 for a BF16 source, an F32 source's own values). f16_from_bf16.wgsl: each pair of
+// values (one 32-bit word of a BF16 tensor) holding a magnitude above 65504 counts once into *over
+template <bool BF16, bool OUT_F32>
+__global__ __launch_bounds__(256) void k_vision_weight(const void *src, size_t n, float scale, void *dst,
+                                                       unsigned *over) {
+    const size_t pairs = (n + 1) / 2;
+    for (size_t p = blockIdx.x * (size_t)256 + threadIdx.x; p < pairs; p += (size_t)gridDim.x * 256) {
+        const size_t i = 2 * p;
+        const bool two = i + 1 < n;
+        float v0, v1 = 0.0f;
+        if constexpr (BF16) {
+            const uint16_t *s = static_cast<const uint16_t *>(src);
+            v0 = __uint_as_float((uint32_t)s[i] << 16);
+            if (two) v1 = __uint_as_float((uint32_t)s[i + 1] << 16);
+        } else {
+            const float *s = static_cast<const float *>(src);
+            v0 = s[i];
+            if (two) v1 = s[i + 1];
+        }
+        v0 *= scale;
+        v1 *= scale;
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        if constexpr (OUT_F32) {
+            float *d = static_cast<float *>(dst);
+            d[i] = BF16 ? (float)h0 : v0;
+            if (two) d[i + 1] = BF16 ? (float)h1 : v1;
+        } else {
+            _Float16 *d = static_cast<_Float16 *>(dst);
+            d[i] = h0;
+            if (two) d[i + 1] = h1;
+        }
+        if constexpr (BF16 || !OUT_F32) {
+            // one atomic a wave: lane 0 is active whenever any lane of its wave is (p rises with the lane)
+            const unsigned long long m = __ballot(fabsf(v0) > 65504.0f || fabsf(v1) > 65504.0f);
+            if ((threadIdx.x & 63) == 0 && m) atomicAdd(over, (unsigned)__popcll(m));
+        }
+    }
+}
+
 }  // namespace
+
+std::string gguf_shape_str(const GgufTensor &t) {
+    std::string s = "[";
+    for (uint32_t k = 0; k < t.n_dims; k++) s += (k ? ", " : "") + std::to_string(t.shape[k]);
+    return s + "]";
+}
+
+const char *ggml_type_name(uint32_t ty) {
+    switch (ty) {
+    case GGUF_F32: return "F32";
+    case GGUF_F16: return "F16";
+    case GGUF_Q8_0: return "Q8_0";
+    case GGUF_BF16: return "BF16";
+    default: return "an unknown ggml type";
+    }
+}
 
 // ---- the streaming upload ---------------------------------------------------------------------------------------------
 
@@ -350,6 +406,68 @@ int gguf_upload_f32(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t n, 
         return htr_fail("hipMemcpyAsync: %s", hipGetErrorString(e));
     if ((e = hipEventRecord(sg.ev[i], sg.dev->stream)) != hipSuccess)
         return htr_fail("hipEventRecord: %s", hipGetErrorString(e));
+    return 0;
+}
+
+// vision.rs:117-142 weight(): the shape check ([cols…, rows]: the last dimension is the output row), BF16 or F32,
+// then the device conversion of each staged range into dst16 (f16) or dst32 (f32)
+int gguf_upload_vision(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t rows, size_t cols, float scale,
+                       unsigned *d_over, _Float16 *dst16, float *dst32) {
+    htr_device *dev = sg.dev;
+    uint64_t inner = 1;
+    for (uint32_t k = 0; k + 1 < t.n_dims; k++) inner *= t.shape[k];
+    if (t.n_dims < 1 || t.shape[t.n_dims - 1] != rows || inner != cols)
+        return htr_fail("%s: shape %s, expected %zu values × %zu rows", t.name, gguf_shape_str(t).c_str(), cols, rows);
+    if (t.type != GGUF_BF16 && t.type != GGUF_F32)
+        return htr_fail("%s: %s weights are not supported in the vision encoder", t.name, ggml_type_name(t.type));
+    const bool bf16 = t.type == GGUF_BF16;
+    const size_t es = bf16 ? 2 : 4, n = rows * cols;
+    const size_t per = STAGE_BYTES / 4 / 256 * 256;  // values a staged range: even, whole for either width
+    for (size_t e0 = 0; e0 < n; e0 += per) {
+        const size_t ne = std::min(per, n - e0);
+        const int i = sg.next;
+        sg.next ^= 1;
+        hipError_t e = hipEventSynchronize(sg.ev[i]);
+        if (e != hipSuccess) return htr_fail("hipEventSynchronize: %s", hipGetErrorString(e));
+        HTR_TRY(src_read(g, t.file_offset + es * (uint64_t)e0, sg.host[i], ne * es));
+        if ((e = hipMemcpyAsync(sg.dev_buf[i], sg.host[i], ne * es, hipMemcpyHostToDevice, dev->stream)) != hipSuccess)
+            return htr_fail("hipMemcpyAsync: %s", hipGetErrorString(e));
+        const int grid = (int)std::min<size_t>((ne / 2 + 256) / 256, (size_t)dev->n_cu * 8);
+        void *dst = dst32 ? (void *)(dst32 + e0) : (void *)(dst16 + e0);
+        if (bf16 && dst32)
+            hipLaunchKernelGGL((k_vision_weight<true, true>), dim3(grid), dim3(256), 0, dev->stream, sg.dev_buf[i], ne,
+                               scale, dst, d_over);
+        else if (bf16)
+            hipLaunchKernelGGL((k_vision_weight<true, false>), dim3(grid), dim3(256), 0, dev->stream, sg.dev_buf[i], ne,
+                               scale, dst, d_over);
+        else if (dst32)
+            hipLaunchKernelGGL((k_vision_weight<false, true>), dim3(grid), dim3(256), 0, dev->stream, sg.dev_buf[i], ne,
+                               scale, dst, d_over);
+        else
+            hipLaunchKernelGGL((k_vision_weight<false, false>), dim3(grid), dim3(256), 0, dev->stream, sg.dev_buf[i],
+                               ne, scale, dst, d_over);
+        HTR_TRY(htr_launched(dev, "k_vision_weight"));
+        if ((e = hipEventRecord(sg.ev[i], dev->stream)) != hipSuccess)
+            return htr_fail("hipEventRecord: %s", hipGetErrorString(e));
+    }
+    return 0;
+}
+
+int gguf_meta_bool(htr_gguf *g, const char *key, bool *out) {
+    const Value *v = meta(g, key);
+    if (!v) return -1;
+    if (v->type != 7) return htr_fail("%s is of GGUF type %u, not bool", key, v->type);
+    *out = v->u != 0;
+    return 0;
+}
+
+int gguf_meta_f32_array(htr_gguf *g, const char *key, std::vector<float> *out) {
+    const Value *v = meta(g, key);
+    if (!v) return -1;
+    if (v->type != 9) return htr_fail("%s is of GGUF type %u, not an array", key, v->type);
+    if (v->elem != 6) return htr_fail("%s holds GGUF type %u, not f32", key, v->elem);
+    out->clear();
+    for (const Value &x : v->arr) out->push_back((float)x.f);
     return 0;
 }
 

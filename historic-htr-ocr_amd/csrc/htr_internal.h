@@ -9,6 +9,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "htr.h"
 
@@ -211,6 +212,15 @@ int gguf_meta_str(htr_gguf *g, const char *key, std::string *out);
 // device's stream: synchronise before the staging goes away)
 int gguf_upload_q8_0(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t rows, size_t cols, htr_weight **out);
 int gguf_upload_f32(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t n, float **out);
+// a vision weight [rows][cols] (BF16 or F32 in the file) streamed onto the device into dst16 (f16 of value × scale) or
+// dst32 (a BF16 tensor's f16 values as f32, an F32 tensor's own); pairs of values beyond f16's range counted into
+// d_over (device u32)
+int gguf_upload_vision(GgufStager &sg, htr_gguf *g, const GgufTensor &t, size_t rows, size_t cols, float scale,
+                       unsigned *d_over, _Float16 *dst16, float *dst32);
+int gguf_meta_bool(htr_gguf *g, const char *key, bool *out);
+int gguf_meta_f32_array(htr_gguf *g, const char *key, std::vector<float> *out);
+const char *ggml_type_name(uint32_t ty);
+std::string gguf_shape_str(const GgufTensor &t);  // "[a, b, …]"
 
 // the vision encoder's other kernels (vision.hip)
 int launch_patchify(htr_device *dev, hipStream_t st, const uint8_t *rgb, const float *lut, int w, int px, int n,

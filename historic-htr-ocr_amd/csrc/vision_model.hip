@@ -176,13 +176,88 @@ extern "C" int htr_vision_free(htr_vision *v) {
     return 0;
 }
 
-// Vision::from_gguf (vision.rs:177-233) from host tensors
-extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, const float *patch_embd,
-                                 const float *pre_ln, const htr_vision_layer *layers, const float *input_norm,
-                                 const void *merger, const void *mm1, const void *mm2, htr_vision **out) {
-    HTR_TRY(htr_check_alive(dev));
-    if (!cfg || !layers || !out) return htr_fail("htr_vision_create: null argument");
-    const htr_vision_config &c = *cfg;
+namespace {
+
+// where the encoder's tensors come from: host arrays (htr_vision_create) or an mmproj GGUF (htr_vision_load_gguf).
+// Names are the GGUF's (v.blk.{i}.attn_q.weight …); w16 fills an f16 [rows][cols] plane (× scale), patch an f32 one
+struct VisionFeed {
+    virtual int w16(int layer, const char *kind, size_t rows, size_t cols, float scale, htr_weight **out) = 0;
+    virtual int vec(int layer, const char *kind, size_t n, float **out) = 0;
+    virtual int patch(size_t rows, size_t cols, float **out) = 0;
+    virtual ~VisionFeed() = default;
+    static std::string name(int layer, const char *kind) {
+        return layer < 0 ? std::string(kind) + ".weight" : "v.blk." + std::to_string(layer) + "." + kind + ".weight";
+    }
+};
+
+struct ArrayVisionFeed : VisionFeed {
+    htr_device *dev;
+    const htr_vision_layer *layers;
+    const float *patch_embd, *pre_ln, *input_norm;
+    const void *merger, *mm1, *mm2;
+    int w16(int layer, const char *kind, size_t rows, size_t cols, float scale, htr_weight **out) override {
+        const std::string k = kind;
+        const void *h = k == "mm.patch_merger" ? merger : k == "mm.1" ? mm1 : mm2;
+        if (layer >= 0) {
+            const htr_vision_layer &t = layers[layer];
+            h = k == "attn_q" ? t.q : k == "attn_k" ? t.k : k == "attn_v" ? t.v : k == "attn_out" ? t.o
+                : k == "ffn_gate" ? t.gate : k == "ffn_up" ? t.up : t.down;
+        }
+        return up_w16(dev, h, rows, cols, scale, name(layer, kind).c_str(), out);
+    }
+    int vec(int layer, const char *kind, size_t n, float **out) override {
+        const std::string k = kind;
+        const float *h = k == "v.pre_ln" ? pre_ln : input_norm;
+        if (layer >= 0) h = k == "ln1" ? layers[layer].ln1 : layers[layer].ln2;
+        return up_vec(dev, h, n, name(layer, kind).c_str(), out);
+    }
+    int patch(size_t rows, size_t cols, float **out) override {
+        return up_vec(dev, patch_embd, rows * cols, "v.patch_embd.weight", out);
+    }
+};
+
+struct GgufVisionFeed : VisionFeed {
+    htr_gguf *g;
+    GgufStager sg;
+    unsigned *over = nullptr;  // device u32: pairs of values beyond f16's range
+    explicit GgufVisionFeed(htr_gguf *gg) : g(gg) {}
+    ~GgufVisionFeed() override {
+        if (over) htr_dev_free(sg.dev, over);
+    }
+    int w16(int layer, const char *kind, size_t rows, size_t cols, float scale, htr_weight **out) override {
+        const GgufTensor *t;
+        HTR_TRY(gguf_find(g, name(layer, kind).c_str(), &t));
+        auto *w = new htr_weight;
+        w->dev = sg.dev;
+        w->rows = rows;
+        w->cols = cols;
+        int rc = htr_dev_alloc(sg.dev, rows * cols * 2, HTR_MEM_WEIGHTS, (void **)&w->h);
+        if (rc == 0) rc = gguf_upload_vision(sg, g, *t, rows, cols, scale, over, w->h, nullptr);
+        if (rc < 0) {
+            std::string keep = htr_last_error();
+            htr_weight_free(w);
+            return htr_fail("%s", keep.c_str());
+        }
+        *out = w;
+        return 0;
+    }
+    int vec(int layer, const char *kind, size_t n, float **out) override {
+        const GgufTensor *t;
+        HTR_TRY(gguf_find(g, name(layer, kind).c_str(), &t));
+        if (t->type != GGUF_F32 || t->n_dims != 1 || t->shape[0] != n)  // vision.rs:144-150
+            return htr_fail("%s: %s %s, expected F32 [%zu]", t->name, ggml_type_name(t->type), gguf_shape_str(*t).c_str(),
+                            n);
+        return gguf_upload_f32(sg, g, *t, n, out);
+    }
+    int patch(size_t rows, size_t cols, float **out) override {
+        const GgufTensor *t;
+        HTR_TRY(gguf_find(g, "v.patch_embd.weight", &t));
+        HTR_TRY(htr_dev_alloc(sg.dev, rows * cols * 4, HTR_MEM_WEIGHTS, (void **)out));
+        return gguf_upload_vision(sg, g, *t, rows, cols, 1.0f, over, nullptr, *out);
+    }
+};
+
+int check_vision_cfg(const htr_vision_config &c) {
     if (c.n_layer < 1 || c.dim < 64 || c.n_head < 1 || c.patch < 1 || c.proj_dim < 1 || c.n_ff < 1)
         return htr_fail("vision config: %d layers, dim %d, %d heads, patch %d, projection %d, ffn %d", c.n_layer, c.dim,
                         c.n_head, c.patch, c.proj_dim, c.n_ff);
@@ -193,45 +268,147 @@ extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, 
     if (c.dim % 128 || c.n_ff % 128 || c.proj_dim % 64)
         return htr_fail("dims %d / %d / projection %d: the matrix-core GEMMs take widths that are multiples of 128 (the "
                         "projection: of 64)", c.dim, c.n_ff, c.proj_dim);
-    auto *v = new htr_vision;
+    return 0;
+}
+
+// Vision::from_gguf's body (vision.rs:196-227) over either feed, in its order: the layers, then the patch embedding,
+// pre_ln, the projector. Then the device forms of the f32-activation products (projector [w | w], patch [hi | lo | hi])
+int build_vision(htr_device *dev, const htr_vision_config &c, VisionFeed &feed, htr_vision *v) {
     v->dev = dev;
     v->cfg = c;
     v->layers.resize(c.n_layer);
     const size_t d = c.dim, f = c.n_ff, pp = 3 * (size_t)c.patch * c.patch;
+    for (int i = 0; i < c.n_layer; i++) {
+        VLayer &l = v->layers[i];
+        HTR_TRY(feed.vec(i, "ln1", d, &l.ln1));
+        HTR_TRY(feed.vec(i, "ln2", d, &l.ln2));
+        HTR_TRY(feed.w16(i, "attn_q", d, d, 1.0f, &l.q));
+        HTR_TRY(feed.w16(i, "attn_k", d, d, 1.0f, &l.k));
+        HTR_TRY(feed.w16(i, "attn_v", d, d, 1.0f, &l.v));
+        HTR_TRY(feed.w16(i, "attn_out", d, d, 1.0f, &l.o));
+        HTR_TRY(feed.w16(i, "ffn_gate", f, d, 1.0f, &l.gate));
+        HTR_TRY(feed.w16(i, "ffn_up", f, d, 1.0f, &l.up));
+        HTR_TRY(feed.w16(i, "ffn_down", d, f, FFN_DOWN_SCALE, &l.down));
+    }
     // vision.rs:143-146 pixel_lut
     std::vector<float> lut(768);
     for (int ch = 0; ch < 3; ch++)
         for (int i = 0; i < 256; i++) lut[ch * 256 + i] = ((float)i / 255.0f - c.mean[ch]) / c.std[ch];
-    int rc = up_vec(dev, lut.data(), 768, "pixel lut", &v->lut);
-    if (rc == 0) rc = up_vec(dev, patch_embd, d * pp, "v.patch_embd.weight", &v->patch_embd);
-    if (rc == 0) rc = up_vec(dev, pre_ln, d, "v.pre_ln.weight", &v->pre_ln);
-    for (int i = 0; i < c.n_layer && rc == 0; i++) {
-        const htr_vision_layer &t = layers[i];
-        VLayer &l = v->layers[i];
-        rc = up_vec(dev, t.ln1, d, "ln1", &l.ln1);
-        if (rc == 0) rc = up_vec(dev, t.ln2, d, "ln2", &l.ln2);
-        if (rc == 0) rc = up_w16(dev, t.q, d, d, 1.0f, "attn_q", &l.q);
-        if (rc == 0) rc = up_w16(dev, t.k, d, d, 1.0f, "attn_k", &l.k);
-        if (rc == 0) rc = up_w16(dev, t.v, d, d, 1.0f, "attn_v", &l.v);
-        if (rc == 0) rc = up_w16(dev, t.o, d, d, 1.0f, "attn_out", &l.o);
-        if (rc == 0) rc = up_w16(dev, t.gate, f, d, 1.0f, "ffn_gate", &l.gate);
-        if (rc == 0) rc = up_w16(dev, t.up, f, d, 1.0f, "ffn_up", &l.up);
-        if (rc == 0) rc = up_w16(dev, t.down, d, f, FFN_DOWN_SCALE, "ffn_down", &l.down);
-        if (rc < 0) rc = htr_fail("v.blk.%d: %s", i, std::string(htr_last_error()).c_str());
-    }
-    if (rc == 0) rc = up_vec(dev, input_norm, d, "mm.input_norm.weight", &v->input_norm);
-    if (rc == 0) rc = up_w16(dev, merger, d, 4 * d, 1.0f, "mm.patch_merger.weight", &v->merger);
-    if (rc == 0) rc = up_w16(dev, mm1, c.proj_dim, d, 1.0f, "mm.1.weight", &v->mm1);
-    if (rc == 0) rc = up_w16(dev, mm2, c.proj_dim, c.proj_dim, 1.0f, "mm.2.weight", &v->mm2);
-    for (htr_weight *w : {v->merger, v->mm1, v->mm2})
-        if (rc == 0) rc = widen_w16(dev, w);
-    if (rc == 0) rc = split_patch_embd(v, pp);
+    HTR_TRY(up_vec(dev, lut.data(), 768, "pixel lut", &v->lut));
+    HTR_TRY(feed.patch(d, pp, &v->patch_embd));
+    HTR_TRY(feed.vec(-1, "v.pre_ln", d, &v->pre_ln));
+    HTR_TRY(feed.vec(-1, "mm.input_norm", d, &v->input_norm));
+    HTR_TRY(feed.w16(-1, "mm.patch_merger", d, 4 * d, 1.0f, &v->merger));
+    HTR_TRY(feed.w16(-1, "mm.1", c.proj_dim, d, 1.0f, &v->mm1));
+    HTR_TRY(feed.w16(-1, "mm.2", c.proj_dim, c.proj_dim, 1.0f, &v->mm2));
+    for (htr_weight *w : {v->merger, v->mm1, v->mm2}) HTR_TRY(widen_w16(dev, w));
+    return split_patch_embd(v, pp);
+}
+
+int finish(htr_vision *v, int rc, htr_vision **out) {
     if (rc < 0) {
         std::string keep = htr_last_error();
         htr_vision_free(v);
         return htr_fail("%s", keep.c_str());
     }
     *out = v;
+    return 0;
+}
+
+// VisionConfig::from_gguf (vision.rs:55-84)
+int vision_config_from_gguf(htr_gguf *g, htr_vision_config *out) {
+    htr_vision_config c{};
+    std::string proj;
+    HTR_TRY(gguf_meta_str(g, "clip.projector_type", &proj));
+    if (proj != "lightonocr") return htr_fail("projector \"%s\": this engine runs lightonocr only", proj.c_str());
+    bool silu = false;
+    HTR_TRY(gguf_meta_bool(g, "clip.use_silu", &silu));
+    if (!silu) return htr_fail("clip.use_silu is false: the encoder's FFN would not be SwiGLU");
+    uint32_t u[8];
+    const char *keys[8] = {"clip.vision.embedding_length", "clip.vision.attention.head_count",
+                           "clip.vision.block_count",      "clip.vision.feed_forward_length",
+                           "clip.vision.patch_size",       "clip.vision.spatial_merge_size",
+                           "clip.vision.image_size",       "clip.vision.projection_dim"};
+    for (int k = 0; k < 2; k++) HTR_TRY(gguf_meta_u32(g, keys[k], &u[k]));
+    if (u[1] == 0 || u[0] % u[1] != 0 || u[0] / u[1] != 64)
+        return htr_fail("head dim %u/%u: the attention kernel is written for 64", u[0], u[1]);
+    for (int k = 2; k < 8; k++) HTR_TRY(gguf_meta_u32(g, keys[k], &u[k]));
+    for (int k = 0; k < 8; k++)
+        if (u[k] > (1u << 24)) return htr_fail("%s = %u is not a vision encoder's size", keys[k], u[k]);
+    c.dim = (int)u[0];
+    c.n_head = (int)u[1];
+    c.d_head = c.dim / c.n_head;
+    c.n_layer = (int)u[2];
+    c.n_ff = (int)u[3];
+    c.patch = (int)u[4];
+    c.merge = (int)u[5];
+    c.image_size = (int)u[6];
+    c.proj_dim = (int)u[7];
+    HTR_TRY(gguf_meta_f32(g, "clip.vision.attention.layer_norm_epsilon", &c.eps));
+    c.rope_theta = 10000.0f;  // vision.rs:28-29: clip.cpp's LIGHTONOCR constant; the GGUF has no key for it
+    std::vector<float> three;
+    for (int k = 0; k < 2; k++) {
+        const char *key = k ? "clip.vision.image_std" : "clip.vision.image_mean";
+        HTR_TRY(gguf_meta_f32_array(g, key, &three));
+        if (three.size() != 3) return htr_fail("%s has %zu values", key, three.size());
+        for (int ch = 0; ch < 3; ch++) (k ? c.std : c.mean)[ch] = three[ch];
+    }
+    *out = c;
+    return 0;
+}
+
+}  // namespace
+
+// Vision::from_gguf (vision.rs:177-233) from host tensors
+extern "C" int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, const float *patch_embd,
+                                 const float *pre_ln, const htr_vision_layer *layers, const float *input_norm,
+                                 const void *merger, const void *mm1, const void *mm2, htr_vision **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!cfg || !layers || !out) return htr_fail("htr_vision_create: null argument");
+    HTR_TRY(check_vision_cfg(*cfg));
+    ArrayVisionFeed feed;
+    feed.dev = dev;
+    feed.layers = layers;
+    feed.patch_embd = patch_embd;
+    feed.pre_ln = pre_ln;
+    feed.input_norm = input_norm;
+    feed.merger = merger;
+    feed.mm1 = mm1;
+    feed.mm2 = mm2;
+    auto *v = new htr_vision;
+    return finish(v, build_vision(dev, *cfg, feed, v), out);
+}
+
+// Vision::from_gguf (vision.rs:177-233) from an mmproj GGUF: BF16 weights converted to f16 on the device as they
+// arrive (the down projection × 64), a load refused when any value lies beyond f16's range (vision.rs:224-232)
+extern "C" int htr_vision_load_gguf(htr_device *dev, htr_gguf *g, htr_vision **out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!g || !out) return htr_fail("htr_vision_load_gguf: null argument");
+    htr_vision_config c{};
+    HTR_TRY(vision_config_from_gguf(g, &c));
+    HTR_TRY(check_vision_cfg(c));
+    // vision.rs:209-214: tensors the graph would use if present (checked before any weight is streamed)
+    for (const char *absent : {"v.patch_embd.bias", "v.post_ln.weight", "mm.1.bias", "mm.2.bias",
+                               "v.token_embd.img_break", "mm.input_norm.bias"})
+        if (gguf_has(g, absent)) return htr_fail("%s is in the GGUF but not part of this engine's graph", absent);
+    GgufVisionFeed feed(g);
+    HTR_TRY(feed.sg.init(dev));
+    HTR_TRY(htr_dev_alloc(dev, 4, HTR_MEM_WORK, (void **)&feed.over));
+    auto *v = new htr_vision;
+    int rc = build_vision(dev, c, feed, v);
+    unsigned n_over = 0;
+    if (rc == 0) rc = htr_hip(dev, hipMemcpyAsync(&n_over, feed.over, 4, hipMemcpyDeviceToHost, dev->stream),
+                              "read the f16 range count");
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc == 0 && n_over > 0)
+        rc = htr_fail("%u words of vision weights hold values beyond f16's range (65504): this model cannot run on the "
+                      "f16 compute path", n_over);
+    return finish(v, rc, out);
+}
+
+extern "C" int htr_vision_get_config(htr_vision *v, htr_vision_config *out) {
+    if (!v || !out) return htr_fail("htr_vision_get_config: null argument");
+    *out = v->cfg;
     return 0;
 }
 

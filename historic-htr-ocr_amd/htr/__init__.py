@@ -29,7 +29,7 @@ SYMBOLS = [
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_causal_attention", "htr_choose",
     "htr_choose_many", "htr_matmul_q8_0", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
-    "htr_vision_out_shape", "htr_vision_encode", "htr_gguf_open", "htr_gguf_open_source", "htr_gguf_close",
+    "htr_vision_get_config", "htr_vision_load_gguf", "htr_vision_out_shape", "htr_vision_encode", "htr_gguf_open", "htr_gguf_open_source", "htr_gguf_close",
     "htr_gguf_header", "htr_gguf_tensor", "htr_gguf_u32", "htr_gguf_f32", "htr_gguf_str", "htr_gguf_f32_array",
     "htr_gguf_read_small", "htr_text_model_create", "htr_text_model_free", "htr_text_model_load_gguf",
     "htr_text_model_config", "htr_session_create", "htr_session_free",
@@ -136,6 +136,8 @@ def lib() -> C.CDLL:
             "htr_vision_create": (i32, [vp, C.POINTER(VisionConfigC), vp, vp, C.POINTER(VisionLayerC), vp, vp, vp, vp,
                                         pp]),
             "htr_vision_free": (i32, [vp]),
+            "htr_vision_get_config": (i32, [vp, C.POINTER(VisionConfigC)]),
+            "htr_vision_load_gguf": (i32, [vp, vp, pp]),
             "htr_vision_out_shape": (i32, [vp, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)]),
             "htr_vision_encode": (i32, [vp, vp, i32, i32, i32, vp]),
             "htr_gguf_open": (i32, [C.c_char_p, pp]),
@@ -685,7 +687,21 @@ class Choice:
 class Vision:
     """Vision::from_gguf (vision.rs:177-233) from host tensors. ``cfg``: n_layer, dim, n_head, n_ff, patch,
     image_size, proj_dim, eps, rope_theta, mean, std; ``t``: patch_embd (f32), pre_ln, input_norm (f32), merger, mm1,
-    mm2 (q8_0 blocks) and ``layers`` (dicts with ln1, ln2 f32 and q, k, v, o, gate, up, down q8_0 blocks)."""
+    mm2 (q8_0 blocks) and ``layers`` (dicts with ln1, ln2 f32 and q, k, v, o, gate, up, down q8_0 blocks).
+    ``Vision.from_gguf`` loads one from an mmproj GGUF (BF16 / F32 weights) instead."""
+
+    @classmethod
+    def from_gguf(cls, dev: Device, g: Gguf) -> "Vision":
+        self = cls.__new__(cls)
+        h = C.c_void_p()
+        _check(lib().htr_vision_load_gguf(dev.h, g.h, C.byref(h)))
+        self.dev, self.h = dev, h.value
+        c = VisionConfigC()
+        _check(lib().htr_vision_get_config(self.h, C.byref(c)))
+        self.cfg = dict(n_layer=c.n_layer, dim=c.dim, n_head=c.n_head, n_ff=c.n_ff, patch=c.patch, merge=c.merge,
+                        image_size=c.image_size, proj_dim=c.proj_dim, eps=c.eps, rope_theta=c.rope_theta,
+                        mean=list(c.mean), std=list(c.std))
+        return self
 
     def __init__(self, dev: Device, cfg: dict, t: dict):
         self.dev, self.cfg = dev, cfg

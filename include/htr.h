@@ -173,6 +173,8 @@ int htr_vision_create(htr_device *dev, const htr_vision_config *cfg, const float
                       const htr_vision_layer *layers, const float *input_norm, const void *merger, const void *mm1,
                       const void *mm2, htr_vision **out);
 int htr_vision_free(htr_vision *v);
+/* the configuration of an encoder (Vision::cfg, vision.rs:91) */
+int htr_vision_get_config(htr_vision *v, htr_vision_config *out);
 /* the output of an encode of a width × height page (Vision::grid, vision.rs:236-244: both sides on the patch·merge
  * grid, the longer ≤ image_size): n_layers < 0 → [n/4][proj_dim] embeddings; n_layers ≥ 0 → the residual after that
  * many layers [n][dim] (the reference's `layers` bisect hook, vision.rs:246-256) */
@@ -236,6 +238,15 @@ int htr_text_model_free(htr_text_model *m);
 int htr_text_model_load_gguf(htr_device *dev, htr_gguf *g, htr_text_model **out);
 /* the configuration a model was built with */
 int htr_text_model_config(htr_text_model *m, htr_text_config *out);
+/* Vision::load / Vision::from_gguf (vision.rs:177-233) from an mmproj GGUF: the configuration from the clip.* keys
+ * (VisionConfig::from_gguf, vision.rs:55-84: projector "lightonocr", SwiGLU, head dim 64, rope θ 10000), the encoder
+ * tensors v.blk.{i}.{ln1,ln2,attn_q,attn_k,attn_v,attn_out,ffn_gate,ffn_up,ffn_down}.weight, v.patch_embd.weight,
+ * v.pre_ln.weight, mm.input_norm.weight, mm.patch_merger.weight, mm.1.weight, mm.2.weight streamed onto the device;
+ * BF16 weights converted to f16 there (f16_from_bf16.wgsl; ffn_down × 64), F32 weights taken as they are (the
+ * projections rounded to f16), F32 norms. Refused: another projector, a tensor the graph would read if present
+ * (v.patch_embd.bias, v.post_ln.weight, mm.1.bias, mm.2.bias, v.token_embd.img_break, mm.input_norm.bias), a
+ * weight of another type or shape, and values beyond f16's range (65504, after the scale) */
+int htr_vision_load_gguf(htr_device *dev, htr_gguf *g, htr_vision **out);
 
 /* TextModel::session (text.rs:378-434): n_ctx positions (prompt + new tokens); the KV cache is sized once to n_ctx */
 int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out);

@@ -86,3 +86,57 @@ def text_model_gguf(cfg: dict, tok_embd, output_norm, layers, extra_kvs=(), extr
     ts.append(("output_norm.weight", GGML_F32, [d], f32(output_norm)))
     ts = [t for t in ts if t[0] not in skip] + list(extra_tensors)
     return gguf_bytes(kvs, ts)
+
+
+def bf16_bits(a) -> np.ndarray:
+    """float32 values → bf16 bit patterns (round to nearest even)"""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_value(b) -> np.ndarray:
+    """bf16 bit patterns → their float32 values (exact)"""
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def vision_model_gguf(cfg: dict, t: dict, kvs_over=None, extra_tensors=(), skip=()) -> bytes:
+    """an mmproj GGUF of a LightOnOCR-shaped encoder with the clip.* keys VisionConfig::from_gguf reads
+    (vision.rs:55-84). ``t`` as the host-array encoder takes it, but each weight a uint16 array (BF16 bits) or a
+    float32 array (F32), [rows][cols]; norms float32. The patch embedding is written [p, p, 3, dim] as an mmproj holds
+    it. ``kvs_over``: {key: (type, value)} replacing or adding keys (value None drops the key)"""
+    d, f, pd, p = cfg["dim"], cfg["n_ff"], cfg["proj_dim"], cfg["patch"]
+    kvs = {"general.architecture": (STR, "clip"), "clip.projector_type": (STR, "lightonocr"),
+           "clip.use_silu": (BOOL, 1), "clip.vision.embedding_length": (U32, d),
+           "clip.vision.attention.head_count": (U32, cfg["n_head"]), "clip.vision.block_count": (U32, cfg["n_layer"]),
+           "clip.vision.feed_forward_length": (U32, f), "clip.vision.patch_size": (U32, p),
+           "clip.vision.spatial_merge_size": (U32, 2), "clip.vision.image_size": (U32, cfg.get("image_size", 1540)),
+           "clip.vision.projection_dim": (U32, pd),
+           "clip.vision.attention.layer_norm_epsilon": (F32, cfg["eps"]),
+           "clip.vision.image_mean": (ARR, (F32, list(cfg["mean"]))),
+           "clip.vision.image_std": (ARR, (F32, list(cfg["std"])))}
+    for k, v in (kvs_over or {}).items():
+        if v is None:
+            kvs.pop(k, None)
+        else:
+            kvs[k] = v
+
+    def w(name, a, dims):
+        a = np.ascontiguousarray(a)
+        ty = GGML_BF16 if a.dtype == np.uint16 else GGML_F32
+        assert a.dtype in (np.uint16, np.float32) and a.size == int(np.prod(dims)), name
+        return (name, ty, dims, a.tobytes())
+
+    vec = lambda name, a: (name, GGML_F32, [a.size], np.ascontiguousarray(a, np.float32).tobytes())
+    ts = []
+    for i, ly in enumerate(t["layers"]):
+        b = f"v.blk.{i}."
+        ts += [vec(b + "ln1.weight", ly["ln1"]), vec(b + "ln2.weight", ly["ln2"]),
+               w(b + "attn_q.weight", ly["q"], [d, d]), w(b + "attn_k.weight", ly["k"], [d, d]),
+               w(b + "attn_v.weight", ly["v"], [d, d]), w(b + "attn_out.weight", ly["o"], [d, d]),
+               w(b + "ffn_gate.weight", ly["gate"], [d, f]), w(b + "ffn_up.weight", ly["up"], [d, f]),
+               w(b + "ffn_down.weight", ly["down"], [f, d])]
+    ts += [w("v.patch_embd.weight", t["patch_embd"], [p, p, 3, d]), vec("v.pre_ln.weight", t["pre_ln"]),
+           vec("mm.input_norm.weight", t["input_norm"]), w("mm.patch_merger.weight", t["merger"], [4 * d, d]),
+           w("mm.1.weight", t["mm1"], [d, pd]), w("mm.2.weight", t["mm2"], [pd, pd])]
+    ts = [x for x in ts if x[0] not in skip] + list(extra_tensors)
+    return gguf_bytes([(k, ty, v) for k, (ty, v) in kvs.items()], ts)

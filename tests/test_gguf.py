@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import htr
-from gguf_writer import ARR, F32, GGML_BF16, GGML_Q8_0, STR, U32, gguf_bytes, text_model_gguf
+from gguf_writer import (ARR, F32, GGML_BF16, GGML_F32, GGML_Q8_0, STR, U32, bf16_bits, bf16_value, gguf_bytes,
+                         text_model_gguf, vision_model_gguf)
 from helpers import tiny_text_model
 
 
@@ -147,6 +148,42 @@ def test_text_model_file_metadata():
         assert g.info("token_embd.weight")["shape"] == [256, 1000]
         assert g.header()["n_tensors"] == 2 + 5 * 11
         assert g.read_small("blk.0.attn_norm.weight").view(np.float32).tolist() == layers[0]["attn_norm"].tolist()
+
+
+def test_bf16_bits_round_to_nearest_even():
+    """the writer's f32 → bf16 (the mmproj tensors of the tests): ties to even, the exact values kept, 65504 (no
+    bf16) to 65536, subnormals kept; bf16_value is exact"""
+    a = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 1 + 2 ** -7, -3.0, 65504.0, 2.0 ** -130], np.float32)
+    b = bf16_bits(a)
+    assert b.tolist() == [0x3F80, 0x3F80, 0x3F82, 0x3F81, 0xC040, 0x4780, 0x0008]
+    assert bf16_value(b).tolist() == [1.0, 1.0, 1 + 2 ** -6, 1 + 2 ** -7, -3.0, 65536.0, 2.0 ** -130]
+
+
+def test_vision_model_file_metadata():
+    """an mmproj GGUF of the tiny encoder: the clip.* keys VisionConfig::from_gguf reads and the tensor table (BF16
+    weights [cols, rows], the patch embedding [p, p, 3, dim], F32 norms)"""
+    from test_vision_oracle import tiny_vision_cfg
+
+    cfg = tiny_vision_cfg()
+    d, f, pp = cfg["dim"], cfg["n_ff"], 3 * cfg["patch"] ** 2
+    r = np.random.default_rng(0)
+    w = lambda rows, cols: bf16_bits(r.normal(0, 0.05, (rows, cols)))
+    nv = lambda n: np.ones(n, np.float32)
+    layers = [dict(ln1=nv(d), ln2=nv(d), q=w(d, d), k=w(d, d), v=w(d, d), o=w(d, d), gate=w(f, d), up=w(f, d),
+                   down=w(d, f)) for _ in range(cfg["n_layer"])]
+    t = dict(patch_embd=w(d, pp), pre_ln=nv(d), layers=layers, input_norm=nv(d), merger=w(d, 4 * d),
+             mm1=w(cfg["proj_dim"], d), mm2=w(cfg["proj_dim"], cfg["proj_dim"]))
+    with htr.Gguf(data=vision_model_gguf(cfg, t)) as g:
+        assert g.str("clip.projector_type") == "lightonocr"
+        assert g.u32("clip.vision.embedding_length") == d and g.u32("clip.vision.block_count") == 2
+        assert np.array_equal(np.float32(g.f32_array("clip.vision.image_std")), np.float32(cfg["std"]))
+        ti = g.info("v.blk.1.ffn_down.weight")
+        assert (ti["shape"], ti["type"], ti["n_bytes"]) == ([f, d], GGML_BF16, 2 * d * f)
+        assert g.info("v.patch_embd.weight")["shape"] == [14, 14, 3, d]
+        assert g.info("mm.patch_merger.weight")["shape"] == [4 * d, d]
+        assert g.info("v.pre_ln.weight")["type"] == GGML_F32
+        assert g.header()["n_tensors"] == 2 * 9 + 6
+        assert np.array_equal(g.read_small("v.blk.0.attn_q.weight").view(np.uint16), layers[0]["q"].ravel())
 
 
 def test_read_small_refuses_large_tensors():
