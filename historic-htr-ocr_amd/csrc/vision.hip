@@ -151,15 +151,19 @@ __global__ __launch_bounds__(VW) void k_heads_f16(const float *K, const float *V
 // attention_coop.wgsl's arithmetic on the f16 MFMAs: O[t][h] = softmax(q16·K16ᵀ)·V16 with q16 = f16(q·scale), keys in
 // blocks of 32 with the running max (start −3e38), P = f16(e^(S − max)), l = l·corr + Σ P, O = O·corr + P·V (f32
 // accumulation in the matrix unit, as the reference's cooperative matrices accumulate); O / l → f16.
-// A wave takes 32 queries of one head. Per key block, Sᵀ (32 keys × 32 queries) = K·q16ᵀ is 4 MFMAs 32x32x16: lane
-// ℓ = 32h + c then holds query c's scores of keys 8(i / 4) + 4h + i % 4 (i < 16), the other 16 in lane ℓ ^ 32. Oᵀ
-// (64 dims × 32 queries) += Vᵀ·Pᵀ is 4 more, lane ℓ accumulating dims 32t + 8(i / 4) + 4h + i % 4 of query c, so the
-// rescale by the query's corr stays in the lane.
-// The 4 waves of a workgroup (128 queries) share the key blocks: stages of AST blocks are copied from memory to LDS
+// A wave takes QG groups of 32 queries of one head. Per key block and group, Sᵀ (32 keys × 32 queries) = K·q16ᵀ is 4
+// MFMAs 32x32x16: lane ℓ = 32h + c then holds query c's scores of keys 8(i / 4) + 4h + i % 4 (i < 16), the other 16
+// in lane ℓ ^ 32. Oᵀ (64 dims × 32 queries) += Vᵀ·Pᵀ is 4 more, lane ℓ accumulating dims 32t + 8(i / 4) + 4h + i % 4
+// of query c, so the rescale by the query's corr stays in the lane.
+// The 4 waves of a workgroup (128·QG queries) share the key blocks: stages of AST blocks are copied from memory to LDS
 // (coalesced 16-byte loads, the next stage's in flight while the current one is in use) and each wave reads its
-// fragments from there. grid: ⌈n / 128⌉ · H workgroups, numbered so that the workgroups of one head run on one XCD.
+// fragments from there. grid: ⌈n / (128·QG)⌉ · H workgroups, numbered so that the workgroups of one head run on one
+// XCD.
 constexpr int FQ = 32, FB = 32, FWAVES = VW / 64, AST = 2;
 
+// QG groups of 32 queries a wave: the groups share every K / V fragment read from LDS and give the wave QG
+// independent chains (Sᵀ MFMAs → max → exp → P·V) to interleave
+template <int QG>
 __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float16 *KV, _Float16 *O, int n_tok,
                                                     int n_head, int n_blk, int n_qt, float scale, const float *cs,
                                                     int px, int max_pos) {
@@ -175,17 +179,20 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         h = blockIdx.x / n_qt;
         qt = blockIdx.x % n_qt;
     }
-    const int row = n_head * 64, q0 = (qt * FWAVES + wave) * FQ;
-    const int qi = min(q0 + c, n_tok - 1);
-    half8 qf[4];  // B operand of step ks: q16[query c][dims 16ks + 8h … + 7], q turned by rope2d first
+    const int row = n_head * 64, q0 = (qt * FWAVES + wave) * FQ * QG;
+    half8 qf[QG][4];  // B operand of step ks: q16[query c][dims 16ks + 8h … + 7], q turned by rope2d first
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-        const float4 *src = reinterpret_cast<const float4 *>(Q + (size_t)qi * row + h * 64 + 16 * ks + 8 * hf);
-        const float4 x0 = src[0], x1 = src[1];
-        float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        rope8(x, cs, qi, px, max_pos, 16 * ks + 8 * hf);
+    for (int g = 0; g < QG; g++) {
+        const int qi = min(q0 + FQ * g + c, n_tok - 1);
 #pragma unroll
-        for (int e = 0; e < 8; e++) qf[ks][e] = (_Float16)(x[e] * scale);
+        for (int ks = 0; ks < 4; ks++) {
+            const float4 *src = reinterpret_cast<const float4 *>(Q + (size_t)qi * row + h * 64 + 16 * ks + 8 * hf);
+            const float4 x0 = src[0], x1 = src[1];
+            float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            rope8(x, cs, qi, px, max_pos, 16 * ks + 8 * hf);
+#pragma unroll
+            for (int e = 0; e < 8; e++) qf[g][ks][e] = (_Float16)(x[e] * scale);
+        }
     }
     // the lane's fragment chunks within a block: K step ks (key c, dims 16ks + 8h …), Vᵀ tile t step st (dim 32t + c,
     // slots 16st + 8h …)
@@ -210,12 +217,17 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
 #pragma unroll
         for (int i = 0; i < 2 * AST; i++) s_kv[buf][(i / 2) * (KVB / 16) + (i % 2) * VW + tid] = stg[i];
     };
-    f32x16 o[2];
+    f32x16 o[QG][2];
+    float m[QG], l[QG];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int g = 0; g < QG; g++) {
+        m[g] = -3.0e38f;
+        l[g] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[t][i] = 0.0f;
-    float m = -3.0e38f, l = 0.0f;
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[g][t][i] = 0.0f;
+    }
     // one key block at k0 from LDS; MASK: the block holds keys ≥ n_tok (the last one only), which take no part in
     // the max and get p = 0. A rescale by corr = 1 is skipped (x·1 = x).
     auto block = [&](const half8 *sb, int k0, auto mask) {
@@ -225,46 +237,54 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
         for (int ks = 0; ks < 4; ks++) fk[ks] = sb[kc[ks]];
 #pragma unroll
         for (int i = 0; i < 4; i++) fv[i] = sb[vc[i]];
-        f32x16 s;
+        f32x16 s[QG];
 #pragma unroll
-        for (int i = 0; i < 16; i++) s[i] = 0.0f;
+        for (int g = 0; g < QG; g++) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(fk[ks], qf[ks], s, 0, 0, 0);
-        float mx = m;
+            for (int i = 0; i < 16; i++) s[g][i] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            if (!MASK || k0 + 8 * (i >> 2) + 4 * hf + (i & 3) < n_tok) mx = fmaxf(mx, s[i]);
-        mx = pair_max<32>(mx);
-        // e^(s − mx) = 2^(s·log2 e − mx·log2 e): one fma and v_exp_f32 a score; P rounded to f16 in pairs
-        // (v_cvt_pk_f16_f32, round to nearest even) and summed as f32 by v_dot2 against (1, 1)
-        constexpr float LOG2E = 1.4426950408889634f;
-        const float corr = __builtin_amdgcn_exp2f((m - mx) * LOG2E), nml = -mx * LOG2E;
-        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
-#pragma unroll
-            for (int t = 0; t < 2; t++) o[t] *= corr;
+            for (int ks = 0; ks < 4; ks++) s[g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fk[ks], qf[g][ks], s[g], 0, 0, 0);
         }
-        half8 pb[2];
-        float ps = 0.0f;
+        half8 pb[QG][2];
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            float2_t e = {__builtin_amdgcn_exp2f(fmaf(s[i], LOG2E, nml)),
-                          __builtin_amdgcn_exp2f(fmaf(s[i + 1], LOG2E, nml))};
-            if (MASK) {
-                if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) >= n_tok) e[0] = 0.0f;
-                if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) + 1 >= n_tok) e[1] = 0.0f;
+        for (int g = 0; g < QG; g++) {
+            float mx = m[g];
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (!MASK || k0 + 8 * (i >> 2) + 4 * hf + (i & 3) < n_tok) mx = fmaxf(mx, s[g][i]);
+            mx = pair_max<32>(mx);
+            // e^(s − mx) = 2^(s·log2 e − mx·log2 e): one fma and v_exp_f32 a score; P rounded to f16 in pairs
+            // (v_cvt_pk_f16_f32, round to nearest even) and summed as f32 by v_dot2 against (1, 1)
+            constexpr float LOG2E = 1.4426950408889634f;
+            const float corr = __builtin_amdgcn_exp2f((m[g] - mx) * LOG2E), nml = -mx * LOG2E;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) o[g][t] *= corr;
             }
-            const half2_t p2 = __builtin_convertvector(e, half2_t);
-            pb[i >> 3][i & 7] = p2[0];
-            pb[i >> 3][(i & 7) + 1] = p2[1];
-            ps = __builtin_amdgcn_fdot2(p2, half2_t{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                float2_t e = {__builtin_amdgcn_exp2f(fmaf(s[g][i], LOG2E, nml)),
+                              __builtin_amdgcn_exp2f(fmaf(s[g][i + 1], LOG2E, nml))};
+                if (MASK) {
+                    if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) >= n_tok) e[0] = 0.0f;
+                    if (k0 + 8 * (i >> 2) + 4 * hf + (i & 3) + 1 >= n_tok) e[1] = 0.0f;
+                }
+                const half2_t p2 = __builtin_convertvector(e, half2_t);
+                pb[g][i >> 3][i & 7] = p2[0];
+                pb[g][i >> 3][(i & 7) + 1] = p2[1];
+                ps = __builtin_amdgcn_fdot2(p2, half2_t{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
+            }
+            l[g] = l[g] * corr + pair_sum<32>(ps);
+            m[g] = mx;
         }
-        l = l * corr + pair_sum<32>(ps);
-        m = mx;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int g = 0; g < QG; g++)
 #pragma unroll
-            for (int st = 0; st < 2; st++)
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fv[2 * t + st], pb[st], o[t], 0, 0, 0);
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int st = 0; st < 2; st++)
+                    o[g][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fv[2 * t + st], pb[g][st], o[g][t], 0, 0, 0);
     };
     // stages 0 … n_full − 1 hold full blocks only: the loop body has one path, so O stays in the same registers
     // through every iteration (a masked path inside the loop makes the compiler copy it each block)
@@ -293,17 +313,20 @@ __global__ __launch_bounds__(VW) void k_attn_vision(const float *Q, const _Float
                 block(s_kv[buf] + j * (KVB / 16), k0, std::true_type{});
         }
     }
-    if (q0 + c < n_tok) {
-        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-        const float inv = 1.0f / l;
-        _Float16 *dst = O + (size_t)(q0 + c) * row + h * 64 + 4 * hf;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+    for (int g = 0; g < QG; g++) {
+        if (q0 + FQ * g + c < n_tok) {
+            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            const float inv = 1.0f / l[g];
+            _Float16 *dst = O + (size_t)(q0 + FQ * g + c) * row + h * 64 + 4 * hf;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                *reinterpret_cast<half4 *>(dst + 32 * t + 8 * r) =
-                    half4{(_Float16)(o[t][4 * r] * inv), (_Float16)(o[t][4 * r + 1] * inv),
-                          (_Float16)(o[t][4 * r + 2] * inv), (_Float16)(o[t][4 * r + 3] * inv)};
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    *reinterpret_cast<half4 *>(dst + 32 * t + 8 * r) =
+                        half4{(_Float16)(o[g][t][4 * r] * inv), (_Float16)(o[g][t][4 * r + 1] * inv),
+                              (_Float16)(o[g][t][4 * r + 2] * inv), (_Float16)(o[g][t][4 * r + 3] * inv)};
+        }
     }
 }
 
@@ -383,9 +406,12 @@ int launch_attn_vision(htr_device *dev, hipStream_t st, const float *q, const _F
     if (n_tok < 1) return htr_fail("vision attention: %d tokens", n_tok);
     if (px < 1 || (n_tok + px - 1) / px > max_pos || px > max_pos)
         return htr_fail("vision attention: %d tokens on %d columns, rope table of %d positions", n_tok, px, max_pos);
-    const int n_qt = (n_tok + FQ * FWAVES - 1) / (FQ * FWAVES), n_blk = (n_tok + FB - 1) / FB;
-    hipLaunchKernelGGL(k_attn_vision, dim3(n_qt * n_head), dim3(VW), 0, st, q, kv, o, n_tok, n_head, n_blk, n_qt, scale,
-                       cs, px, max_pos);
+    // two query groups a wave: 0.69 ms a layer at 12100 patches against 0.79 ms with one (223 VGPRs, 2 waves a SIMD;
+    // forcing 3 spills 111 of them)
+    constexpr int QG = 2;
+    const int n_qt = (n_tok + QG * FQ * FWAVES - 1) / (QG * FQ * FWAVES), n_blk = (n_tok + FB - 1) / FB;
+    hipLaunchKernelGGL(k_attn_vision<QG>, dim3(n_qt * n_head), dim3(VW), 0, st, q, kv, o, n_tok, n_head, n_blk, n_qt,
+                       scale, cs, px, max_pos);
     return htr_launched(dev, "k_attn_vision");
 }
 
