@@ -334,8 +334,47 @@ def load_traffic():
     return t.get("hbm_bytes_per_launch")
 
 
+def _timed(fn, budget_s, min_n=3):
+    """(calls, seconds) of fn() repeated until budget_s has passed (at least min_n calls)"""
+    n, t0 = 0, time.perf_counter()
+    while n < min_n or time.perf_counter() - t0 < budget_s:
+        fn()
+        n += 1
+    return n, time.perf_counter() - t0
+
+
+def cpu_configs(orc, threads, budget_s=2.0):
+    """the oracle on the host cores for the other single-kernel workloads: the q8_0 matvec W [3072 x 1024], the
+    penalised greedy choice over 151,936 logits (window 64, rp 1.1), the decode attention (16 / 8 heads x 128) at 512 /
+    2048 / 8192 keys"""
+    r = np.random.default_rng(0)
+    w = orc.q8_0_quantize(r.normal(0, 1, 3072 * 1024).astype(np.float32))[0]
+    x = r.normal(0, 1, 1024).astype(np.float32)
+    n, dt = _timed(lambda: orc.matvec_q8_0(w, 3072, 1024, x), budget_s)
+    res = {"matvec_w3072x1024": {"us": dt / n * 1e6, "GBs": MATVEC_UNIT_BYTES / (dt / n) / 1e9, "calls": n}}
+    rows = [r.normal(0, 3, 151936).astype(np.float32) for _ in range(4)]
+    hist = [int(t) for t in r.integers(0, 151936, 64)]
+    spent, n = 0.0, 0
+    while n < 3 or spent < budget_s:
+        lo = rows[n % 4].copy()  # choose penalises in place: a fresh row each step, copied outside the timing
+        t0 = time.perf_counter()
+        orc.choose(lo, 1.1, 64, 0.0, hist)
+        spent += time.perf_counter() - t0
+        n += 1
+    res["choose_151936"] = {"us": spent / n * 1e6, "calls": n}
+    q = r.normal(0, 1, 16 * 128).astype(np.float32)
+    sc = float(np.float32(1 / np.sqrt(128)))
+    for L in (512, 2048, 8192):
+        kv = r.normal(0, 1, (2, L, 8, 128)).astype(np.float16).view(np.uint16)  # the oracle's [key][kv head][128]
+        n, dt = _timed(lambda: orc.attn_decode(q, kv[0], kv[1], 8 * 128, L, 16, 8, sc), budget_s / 3)
+        res[f"attention_{L}"] = {"us": dt / n * 1e6, "GBs": (4096 * L + 16384) / (dt / n) / 1e9, "calls": n}
+    res["threads"] = threads
+    return res
+
+
 def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
-    """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores"""
+    """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores; the other
+    single-kernel workloads timed the same way under per_config"""
     # the oracle (test infrastructure): imported here, for the CPU baseline leg only
     import importlib.util
 
@@ -357,7 +396,10 @@ def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
         n += 1
     dt = time.perf_counter() - t0
     log(f"cpu baseline: {n} tokens in {dt:.1f} s on {threads} threads")
-    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+    per = cpu_configs(orc, threads)
+    log(f"cpu baseline: matvec {per['matvec_w3072x1024']['GBs']:.1f} GB/s, choose {per['choose_151936']['us']:.0f} us, "
+        f"attention 8192 keys {per['attention_8192']['us']:.0f} us")
+    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port", "per_config": per,
             "sample": f"oracle (C restatement, OpenMP) greedy decode of {n} tokens (rp 1.1 / 64) of the same 28-layer q8_0 "
                       f"model after a {prompt_n}-token prompt: attention context {prompt_n}-{prompt_n + n} keys, shorter "
                       f"than the workload's 1024-1536 (the 633 MB of weights per token dominate either way)"}
