@@ -178,3 +178,42 @@ def test_mmproj_refuses_values_beyond_f16(dev):
     g = htr.Gguf(data=vision_model_gguf(cfg, t))
     htr.Vision.from_gguf(dev, g).free()
     g.close()
+
+
+def test_mmproj_at_the_page_encoder_shape(dev, tmp_path):
+    """an mmproj of the page encoder's shape (24 layers, hidden 1024, SwiGLU 4096, projector 1024; 810 MB of BF16,
+    every layer holding the first one's weights) streamed from a file: its load time, the residual after the patch
+    embedding of a 1540 × 1540 page against the oracle (1e-5), and the whole encode finite at 3025 × 1024. The layers'
+    conversion is pinned by the tiny mmproj tests above (the oracle takes about 40 s for one layer of this page)"""
+    import time
+
+    from htr import synth
+
+    cfg, t = synth.vision_model(n_layer=1)
+    d, f, pd = cfg["dim"], cfg["n_ff"], cfg["proj_dim"]
+    deq = lambda b, rows, cols: bf16_bits(orc.q8_0_dequant(b, rows * cols).reshape(rows, cols))
+    shapes = dict(q=(d, d), k=(d, d), v=(d, d), o=(d, d), gate=(f, d), up=(f, d), down=(d, f))
+    ly = dict(ln1=t["layers"][0]["ln1"], ln2=t["layers"][0]["ln2"],
+              **{k: deq(t["layers"][0][k], *rc) for k, rc in shapes.items()})
+    tb = dict(patch_embd=bf16_bits(t["patch_embd"]), pre_ln=t["pre_ln"], input_norm=t["input_norm"], layers=[ly] * 24,
+              merger=deq(t["merger"], d, 4 * d), mm1=deq(t["mm1"], pd, d), mm2=deq(t["mm2"], pd, pd))
+    path = tmp_path / "mmproj-page.gguf"
+    path.write_bytes(vision_model_gguf(dict(cfg, n_layer=24), tb))
+    g = htr.Gguf(str(path))
+    t0 = time.perf_counter()
+    v = htr.Vision.from_gguf(dev, g)
+    dt = time.perf_counter() - t0
+    g.close()
+    size = path.stat().st_size
+    print(f"\n[mmproj page shape] {size / 1e6:.0f} MB loaded in {dt * 1e3:.0f} ms ({size / dt / 1e9:.1f} GB/s)")
+    try:
+        assert v.cfg["n_layer"] == 24
+        rgb = synth.page(99, 1540, 1540)
+        t16 = oracle_planes(dict(tb, layers=[ly]))
+        e = rel_l2(v.encode(rgb, 0), orc.vision_encode(cfg, t16, rgb, 0, w16=True))
+        print(f"[mmproj page shape 1540x1540 layers 0] rel-L2 vs oracle {e:.2e}")
+        assert e < 1e-5
+        out = v.encode(rgb)
+        assert out.shape == (3025, 1024) and np.all(np.isfinite(out))
+    finally:
+        v.free()
