@@ -9,8 +9,9 @@
 //   - first maximum wins (ties → lowest index); NaN never wins; a NaN at index 0 (after the penalty) → token 0, as the
 //     CPU loop `if l > logits[best]` starting at best = 0 decides; every logit NaN → 0.
 //
-// Schedule: grid (groups, rows); a workgroup owns 1024 consecutive logits of one row, stages them in LDS, applies the
-// penalties of the window ids that fall in its range, and reduces (value, index) to its best. The row's best of all
+// Schedule: grid (groups, rows); a workgroup owns SPAN = 4096 consecutive logits of one row (38 workgroups over
+// 151,936), stages them in LDS, applies the penalties of the window ids that fall in its range, and reduces
+// (value, index) to its best. The row's best of all
 // workgroups is one 64-bit atomic max on an order-preserving key (value bits mapped to unsigned order, −0 as +0, then
 // the complemented index, so ties go to the lowest index); the last workgroup of the row (atomic ticket) reads it,
 // writes the token, appends it to the history and updates the counts. One launch per choice; the key and the ticket
