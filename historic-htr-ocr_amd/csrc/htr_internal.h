@@ -158,7 +158,8 @@ struct ChooseArgs {
     uint32_t *counters;  // [rows] × 128 B, zero, self-resetting: the row's ticket
     int rows;
 };
-int choose_groups(int n_vocab);
+// workgroups of the choice over n_vocab logits, span logits each
+int choose_groups(int n_vocab, int span);
 // bytes of the choice's per-row best keys and tickets (one 128-byte line per row; zero, self-resetting)
 size_t choose_best_bytes(int rows);
 size_t choose_ticket_bytes(int rows);
