@@ -193,8 +193,8 @@ __device__ __forceinline__ void post_apply(const PostIn &p, const float (&cs)[16
 template <int NI, bool FUSED>
 __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float16 *kc, const _Float16 *vc, int n_kv,
                                                     int n_ctx, const int *pos_dev, int n_keys_arg, int max_chunk,
-                                                    float scale, float *part, uint32_t *counters, float *out,
-                                                    AttnFuse fz) {
+                                                    float scale, float post, float *part, uint32_t *counters,
+                                                    float *out, AttnFuse fz) {
     constexpr int C = 16 * NI;
     constexpr int N = 2 * NI;              // (key, head) values per thread
     constexpr int KL = C >= 64 ? C / 64 : 1;  // keys per lane in the softmax
@@ -278,12 +278,14 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         }
     }
 
-    // 1. scores
+    // 1. scores. FUSED: every key at or past pos takes the new row (keys past pos were clamped onto row pos, whose
+    // cache contents are stale — a rewound session's old row — and being rewritten by this workgroup): masked keys
+    // then multiply finite values by 0 below, whatever the cache held
     float v[N];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         float kf[8];
-        unpack8(FUSED && k0 + kk + 16 * i == pos ? knew : kr[i], kf);
+        unpack8(FUSED && k0 + kk + 16 * i >= pos ? knew : kr[i], kf);
         float da = 0.0f, db = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         for (int r = 0; r < N / 16; r++) {
             const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
             const int key = kk + 16 * i;
-            s_sc[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
+            s_sc[h][key] = k0 + key < n_keys ? v[r] * post : -INFINITY;
         }
     } else {
         constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;  // log2 N
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
         if ((j & ((16 >> S) - 1)) == 0) {
             const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
             const int key = kk + 16 * i;
-            s_sc[h][key] = k0 + key < n_keys ? t : -INFINITY;
+            s_sc[h][key] = k0 + key < n_keys ? t * post : -INFINITY;
         }
     }
     __syncthreads();
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(AW) void k_attn_decode(const float *q, const _Float
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         float vf[8];
-        unpack8(FUSED && k0 + kk + 16 * i == pos ? vnew : vr[i], vf);
+        unpack8(FUSED && k0 + kk + 16 * i >= pos ? vnew : vr[i], vf);
         const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -676,7 +678,7 @@ int launch_qkv_post(htr_device *dev, hipStream_t st, float *qkv, const float *qn
 
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
-                       const AttnScratch &sc, float *out, const AttnFuse *fuse) {
+                       const AttnScratch &sc, float *out, const AttnFuse *fuse, bool scale_after) {
     if (n_head != 2 * n_kv) return htr_fail("decode attention: %d q heads on %d kv heads (groups of 2)", n_head, n_kv);
     if (sc.chunk < 16 || sc.chunk > MAX_CHUNK_KEYS || (sc.chunk & (sc.chunk - 1)))
         return htr_fail("decode attention: chunk %d (a power of two, 16 … %d)", sc.chunk, MAX_CHUNK_KEYS);
@@ -689,14 +691,18 @@ int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const ui
     const AttnFuse fz = fuse ? *fuse : AttnFuse{};
     if (fuse && (fz.n_head != n_head || !fz.qn || !fz.kn || !fz.rope || !fz.kc || !fz.vc))
         return htr_fail("decode attention: incomplete qkv_post arguments");
+    // the F32 path scales each score after its dot product (attn_scores.wgsl:38); the f16 paths scale q first
+    // (attn_decode.wgsl:40). A scale of exactly 1 on the other side leaves the values as they are.
+    if (scale_after && fuse) return htr_fail("decode attention: the fused step pre-scales q");
+    const float pre = scale_after ? 1.0f : scale, post = scale_after ? scale : 1.0f;
 #define HTR_ATTN(NI)                                                                                                   \
     if (fuse)                                                                                                          \
         hipLaunchKernelGGL((k_attn_decode<NI, true>), grid, dim3(AW), 0, st, q, (const _Float16 *)kc,                  \
-                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part,           \
+                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, pre, post, sc.part,       \
                            sc.counters, out, fz);                                                                      \
     else                                                                                                               \
         hipLaunchKernelGGL((k_attn_decode<NI, false>), grid, dim3(AW), 0, st, q, (const _Float16 *)kc,                 \
-                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, scale, sc.part,           \
+                           (const _Float16 *)vc, n_kv, n_ctx, pos_dev, n_keys, sc.max_chunk, pre, post, sc.part,       \
                            sc.counters, out, fz)
     switch (sc.chunk / 16) {
     case 1: HTR_ATTN(1); break;

@@ -41,7 +41,15 @@ struct htr_device {
     bool use_graphs = true;
     // the compute path of the models created on this device (HTR_COMPUTE_F16 / HTR_COMPUTE_F32)
     int compute = HTR_COMPUTE_F16;
+    // the caller is capturing the device's stream (htr_capture_begin … end): nothing may allocate or synchronise
+    bool capturing = false;
+    // the last kernel launched (its instance: template arguments included), for tests that check the dispatch
+    std::string last_kernel;
 };
+
+// -1 with a message when the device's stream is being captured by the caller (allocation and synchronisation are not
+// part of a graph), else 0
+int htr_check_not_capturing(htr_device *dev, const char *what);
 
 enum {
     SCR_CHOOSE_PART = 0,
@@ -124,9 +132,10 @@ struct AttnFuse {
     int n_head;
     _Float16 *kc, *vc;
 };
+// scale_after: the score is (q·k)·scale (the F32 path's attn_scores) instead of (q·scale)·k (not with fuse)
 int launch_attn_decode(htr_device *dev, hipStream_t st, const float *q, const uint16_t *kc, const uint16_t *vc,
                        int n_head, int n_kv, int n_ctx, const int *pos_dev, int n_keys, float scale,
-                       const AttnScratch &sc, float *out, const AttnFuse *fuse = nullptr);
+                       const AttnScratch &sc, float *out, const AttnFuse *fuse = nullptr, bool scale_after = false);
 // prefill pieces: per-head norm + rope + KV store over n_tok rows
 int launch_qk_norm_rope_rows(htr_device *dev, hipStream_t st, float *q, float *k, const float *v, const float *qn,
                              const float *kn, const float *rope, int n_tok, int n_head, int n_kv, int pos0, int n_ctx,

@@ -19,6 +19,8 @@
 //   math      f32 (the reference's numbers: exact int8·f16-scale dequant, f32 products and sums): the 16 products
 //             of a group are an fma chain, times the block's scale into the row's accumulator. The int8 → f32
 //             conversion is one v_cvt_f32_i32 with a sign-extended byte select per quant.
+#include <cstdio>
+
 #include "htr_internal.h"
 #include "wave.h"
 
@@ -471,6 +473,10 @@ int rows_per_wave(int n_rows, int n_cu, int ng_lane, int nm, int rw) {
     return rw;
 }
 
+const char *mode_name(int mode) {
+    return mode == DMV_PLAIN ? "plain" : mode == DMV_NORM ? "norm" : mode == DMV_QKV ? "qkv" : "ffn";
+}
+
 }  // namespace
 
 int dmv_full_rw(htr_device *dev, int mode, const DmvMat *mats, int n_mats, int k) {
@@ -528,7 +534,9 @@ int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, in
         }
 #undef HTR_FULL_RW
 #undef HTR_FULL
-        return htr_launched(dev, "k_dmv_full");
+        char name[48];
+        snprintf(name, sizeof name, "k_dmv_full<%d,%d,%s>", full_rw, std::min(k / 1024, 3), mode_name(mode));
+        return htr_launched(dev, name);
     }
     // 8 rows a wave at most: the LM head (151,936 rows) decodes 1638 tokens/s against 1630 with 16 and 1631 with 4
     const int rw = rows_per_wave(rows, dev->n_cu, ng_lane, mode == DMV_FFN ? 2 : 1, 8);
@@ -540,7 +548,9 @@ int launch_dmv(htr_device *dev, hipStream_t st, int mode, const DmvMat *mats, in
     case DMV_FFN: rc = dispatch_r<DMV_FFN>(st, rw, ng_lane, a); break;
     }
     if (rc < 0) return htr_fail("matvec: no kernel for mode %d, RW %d, K %d", mode, rw, k);
-    return htr_launched(dev, "k_dmv");
+    char name[48];
+    snprintf(name, sizeof name, "k_dmv<%d,%d,%s>", rw, ng_lane, mode_name(mode));
+    return htr_launched(dev, name);
 }
 
 int launch_dmv_many(htr_device *dev, hipStream_t st, const DmvMat *mats, int n, int k, const float *x, float *y) {

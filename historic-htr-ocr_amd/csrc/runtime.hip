@@ -51,7 +51,21 @@ int htr_hip(htr_device *dev, hipError_t e, const char *what) {
     return htr_latch(dev, kind, msg);
 }
 
-int htr_launched(htr_device *dev, const char *kernel) { return htr_hip(dev, hipGetLastError(), kernel); }
+int htr_launched(htr_device *dev, const char *kernel) {
+    dev->last_kernel = kernel;
+    return htr_hip(dev, hipGetLastError(), kernel);
+}
+
+int htr_check_not_capturing(htr_device *dev, const char *what) {
+    if (dev->capturing) return htr_fail("%s: the device's stream is being captured (htr_capture_begin)", what);
+    return 0;
+}
+
+extern "C" int htr_debug_last_kernel(htr_device *dev, char *name, size_t cap) {
+    if (!dev || !name || !cap) return htr_fail("htr_debug_last_kernel: null argument");
+    snprintf(name, cap, "%s", dev->last_kernel.c_str());
+    return 0;
+}
 
 // ---- device ---------------------------------------------------------------------------------------------------------
 
@@ -128,6 +142,7 @@ extern "C" int htr_timer_begin(htr_device *dev) {
 
 extern "C" int htr_timer_end(htr_device *dev, float *ms) {
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_timer_end"));
     if (!ms) return htr_fail("htr_timer_end: null out");
     HTR_TRY(htr_hip(dev, hipEventRecord(dev->t1, dev->stream), "hipEventRecord"));
     HTR_TRY(htr_hip(dev, hipEventSynchronize(dev->t1), "hipEventSynchronize"));
@@ -137,6 +152,11 @@ extern "C" int htr_timer_end(htr_device *dev, float *ms) {
 extern "C" int htr_device_close(htr_device *dev) {
     if (!dev) return 0;
     hipSetDevice(dev->ordinal);
+    if (dev->capturing) {  // a capture left open: end it and drop what it recorded
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(dev->stream, &g) == hipSuccess && g) hipGraphDestroy(g);
+        dev->capturing = false;
+    }
     if (dev->dead_msg.empty()) hipStreamSynchronize(dev->stream);
     for (auto &a : dev->allocs) hipFree(a.first);
     dev->allocs.clear();
@@ -165,7 +185,56 @@ extern "C" int htr_debug_mark_lost(htr_device *dev, const char *why) {
 
 extern "C" int htr_sync(htr_device *dev) {
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_sync"));
     return htr_hip(dev, hipStreamSynchronize(dev->stream), "hipStreamSynchronize");
+}
+
+// ---- stream capture into HIP graphs -----------------------------------------------------------------------------------
+
+struct htr_graph {
+    htr_device *dev = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" int htr_capture_begin(htr_device *dev) {
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_capture_begin"));
+    HTR_TRY(htr_hip(dev, hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
+    dev->capturing = true;
+    return 0;
+}
+
+extern "C" int htr_capture_end(htr_device *dev, htr_graph **out) {
+    if (!dev || !out) return htr_fail("htr_capture_end: null argument");
+    if (!dev->capturing) return htr_fail("htr_capture_end: no capture in progress");
+    dev->capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(dev->stream, &graph);
+    HTR_TRY(htr_hip(dev, e, "hipStreamEndCapture"));
+    auto *g = new htr_graph;
+    g->dev = dev;
+    e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+        delete g;
+        return htr_hip(dev, e, "hipGraphInstantiate");
+    }
+    *out = g;
+    return 0;
+}
+
+extern "C" int htr_graph_launch(htr_graph *g) {
+    if (!g) return htr_fail("htr_graph_launch: null graph");
+    HTR_TRY(htr_check_alive(g->dev));
+    HTR_TRY(htr_check_not_capturing(g->dev, "htr_graph_launch"));
+    return htr_hip(g->dev, hipGraphLaunch(g->exec, g->dev->stream), "hipGraphLaunch");
+}
+
+extern "C" int htr_graph_free(htr_graph *g) {
+    if (!g) return 0;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    delete g;
+    return 0;
 }
 
 extern "C" int htr_device_info(htr_device *dev, char *name, size_t name_len, int *n_cu) {
@@ -193,6 +262,7 @@ static uint64_t *ledger(htr_device *dev, int kind) {
 
 int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out) {
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "device allocation"));
     if (kind < HTR_MEM_WEIGHTS || kind > HTR_MEM_READBACK) return htr_fail("memory kind %d: 0…3", kind);
     size_t b = std::max<size_t>(bytes, 4);
     void *p = nullptr;
@@ -213,6 +283,7 @@ int htr_dev_free(htr_device *dev, void *p) {
     if (!p) return 0;
     auto it = dev->allocs.find(p);
     if (it == dev->allocs.end()) return htr_fail("htr_free: %p is not an allocation of device %d", p, dev->ordinal);
+    HTR_TRY(htr_check_not_capturing(dev, "htr_free"));
     // the stream's work that may still read it finishes first (a Buf outlives every submission that binds it)
     if (dev->dead_msg.empty()) hipStreamSynchronize(dev->stream);
     *ledger(dev, it->second.second) -= it->second.first;
@@ -251,6 +322,7 @@ extern "C" int htr_free(htr_device *dev, void *d_ptr) {
 
 extern "C" int htr_upload(htr_device *dev, void *d_dst, const void *h_src, size_t bytes) {
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_upload"));
     if (!bytes) return 0;
     HTR_TRY(htr_hip(dev, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, dev->stream), "upload"));
     // pageable source: the copy is complete once the stream reaches it; waiting keeps the caller's buffer free to reuse
@@ -259,6 +331,7 @@ extern "C" int htr_upload(htr_device *dev, void *d_dst, const void *h_src, size_
 
 extern "C" int htr_download(htr_device *dev, void *h_dst, const void *d_src, size_t bytes) {
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_download"));
     if (!bytes) return 0;
     HTR_TRY(htr_hip(dev, hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, dev->stream), "download"));
     return htr_hip(dev, hipStreamSynchronize(dev->stream), "download sync");

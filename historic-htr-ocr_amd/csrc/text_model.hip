@@ -59,6 +59,7 @@ struct htr_session {
     uint16_t *kc = nullptr, *vc = nullptr;
     float *rope = nullptr;
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *g = nullptr, *logits = nullptr;
+    float *h = nullptr, *u = nullptr;  // the F32 path's step: the normed row and the up projection
     uint32_t *tok = nullptr;
     int *state = nullptr;  // [pos, len]
     AttnScratch asc{};
@@ -113,7 +114,45 @@ int upload_w(htr_device *dev, const void *h, size_t rows, size_t cols, const cha
     return 0;
 }
 
-// one decode step on the session's stream: token s->tok at position state[0] → s->logits
+// the F32 path's decode step (text.rs:555-576; its kernels stay the reference's on that path): rms_norm → q / k / v
+// matvecs → qkv_post (per-head norms, RoPE, f16 KV store) → attention with the score scaled after its dot product
+// (attn_scores.wgsl:38) → o matvec (+ residual) → rms_norm → gate and up matvecs → swiglu → down matvec (+ residual);
+// the head as rms_norm + matvec (text.rs:655-658)
+int record_step_f32(htr_session *s, hipStream_t st) {
+    htr_text_model *m = s->m;
+    htr_device *dev = s->dev;
+    const htr_text_config &c = m->cfg;
+    const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
+    const float scale = 1.0f / sqrtf((float)HEAD);
+    for (int li = 0; li < c.n_layer; li++) {
+        const Layer &ly = m->layers[li];
+        uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
+        HTR_TRY(launch_rms_norm(dev, st, s->x, ly.attn_norm, s->h, 1, c.dim, c.eps));
+        const DmvMat q = {ly.q->q, ly.q->d, qd}, k = {ly.k->q, ly.k->d, kvd}, v = {ly.v->q, ly.v->d, kvd};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &q, 1, c.dim, s->h, nullptr, 0.0f, s->qkv, 0));
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &k, 1, c.dim, s->h, nullptr, 0.0f, s->qkv + qd, 0));
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &v, 1, c.dim, s->h, nullptr, 0.0f, s->qkv + qd + kvd, 0));
+        HTR_TRY(launch_qkv_post(dev, st, s->qkv, ly.q_norm, ly.k_norm, s->rope, c.n_head, c.n_kv, s->state, 0, s->n_ctx,
+                                c.eps, kc, vc));
+        HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale, s->asc,
+                                   s->attn, nullptr, true));
+        const DmvMat o = {ly.o->q, ly.o->d, c.dim};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
+        HTR_TRY(launch_rms_norm(dev, st, s->x, ly.ffn_norm, s->h, 1, c.dim, c.eps));
+        const DmvMat gm = {ly.gate->q, ly.gate->d, c.n_ff}, um = {ly.up->q, ly.up->d, c.n_ff};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &gm, 1, c.dim, s->h, nullptr, 0.0f, s->g, 0));
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &um, 1, c.dim, s->h, nullptr, 0.0f, s->u, 0));
+        HTR_TRY(launch_swiglu(dev, st, s->g, s->u, (size_t)c.n_ff));
+        const DmvMat dn = {ly.down->q, ly.down->d, c.dim};
+        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &dn, 1, c.n_ff, s->g, nullptr, 0.0f, s->x, 1));
+    }
+    HTR_TRY(launch_rms_norm(dev, st, s->x, m->output_norm, s->h, 1, c.dim, c.eps));
+    const DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
+    return launch_dmv(dev, st, DMV_PLAIN, &head, 1, c.dim, s->h, nullptr, 0.0f, s->logits, 0);
+}
+
+// one decode step on the session's stream: token s->tok at position state[0] → s->logits. The f16 paths' fused step
+// (record_step, text.rs:540-552 + layers_fused), or the F32 path's (record_step_f32) for a model of that path.
 int record_step(htr_session *s, hipStream_t st) {
     htr_text_model *m = s->m;
     htr_device *dev = s->dev;
@@ -121,6 +160,7 @@ int record_step(htr_session *s, hipStream_t st) {
     const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const float scale = 1.0f / sqrtf((float)HEAD);
     HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
+    if (m->compute == HTR_COMPUTE_F32) return record_step_f32(s, st);
     for (int li = 0; li < c.n_layer; li++) {
         const Layer &ly = m->layers[li];
         uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
@@ -411,7 +451,7 @@ extern "C" int htr_session_free(htr_session *s) {
     if (s->step_graph) hipGraphExecDestroy(s->step_graph);
     for (void *p : {(void *)s->kc, (void *)s->vc, (void *)s->rope, (void *)s->x, (void *)s->qkv, (void *)s->attn,
                     (void *)s->g, (void *)s->logits, (void *)s->tok, (void *)s->state, (void *)s->asc.part,
-                    (void *)s->asc.counters, s->pre, s->kvb})
+                    (void *)s->asc.counters, s->pre, s->kvb, (void *)s->h, (void *)s->u})
         if (p) htr_dev_free(dev, p);
     delete s;
     return 0;
@@ -445,6 +485,8 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
     if (rc == 0) rc = htr_dev_alloc(dev, (qd + 2 * kvd) * 4, HTR_MEM_WORK, (void **)&s->qkv);
     if (rc == 0) rc = htr_dev_alloc(dev, qd * 4, HTR_MEM_WORK, (void **)&s->attn);
     if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_ff * 4, HTR_MEM_WORK, (void **)&s->g);
+    if (rc == 0 && m->compute == HTR_COMPUTE_F32) rc = htr_dev_alloc(dev, (size_t)c.dim * 4, HTR_MEM_WORK, (void **)&s->h);
+    if (rc == 0 && m->compute == HTR_COMPUTE_F32) rc = htr_dev_alloc(dev, (size_t)c.n_ff * 4, HTR_MEM_WORK, (void **)&s->u);
     if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.n_vocab * 4, HTR_MEM_WORK, (void **)&s->logits);
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->tok);
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->state);
@@ -474,6 +516,19 @@ extern "C" int htr_session_logits(htr_session *s, float *h_logits) {
 
 int session_n_vocab(const htr_session *s) { return s->m->cfg.n_vocab; }
 
+extern "C" int htr_session_kv_cache(htr_session *s, htr_kv_view *out) {
+    if (!s || !out) return htr_fail("htr_session_kv_cache: null argument");
+    const htr_text_config &c = s->m->cfg;
+    out->d_k = s->kc;
+    out->d_v = s->vc;
+    out->n_layer = c.n_layer;
+    out->n_kv = c.n_kv;
+    out->n_ctx = s->n_ctx;
+    out->d_head = HEAD;
+    out->layer_stride = s->kv_layer;
+    return 0;
+}
+
 extern "C" int htr_session_rewind(htr_session *s, size_t n_past) {
     if (!s) return htr_fail("htr_session_rewind: null session");
     if (n_past > (size_t)s->n_past) return htr_fail("rewind to %zu: the session is at %d", n_past, s->n_past);
@@ -486,6 +541,7 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
     if (!s || !ids) return htr_fail("htr_prefill: null argument");
     htr_device *dev = s->dev;
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_prefill"));
     htr_text_model *m = s->m;
     const htr_text_config &c = m->cfg;
     if (n == 0) return htr_fail("empty prompt");
@@ -595,6 +651,7 @@ extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
     if (!s) return htr_fail("htr_step: null session");
     htr_device *dev = s->dev;
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_step"));
     const htr_text_config &c = s->m->cfg;
     if (token < 0 || token >= c.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
     if (s->n_past + 1 > s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
@@ -683,6 +740,7 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
     if (!s || !ch || ch->s != s) return htr_fail("htr_decode_gpu: null argument or a choice of another session");
     htr_device *dev = s->dev;
     HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_decode_gpu"));
     const size_t cap = ch->max_new;
     if (max > cap) return htr_fail("%zu choices: the history holds %zu", max, cap);
     if (max == 0) return 0;

@@ -35,6 +35,8 @@ SYMBOLS = [
     "htr_text_model_config", "htr_session_create", "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
+    "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
+    "htr_graph_free",
 ]
 
 
@@ -64,6 +66,11 @@ class GgufTensorC(C.Structure):
 
 
 READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint64, C.c_void_p, C.c_size_t)
+
+
+class KvViewC(C.Structure):
+    _fields_ = [("d_k", C.c_void_p), ("d_v", C.c_void_p), ("n_layer", C.c_int), ("n_kv", C.c_int),
+                ("n_ctx", C.c_int), ("d_head", C.c_int), ("layer_stride", C.c_size_t)]
 
 
 class PresetC(C.Structure):
@@ -162,6 +169,12 @@ def lib() -> C.CDLL:
             "htr_step": (i32, [vp, C.c_int32, vp]),
             "htr_session_logits": (i32, [vp, vp]),
             "htr_session_rewind": (i32, [vp, sz]),
+            "htr_session_kv_cache": (i32, [vp, C.POINTER(KvViewC)]),
+            "htr_debug_last_kernel": (i32, [vp, C.c_char_p, sz]),
+            "htr_capture_begin": (i32, [vp]),
+            "htr_capture_end": (i32, [vp, pp]),
+            "htr_graph_launch": (i32, [vp]),
+            "htr_graph_free": (i32, [vp]),
             "htr_choice_create": (i32, [vp, C.POINTER(PresetC), vp, sz, sz, sz, pp]),
             "htr_choice_free": (i32, [vp]),
             "htr_decode_gpu": (i32, [vp, vp, sz, TOKEN_CB, vp]),
@@ -311,12 +324,41 @@ class Device:
     def mark_lost(self, why: str = "") -> None:
         _check(lib().htr_debug_mark_lost(self.h, why.encode()))
 
+    def last_kernel(self) -> str:
+        """the instance name of the last kernel this device launched (e.g. 'k_dmv_full<4,1,qkv>')"""
+        buf = C.create_string_buffer(96)
+        _check(lib().htr_debug_last_kernel(self.h, buf, 96))
+        return buf.value.decode()
+
+    def capture_begin(self) -> None:
+        _check(lib().htr_capture_begin(self.h))
+
+    def capture_end(self) -> "Graph":
+        g = C.c_void_p()
+        _check(lib().htr_capture_end(self.h, C.byref(g)))
+        return Graph(self, g.value)
+
     def alloc(self, nbytes: int, kind: int = MEM_WORK) -> Buffer:
         return Buffer(self, nbytes, kind)
 
     def upload(self, a: np.ndarray, kind: int = MEM_WORK) -> Buffer:
         a = np.ascontiguousarray(a)
         return Buffer(self, max(a.nbytes, 4), kind).upload(a)
+
+
+class Graph:
+    """a recorded HIP graph of the device's stream (Device.capture_begin … capture_end), replayed by launch()"""
+
+    def __init__(self, dev: "Device", h: int):
+        self.dev, self.h = dev, h
+
+    def launch(self) -> None:
+        _check(lib().htr_graph_launch(self.h))
+
+    def free(self) -> None:
+        if self.h:
+            lib().htr_graph_free(self.h)
+            self.h = None
 
 
 class Weight:
@@ -631,6 +673,33 @@ class Session:
 
     def rewind(self, n_past: int) -> None:
         _check(lib().htr_session_rewind(self.h, n_past))
+
+    def kv_view(self) -> KvViewC:
+        v = KvViewC()
+        _check(lib().htr_session_kv_cache(self.h, C.byref(v)))
+        return v
+
+    def kv_rows(self, layer: int, pos0: int, n: int) -> tuple[np.ndarray, np.ndarray]:
+        """cache rows [pos0, pos0 + n) of a layer as f16 bits in the reference's layout [n][n_kv·128] (K, V)"""
+        v = self.kv_view()
+        out = []
+        for base in (v.d_k, v.d_v):
+            a = np.empty((v.n_kv, n, v.d_head), np.uint16)
+            for h in range(v.n_kv):
+                off = 2 * (layer * v.layer_stride + (h * v.n_ctx + pos0) * v.d_head)
+                _check(lib().htr_download(self.m.dev.h, _ptr(a[h]), base + off, n * v.d_head * 2))
+            out.append(np.ascontiguousarray(a.transpose(1, 0, 2).reshape(n, v.n_kv * v.d_head)))
+        return out[0], out[1]
+
+    def set_kv_rows(self, layer: int, pos0: int, k: np.ndarray, v_rows: np.ndarray) -> None:
+        """write cache rows [pos0, pos0 + n) of a layer from f16 bits [n][n_kv·128] (tests that plant rows)"""
+        v = self.kv_view()
+        n = k.shape[0]
+        for base, rows in ((v.d_k, k), (v.d_v, v_rows)):
+            a = np.ascontiguousarray(np.asarray(rows, np.uint16).reshape(n, v.n_kv, v.d_head).transpose(1, 0, 2))
+            for h in range(v.n_kv):
+                off = 2 * (layer * v.layer_stride + (h * v.n_ctx + pos0) * v.d_head)
+                _check(lib().htr_upload(self.m.dev.h, base + off, _ptr(a[h]), n * v.d_head * 2))
 
     def choice(self, preset: Preset, history, chunk: int = 4, depth: int = 2) -> "Choice":
         return Choice(self, preset, history, chunk, depth)

@@ -54,8 +54,10 @@ int htr_sync(htr_device *dev);
  * default, and what the reference picks on a device with f16 and matrix units (F16Coop) — rounds the prefill GEMMs' X
  * and dequantised W to f16 and sums in f32 (matmul_coop_q8_0); HTR_COMPUTE_F32 computes them from the exact q8_0
  * values in f32 (matmul128_q8_0). OCR_WGPU_COMPUTE = f32 / f16 / coop at open sets it as the reference's env var does.
- * A text model keeps the path of its device at creation. The decode step and the vision encoder run the f16 paths'
- * kernels on either setting (f32 arithmetic in the decode; the vision encoder's F32 path is not built). */
+ * A text model keeps the path of its device at creation, for its prefill and its decode step: the F32 path's step is
+ * the reference's (text.rs:555-576: rms_norm, one matvec per projection, qkv_post, the attention with each score
+ * scaled after its dot product, swiglu), the f16 paths' the fused one (layers_fused, text.rs:630-647); both compute
+ * in f32. The vision encoder runs its f16 path on either setting (its F32 path is not built). */
 enum { HTR_COMPUTE_F32 = 0, HTR_COMPUTE_F16 = 1 };
 int htr_device_set_compute(htr_device *dev, int compute);
 int htr_device_compute(htr_device *dev, int *compute);
@@ -66,6 +68,22 @@ int htr_device_info(htr_device *dev, char *name, size_t name_len, int *n_cu);
  * and returns the elapsed milliseconds */
 int htr_timer_begin(htr_device *dev);
 int htr_timer_end(htr_device *dev, float *ms);
+
+/* the name of the last kernel this device launched, template arguments included (e.g. "k_dmv_full<4,1,qkv>"): for tests
+ * that check which kernel instance an entry point dispatched (no reference counterpart) */
+int htr_debug_last_kernel(htr_device *dev, char *name, size_t cap);
+
+/* ---- HIP graphs of the device's stream (no reference counterpart: the reference records a wgpu command buffer per
+ *      submission, gpu.rs:1864-1960; here a caller records entry-point calls once and replays them) --------------- */
+typedef struct htr_graph htr_graph;
+/* begin recording the device's stream: the kernel entry points called until htr_capture_end are recorded, not run.
+ * While recording, every call that allocates, frees, copies to or from the host or waits fails (an entry point whose
+ * scratch would grow must have run once at that size before); so do htr_prefill, htr_step and htr_decode_gpu. */
+int htr_capture_begin(htr_device *dev);
+int htr_capture_end(htr_device *dev, htr_graph **out);
+/* replay a recorded graph on the device's stream */
+int htr_graph_launch(htr_graph *g);
+int htr_graph_free(htr_graph *g);
 
 /* ---- memory (gpu.rs:509-561 ledger per MemKind; gpu.rs:1489-1590 upload / scratch / readback / read_f32) ------- */
 enum { HTR_MEM_WEIGHTS = 0, HTR_MEM_KV_CACHE = 1, HTR_MEM_WORK = 2, HTR_MEM_READBACK = 3 };
@@ -259,6 +277,15 @@ int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *h_logits);
 int htr_step(htr_session *s, int32_t tok, float *h_logits);
 /* the session's last logits (after prefill / step / a GPU choice: penalised in place) → h_logits */
 int htr_session_logits(htr_session *s, float *h_logits);
+/* the session's KV cache on the device (text.rs:242-260 Session::k / v, one buffer per layer there): f16 K and V,
+ * each [n_layer][n_kv][n_ctx][d_head] (layer_stride halves per layer) — head-major, where the reference keeps
+ * [pos][n_kv·d_head]. For tests that read back or plant rows; the pointers live as long as the session. */
+typedef struct {
+    uint16_t *d_k, *d_v;
+    int n_layer, n_kv, n_ctx, d_head;
+    size_t layer_stride;
+} htr_kv_view;
+int htr_session_kv_cache(htr_session *s, htr_kv_view *out);
 /* forget the positions ≥ n_past (≤ the current n_past): later steps rewrite their KV rows. No reference counterpart
  * (a read's session only grows, text.rs:242-328); it lets a bench replay one read's decode */
 int htr_session_rewind(htr_session *s, size_t n_past);

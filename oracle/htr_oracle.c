@@ -520,6 +520,79 @@ void or_attn_decode(const float *q, const uint16_t *k, const uint16_t *v, size_t
     free(part);
 }
 
+/* the F32 path's decode attention, three kernels (text.rs:567-569), one q head at a time:
+ *   attn_scores.wgsl:26-38   S[j] = (Σ over the 32 vec4 of the head: d = fma(q4, k4, d) per component;
+ *                            then ((d.x + d.y) + d.z) + d.w) · scale
+ *   attn_softmax.wgsl:22-60  256 lanes: lane ℓ takes keys ℓ, ℓ + 256, …; max from −3e38; e = exp(S − m) in place;
+ *                            lane sums in key order, then the tree part[i] += part[i + n] (n = 128 … 1); S ·= 1 / Σ
+ *   attn_values.wgsl:29-45   lane (e, r): vec4 e of the head, keys r, r + 8, … (fma(S_j, v4, acc)); then
+ *                            part_0 + part_1 + … + part_7 of vec4 e in order */
+void or_attn_decode_f32(const float *q, const uint16_t *k, const uint16_t *v, size_t kv_stride, int n_keys, int n_head,
+                        int n_kv, float scale, float *out) {
+    int group = n_head / n_kv;
+#pragma omp parallel for schedule(static)
+    for (int h = 0; h < n_head; h++) {
+        int kvh = h / group;
+        float *S = (float *)malloc((size_t)n_keys * sizeof(float));
+        const float *qh = q + (size_t)h * 128;
+        for (int j = 0; j < n_keys; j++) {
+            const uint16_t *kr = k + (size_t)j * kv_stride + (size_t)kvh * 128;
+            float dv[4] = {0, 0, 0, 0};
+            for (int e = 0; e < 32; e++) {
+                for (int cc = 0; cc < 4; cc++) {
+                    dv[cc] = fmaf(qh[4 * e + cc], or_f32_from_f16(kr[4 * e + cc]), dv[cc]);
+                }
+            }
+            S[j] = (((dv[0] + dv[1]) + dv[2]) + dv[3]) * scale;
+        }
+        float part[256];
+        float m = -3.0e38f;
+        for (int j = 0; j < n_keys; j++) {
+            m = fmaxf(m, S[j]);
+        }
+        for (int li = 0; li < 256; li++) {
+            float sm = 0.0f;
+            for (int j = li; j < n_keys; j += 256) {
+                float e = expf(S[j] - m);
+                S[j] = e;
+                sm += e;
+            }
+            part[li] = sm;
+        }
+        for (int n = 128; n > 0; n >>= 1) {
+            for (int li = 0; li < n; li++) {
+                part[li] += part[li + n];
+            }
+        }
+        float inv = 1.0f / part[0];
+        for (int j = 0; j < n_keys; j++) {
+            S[j] *= inv;
+        }
+        for (int e = 0; e < 32; e++) {
+            float acc[8][4];
+            for (int r = 0; r < 8; r++) {
+                for (int cc = 0; cc < 4; cc++) {
+                    acc[r][cc] = 0.0f;
+                }
+                for (int j = r; j < n_keys; j += 8) {
+                    const uint16_t *vr = v + (size_t)j * kv_stride + (size_t)kvh * 128 + 4 * e;
+                    for (int cc = 0; cc < 4; cc++) {
+                        acc[r][cc] = fmaf(S[j], or_f32_from_f16(vr[cc]), acc[r][cc]);
+                    }
+                }
+            }
+            for (int cc = 0; cc < 4; cc++) {
+                float sm = acc[0][cc];
+                for (int r = 1; r < 8; r++) {
+                    sm += acc[r][cc];
+                }
+                out[(size_t)h * 128 + 4 * e + cc] = sm;
+            }
+        }
+        free(S);
+    }
+}
+
 /* attention_causal.wgsl:42-93 (F32 path, tiles of TK = 8 keys): one query row, one head */
 static void attn_causal_row(const float *q, const uint16_t *k, const uint16_t *v, size_t kv_stride, int qpos, int kvh,
                             float scale, float *out) {
@@ -744,9 +817,34 @@ struct or_session {
     uint16_t *kc, *vc; /* [layer][pos][n_kv·128] f16, the reference's cache layout (kv_store.wgsl) */
     float *rope;       /* [n_ctx][64] × (cos, sin) */
     int r16;           /* the prefill GEMMs on the f16 paths' rounding */
+    int step_f32;      /* the decode step of the F32 path (text.rs:555-576) instead of the fused one */
 };
 
 void or_session_set_f16(or_session *s, int on) { s->r16 = on != 0; }
+
+void or_session_set_step_f32(or_session *s, int on) { s->step_f32 = on != 0; }
+
+/* the cache rows [pos0, pos0 + n) of one layer in the reference's layout [pos][n_kv·128] f16: copied out of / into the
+ * session (a test hands a device's cache over, or reads back what a step stored) */
+int or_session_get_kv(const or_session *s, int layer, int pos0, int n, uint16_t *k, uint16_t *v) {
+    if (layer < 0 || layer >= s->c.n_layer || pos0 < 0 || n < 0 || pos0 + n > s->n_ctx) {
+        return -1;
+    }
+    size_t kvd = (size_t)s->c.n_kv * 128, off = ((size_t)layer * s->n_ctx + pos0) * kvd;
+    memcpy(k, s->kc + off, (size_t)n * kvd * 2);
+    memcpy(v, s->vc + off, (size_t)n * kvd * 2);
+    return 0;
+}
+
+int or_session_set_kv(or_session *s, int layer, int pos0, int n, const uint16_t *k, const uint16_t *v) {
+    if (layer < 0 || layer >= s->c.n_layer || pos0 < 0 || n < 0 || pos0 + n > s->n_ctx) {
+        return -1;
+    }
+    size_t kvd = (size_t)s->c.n_kv * 128, off = ((size_t)layer * s->n_ctx + pos0) * kvd;
+    memcpy(s->kc + off, k, (size_t)n * kvd * 2);
+    memcpy(s->vc + off, v, (size_t)n * kvd * 2);
+    return 0;
+}
 
 or_session *or_session_new(const or_text_cfg *cfg, const uint8_t *tok_embd, const float *output_norm,
                            const or_layer *layers, int n_ctx) {
@@ -925,11 +1023,57 @@ int or_session_prefill(or_session *s, const int32_t *ids, int l, float *logits) 
     return 0;
 }
 
-/* text.rs:540-552 + layers_fused text.rs:630-647 */
+/* record_step on the F32 path (text.rs:555-576): rms_norm → matvec_q8_0 q / k / v → per-head rms_norm of q and k →
+ * rope_neox → kv_store → attn_scores / attn_softmax / attn_values → matvec o (+ residual) → rms_norm → matvec gate
+ * and up → swiglu → matvec down (+ residual); head (text.rs:655-658): rms_norm + matvec_q8_0 */
+static void step_f32(or_session *s, int32_t tok, float *logits) {
+    const or_text_cfg *c = &s->c;
+    size_t d = c->dim, f = c->n_ff, qd = (size_t)c->n_head * 128, kvd = (size_t)c->n_kv * 128;
+    int pos = s->n_past;
+    float *x = (float *)malloc(d * 4), *h = (float *)malloc(d * 4);
+    float *qr = (float *)malloc(qd * 4), *q = (float *)malloc(qd * 4), *a = (float *)malloc(qd * 4);
+    float *kr = (float *)malloc(kvd * 4), *kn = (float *)malloc(kvd * 4), *vr = (float *)malloc(kvd * 4);
+    float *g = (float *)malloc(f * 4), *u = (float *)malloc(f * 4);
+    embed_row(s, tok, x);
+    float scale = 1.0f / sqrtf(128.0f);
+    for (int li = 0; li < c->n_layer; li++) {
+        const or_layer *ly = &s->layers[li];
+        uint16_t *kc = s->kc + (size_t)li * s->n_ctx * kvd, *vc = s->vc + (size_t)li * s->n_ctx * kvd;
+        or_rms_norm(x, ly->attn_norm, h, 1, d, c->eps);
+        or_matvec_q8_0(ly->q, qd, d, h, qr, 0);
+        or_matvec_q8_0(ly->k, kvd, d, h, kr, 0);
+        or_matvec_q8_0(ly->v, kvd, d, h, vr, 0);
+        or_rms_norm(qr, ly->q_norm, q, c->n_head, 128, c->eps);
+        or_rms_norm(kr, ly->k_norm, kn, c->n_kv, 128, c->eps);
+        rope_rows(s, q, 1, c->n_head, pos);
+        rope_rows(s, kn, 1, c->n_kv, pos);
+        or_f16_from_f32_n(kn, kc + (size_t)pos * kvd, kvd); /* kv_store.wgsl:18-24 */
+        or_f16_from_f32_n(vr, vc + (size_t)pos * kvd, kvd);
+        or_attn_decode_f32(q, kc, vc, kvd, pos + 1, c->n_head, c->n_kv, scale, a);
+        or_matvec_q8_0(ly->o, d, qd, a, x, 1);
+        or_rms_norm(x, ly->ffn_norm, h, 1, d, c->eps);
+        or_matvec_q8_0(ly->gate, f, d, h, g, 0);
+        or_matvec_q8_0(ly->up, f, d, h, u, 0);
+        for (size_t i = 0; i < f; i++) { /* swiglu.wgsl:18-24 */
+            g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        }
+        or_matvec_q8_0(ly->down, d, f, g, x, 1);
+    }
+    or_rms_norm(x, s->output_norm, h, 1, d, c->eps);
+    or_matvec_q8_0(s->tok_embd, c->n_vocab, d, h, logits, 0);
+    free(x), free(h), free(qr), free(q), free(a), free(kr), free(kn), free(vr), free(g), free(u);
+}
+
+/* text.rs:540-552 + layers_fused text.rs:630-647 (the f16 paths), or the F32 path's step (or_session_set_step_f32) */
 int or_session_step(or_session *s, int32_t tok, float *logits) {
     const or_text_cfg *c = &s->c;
     if (tok < 0 || tok >= c->n_vocab || s->n_past + 1 > s->n_ctx) {
         return -1;
+    }
+    if (s->step_f32) {
+        step_f32(s, tok, logits);
+        s->n_past += 1;
+        return 0;
     }
     size_t d = c->dim, f = c->n_ff, qd = (size_t)c->n_head * 128, kvd = (size_t)c->n_kv * 128;
     int pos = s->n_past;

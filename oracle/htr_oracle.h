@@ -15,11 +15,13 @@
  *   or_matvec_q8_0, or_dmv*           fp64 closed form (numpy) on LCG inputs of text.rs:707-741 / 864-905
  *   or_rms_norm, or_rope_table,
  *   or_qkv_post                       fp64 closed form (numpy) as in text.rs:768-792, 943-972
- *   or_attn_decode, or_attn_causal    fp64 softmax attention (numpy) on f16-rounded K / V, text.rs:797-858, 1264-1292
+ *   or_attn_decode, or_attn_causal,
+ *   or_attn_decode_f32                fp64 softmax attention (numpy) on f16-rounded K / V, text.rs:797-858, 1264-1292
  *   or_choose                         sampling.rs:297-321 unit cases, numpy IEEE division (text.rs:1061-1099 sweep),
  *                                     a brute-force numpy argmax
- *   or_session_prefill / or_session_step
+ *   or_session_prefill / or_session_step (both step forms)
  *                                     an independent numpy float64 forward of the same graph (tiny model shape)
+ *   or_session_get_kv / set_kv        round trip, and the rows a prefill stores against the forward's f16 K / V
  *   or_pixel_lut / or_patchify, or_rope2d_table / or_rope2d, or_unfold2x2, or_gelu, or_rms_norm_h, or_matmul_f16,
  *   or_ffn_f16, or_attention_coop, or_vision_encode, or_vision_encode_w16
  *                                     numpy restatements (fp64 closed forms, ggml's rope cache by its own recurrence,
@@ -85,6 +87,10 @@ void or_qkv_post(float *qkv, const float *qn, const float *kn, const float *cs, 
  * q [n_head·128] f32, K / V f16 rows [key][n_kv·128] (row stride kv_stride halves), out [n_head·128] */
 void or_attn_decode(const float *q, const uint16_t *k, const uint16_t *v, size_t kv_stride, int n_keys, int n_head,
                     int n_kv, float scale, float *out);
+/* the F32 path's decode attention (attn_scores / attn_softmax / attn_values, text.rs:567-569): the score scaled after
+ * its dot product, the softmax normalised before the values; same arguments as or_attn_decode */
+void or_attn_decode_f32(const float *q, const uint16_t *k, const uint16_t *v, size_t kv_stride, int n_keys, int n_head,
+                        int n_kv, float scale, float *out);
 /* causal prefill attention attention_causal.wgsl:42-93 (tiles of 8 keys, online softmax): queries t < n_q at
  * positions pos0 + t, q / out [n_q][n_head·128] */
 void or_attn_causal(const float *q, const uint16_t *k, const uint16_t *v, size_t kv_stride, int n_q, int pos0,
@@ -135,8 +141,15 @@ void or_session_set_f16(or_session *s, int on);
 /* Batch::matmul with a q8_0 weight (gpu.rs:1963-2014): Y[m][n] (+)= X·Wᵀ, W as q8_0 blocks [n][k]; r16: the f16
  * paths' rounding of X and W */
 void or_matmul_q8_0(const float *x, const uint8_t *w, float *y, size_t m, size_t n, size_t k, int acc, int r16);
-/* record_step (text.rs:540-578) on the f16 paths: embed + layers_fused (text.rs:630-647) + dmv_norm LM head */
+/* record_step (text.rs:540-578) on the f16 paths: embed + layers_fused (text.rs:630-647) + dmv_norm LM head; with
+ * or_session_set_step_f32 the F32 path's step (text.rs:555-576: rms_norm, matvec_q8_0 per projection, rope_neox,
+ * kv_store, the three-kernel attention or_attn_decode_f32, swiglu; head rms_norm + matvec_q8_0) */
 int or_session_step(or_session *s, int32_t tok, float *logits);
+void or_session_set_step_f32(or_session *s, int on);
+/* cache rows [pos0, pos0 + n) of one layer in the reference's layout [pos][n_kv·128] f16, out of / into the session;
+ * −1 outside the session */
+int or_session_get_kv(const or_session *s, int layer, int pos0, int n, uint16_t *k, uint16_t *v);
+int or_session_set_kv(or_session *s, int layer, int pos0, int n, const uint16_t *k, const uint16_t *v);
 /* rewind to n_past positions (the rows beyond are overwritten by later steps) */
 void or_session_rewind(or_session *s, int n_past);
 

@@ -53,6 +53,10 @@ def lib() -> C.CDLL:
             "or_session_step": (i32, [vp, C.c_int32, vp]),
             "or_session_rewind": (None, [vp, i32]),
             "or_session_set_f16": (None, [vp, i32]),
+            "or_session_set_step_f32": (None, [vp, i32]),
+            "or_session_get_kv": (i32, [vp, i32, i32, i32, vp, vp]),
+            "or_session_set_kv": (i32, [vp, i32, i32, i32, vp, vp]),
+            "or_attn_decode_f32": (None, [vp, vp, vp, sz, i32, i32, i32, f32, vp]),
             "or_matmul_q8_0": (None, [vp, vp, vp, sz, sz, sz, i32, i32]),
             "or_pixel_lut": (None, [vp, vp, vp]),
             "or_patchify": (None, [vp, i32, i32, i32, i32, vp, vp]),
@@ -196,6 +200,14 @@ def attn_decode(q, k, v, kv_stride, n_keys, n_head, n_kv, scale) -> np.ndarray:
     return out
 
 
+def attn_decode_f32(q, k, v, kv_stride, n_keys, n_head, n_kv, scale) -> np.ndarray:
+    """the F32 path's three-kernel decode attention (attn_scores / attn_softmax / attn_values)"""
+    out = np.empty(n_head * 128, np.float32)
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_attn_decode_f32(_p(q), _p(k), _p(v), kv_stride, n_keys, n_head, n_kv, scale, _p(out))
+    return out
+
+
 def attn_causal(q, k, v, kv_stride, n_q, pos0, n_head, n_kv, scale) -> np.ndarray:
     out = np.empty(n_q * n_head * 128, np.float32)
     q = np.ascontiguousarray(q, np.float32)
@@ -255,11 +267,15 @@ class LayerC(C.Structure):
 
 
 class Session:
-    """The decoder restated (text.rs:437-658): prefill on the F32 path's kernels, steps on the fused f16-path kernels.
-    The weights are the same host tensors the library gets (dicts of q8_0 block bytes / f32 norms)."""
+    """The decoder restated (text.rs:437-658) on one compute path: the F32 path (exact q8_0 values in the prefill
+    GEMMs, the F32 step of text.rs:555-576) or, with f16, the f16 paths (X and q·d rounded to f16 in the prefill GEMMs,
+    the fused step of layers_fused). The weights are the same host tensors the library gets (dicts of q8_0 block
+    bytes / f32 norms)."""
 
-    def __init__(self, cfg: dict, tok_embd, output_norm, layers: list[dict], n_ctx: int, f16: bool = False):
-        """f16: the prefill GEMMs on the f16 paths' rounding (X and q·d rounded to f16, f32 sums)"""
+    def __init__(self, cfg: dict, tok_embd, output_norm, layers: list[dict], n_ctx: int, f16: bool = False,
+                 step_f32: bool | None = None):
+        """f16: the f16 paths' prefill rounding and fused step; step_f32 overrides the step's form (default: the F32
+        path's step exactly when f16 is off)"""
         self._keep = [tok_embd, output_norm, layers]
         self.cfg = cfg
         c = TextCfg(cfg["n_layer"], cfg["dim"], cfg["n_head"], cfg["n_kv"], 128, cfg["n_ff"], cfg["n_vocab"],
@@ -273,6 +289,8 @@ class Session:
         if not self.h:
             raise ValueError("oracle session: unsupported shape")
         lib().or_session_set_f16(self.h, int(f16))
+        lib().or_session_set_step_f32(self.h, int(not f16 if step_f32 is None else step_f32))
+        self.n_ctx = n_ctx
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -298,6 +316,23 @@ class Session:
         if lib().or_session_step(self.h, int(tok), _p(out)) != 0:
             raise ValueError("oracle step: bad id or overflow")
         return out
+
+    def get_kv(self, layer: int, pos0: int, n: int) -> tuple[np.ndarray, np.ndarray]:
+        """cache rows [pos0, pos0 + n) of a layer as f16 bits [n][n_kv·128] (K, V)"""
+        kvd = self.cfg["n_kv"] * 128
+        k = np.empty((n, kvd), np.uint16)
+        v = np.empty((n, kvd), np.uint16)
+        if lib().or_session_get_kv(self.h, layer, pos0, n, _p(k), _p(v)) != 0:
+            raise ValueError("oracle get_kv: outside the session")
+        return k, v
+
+    def set_kv(self, layer: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
+        """cache rows [pos0, pos0 + n) of a layer from f16 bits [n][n_kv·128]"""
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        n = k.shape[0]
+        if lib().or_session_set_kv(self.h, layer, pos0, n, _p(k), _p(v)) != 0:
+            raise ValueError("oracle set_kv: outside the session")
 
 
 # ---- the vision encoder (htr_vision_oracle.c) ----------------------------------------------------------------------

@@ -62,25 +62,11 @@ def test_choose_penalty_is_ieee_exact(dev):
 
 
 def config1_inputs(seed: int, rows: int, n_vocab: int = 151936, window: int = 64):
-    """151936 logits N(0, 3) + 8 planted equal maxima (3 of them on window ids, so the penalty reverses them),
-    history = 64 ids uniform over the vocabulary with 25 % repeats"""
-    logits = np.empty((rows, n_vocab), np.float32)
-    hist = np.empty((rows, window), np.int32)
-    for r in range(rows):
-        l = htr.synth_normal(seed * 100003 + r, n_vocab, 0.0, 3.0)
-        u = htr.synth_normal(seed * 100003 + r + 7 * rows + 11, 3 * window, 0.0, 1.0)
-        frac = (u - np.floor(u)).astype(np.float64)
-        fresh = (np.abs(u[:window]) * 1e6).astype(np.int64) % n_vocab
-        h = fresh.copy()
-        rep = np.arange(window)[frac[window:2 * window] < 0.25]
-        for j in rep[rep > 0]:
-            h[j] = h[int(frac[2 * window + j] * j)]
-        planted = (np.abs(u[2 * window - 8:2 * window]) * 7e5).astype(np.int64) % n_vocab
-        planted[:3] = h[[1, 17, 40]]
-        l[planted] = l.max() + np.float32(1.0)
-        logits[r] = l
-        hist[r] = h
-    return logits, hist
+    """the choice workload's generator (htr.synth.choice_inputs): N(0, 3) logits with 8 planted equal maxima, 3 of
+    them on window ids; 64 uniform history ids with 25 % repeats"""
+    from htr import synth
+
+    return synth.choice_inputs(seed, rows, n_vocab, window)
 
 
 def test_config1_choice_bit_exact(dev):

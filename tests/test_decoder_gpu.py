@@ -310,7 +310,8 @@ def test_f16_path_other_shapes_use_the_rounding_tiled_kernel(dev):
 
 def test_full_size_decoder_f16_path_matches_oracle(dev):
     """the full model shape on the f16 path: prefill logits against the oracle's f16-path prefill (bar 1e-2, the path's
-    sensitivity), then 16 greedy tokens teacher-forced against the oracle"""
+    sensitivity), then 16 greedy tokens teacher-forced against the oracle decoding from the same cache (the GPU's rows
+    handed over) and the GPU's prefill logits: the first choice is the oracle's choose on those logits"""
     cfg, te, on, layers = synth_text_model()
     m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)
     prompt = (np.abs(htr.synth_normal(78, 64)) * 1e5).astype(np.int64) % cfg["n_vocab"]
@@ -323,9 +324,15 @@ def test_full_size_decoder_f16_path_matches_oracle(dev):
     print(f"\n[full prefill f16] rel-L2 vs oracle {e:.2e}")
     assert e < 1e-2
     assert int(np.argmax(lg)) == int(np.argmax(lo)) or near_tie(lo, int(np.argmax(lo)), int(np.argmax(lg)))
+    for li in range(cfg["n_layer"]):
+        k, v = s.kv_rows(li, 0, prompt.size)
+        o.set_kv(li, 0, k, v)
     ch = s.choice(htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new), prompt, 8, 2)
     toks = s.decode_gpu(ch, n_new)
     assert len(toks) == n_new
+    ties = []
+    teacher_forced(o, lg, prompt, toks, 1.1, 64, ties)
+    print(f"[full decode f16] tokens {toks[:8]}…, near-ties {ties}")
     ch.free()
     s.free()
     m.free()

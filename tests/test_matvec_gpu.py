@@ -106,3 +106,115 @@ def test_matvec_many_equals_single(dev):
         htr.matvec_q8_0(dev, w, xb, yb)
         assert np.array_equal(got[i], yb.download(np.float32)), i
         w.free()
+
+
+def _dmv_full_name(dev, rows, k, mode):
+    """the instance launch_dmv picks for a decoder shape: one workgroup a CU, rows / (4·CUs) rows a wave"""
+    n_cu = dev.info()[1]
+    if rows % (4 * n_cu) or k % 1024 or rows // (4 * n_cu) > 4:
+        return None
+    return f"k_dmv_full<{rows // (4 * n_cu)},{k // 1024},{mode}>"
+
+
+def test_decode_qkv_instance(dev):
+    """the decode step's Q / K / V matvec as the 28-layer decoder runs it (text.rs:638, dmv_qkv.wgsl): q 2048, k 1024,
+    v 1024 rows × K 1024 with attn_norm fused — the k_dmv_full QKV instance (4 rows a wave on 256 CUs) — against the
+    oracle's restatement (≤ 1e-5, f32 in another order) and the fp64 closed form (≤ 1e-3); bars of text.rs:864-905"""
+    k, eps, qd, kvd = 1024, 1e-6, 2048, 1024
+    bq, bk, bv = (htr.synth_q8_0(300 + i, r, k) for i, r in enumerate((qd, kvd, kvd)))
+    x = htr.synth_normal(31, k, 0.0, 2.0)
+    nw = htr.synth_normal(32, k, 1.0, 0.02)
+    ws = [htr.Weight(dev, b, r, k) for b, r in ((bq, qd), (bk, kvd), (bv, kvd))]
+    y = dev.alloc((qd + 2 * kvd) * 4)
+    htr.matvec_qkv(dev, *ws, dev.upload(x), dev.upload(nw), eps, y)
+    want_name = _dmv_full_name(dev, qd + 2 * kvd, k, "qkv")
+    if want_name:
+        assert dev.last_kernel() == want_name
+    got = y.download(np.float32)
+    assert rel_l2(got, orc.dmv_qkv(bq, bk, bv, qd, kvd, k, x, nw, eps)) < 1e-5
+    xn = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps) * nw
+    want = np.concatenate([_np_deq(b, r, k) @ xn for b, r in ((bq, qd), (bk, kvd), (bv, kvd))])
+    assert rel_l2(got, want) < 1e-3
+    for part, (lo, hi) in (("q", (0, qd)), ("k", (qd, qd + kvd)), ("v", (qd + kvd, qd + 2 * kvd))):
+        assert rel_l2(got[lo:hi], want[lo:hi]) < 1e-3, part
+    for w in ws:
+        w.free()
+
+
+def test_decode_ffn_instance(dev):
+    """the decode step's gate / up matvec with ffn_norm and SwiGLU fused (text.rs:643, dmv_ffn.wgsl): 3072 × 1024 each,
+    the k_dmv_full FFN instance (3 rows a wave on 256 CUs), against the oracle (≤ 1e-5) and fp64 silu(g)·u (≤ 1e-3)"""
+    rows, k, eps = 3072, 1024, 1e-6
+    bg, bu = htr.synth_q8_0(310, rows, k), htr.synth_q8_0(311, rows, k)
+    x = htr.synth_normal(33, k, 0.0, 2.0)
+    nw = htr.synth_normal(34, k, 1.0, 0.02)
+    wg, wu = htr.Weight(dev, bg, rows, k), htr.Weight(dev, bu, rows, k)
+    y = dev.alloc(rows * 4)
+    htr.matvec_ffn(dev, wg, wu, dev.upload(x), dev.upload(nw), eps, y)
+    want_name = _dmv_full_name(dev, rows, k, "ffn")
+    if want_name:
+        assert dev.last_kernel() == want_name
+    got = y.download(np.float32)
+    assert rel_l2(got, orc.dmv_ffn(bg, bu, rows, k, x, nw, eps)) < 1e-5
+    xn = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps) * nw
+    g, u = _np_deq(bg, rows, k) @ xn, _np_deq(bu, rows, k) @ xn
+    assert rel_l2(got, g / (1 + np.exp(-g)) * u) < 1e-3
+    wg.free()
+    wu.free()
+
+
+@pytest.mark.parametrize("rows,k,name", [(1024, 2048, "o"), (1024, 3072, "down")])
+def test_decode_residual_instances(dev, rows, k, name):
+    """the decode step's o and down projections, accumulating onto the residual (text.rs:642, 644: dmv with acc = 1):
+    the k_dmv_full plain instance (1 row a wave on 256 CUs), y + W·x against the oracle (≤ 1e-5) and fp64 (≤ 1e-3)"""
+    blocks = htr.synth_q8_0(320 + k, rows, k)
+    x = htr.synth_normal(35 + k, k)
+    base = htr.synth_normal(36 + k, rows, 0.0, 4.0)
+    w = htr.Weight(dev, blocks, rows, k)
+    yb = dev.upload(base)
+    htr.matvec_q8_0(dev, w, dev.upload(x), yb, acc=True)
+    want_name = _dmv_full_name(dev, rows, k, "plain")
+    if want_name:
+        assert dev.last_kernel() == want_name
+    got = yb.download(np.float32)
+    assert rel_l2(got, orc.dmv(blocks, rows, k, x, None, 0.0, base, True)) < 1e-5, name
+    want = base.astype(np.float64) + _np_deq(blocks, rows, k) @ x.astype(np.float64)
+    assert rel_l2(got, want) < 1e-3, name
+    # the product alone, the accumulated part taken back off
+    assert rel_l2(got - base, want - base) < 1e-3, name
+    w.free()
+
+
+def test_graph_capture_replays_the_same_matvecs(dev):
+    """htr_capture_begin / end: 8 matvecs over 4 weights recorded once, replayed 3 times with eager work and host
+    reads between the replays; every replay equals the eager result bit for bit. A call that would allocate or wait
+    fails while recording, and the device stays usable."""
+    rows, k = 3072, 1024
+    ws = [htr.Weight(dev, htr.synth_q8_0(400 + i, rows, k), rows, k) for i in range(4)]
+    xb = dev.upload(htr.synth_normal(41, k))
+    ys = [dev.alloc(rows * 4) for _ in range(8)]
+    for i, y in enumerate(ys):
+        htr.matvec_q8_0(dev, ws[i % 4], xb, y)
+    eager = [y.download(np.float32) for y in ys]
+    poison = np.full(rows, np.nan, np.float32)
+    for y in ys:
+        y.upload(poison)
+    dev.capture_begin()
+    for i, y in enumerate(ys):
+        htr.matvec_q8_0(dev, ws[i % 4], xb, y)
+    with pytest.raises(htr.HtrError, match="captured"):
+        dev.sync()
+    with pytest.raises(htr.HtrError, match="captured"):
+        dev.alloc(64)
+    g = dev.capture_end()
+    for rep in range(3):
+        for y in ys:  # eager work between the replays: poison the outputs
+            y.upload(poison)
+        g.launch()
+        dev.sync()
+        for i, y in enumerate(ys):
+            assert np.array_equal(y.download(np.float32), eager[i]), (rep, i)
+    g.free()
+    dev.alive()
+    for w in ws:
+        w.free()

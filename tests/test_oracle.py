@@ -220,6 +220,23 @@ def test_decode_attention_matches_fp64():
     assert rel_l2(orc.attn_f64(q, k, v, n_kv * 128, n, n_head, n_kv, sc), want.ravel()) < 1e-12
 
 
+@pytest.mark.parametrize("n_head,n_kv,n", [(4, 2, 300), (16, 8, 600), (2, 1, 1)])
+def test_decode_attention_f32_path_matches_fp64(n_head, n_kv, n):
+    """the F32 path's three-kernel decode attention (attn_scores / attn_softmax / attn_values, text.rs:567-569) at the
+    reference's bar (rel-L2 < 1e-5, text.rs:1290-1291): key counts over one and several of attn_softmax's 256-lane
+    strides and attn_values' 8-lane strides, GQA groups of 2; and within f32 rounding of the split-K form"""
+    g = orc.Lcg(41 + n)
+    k, v = _kv(g, n, n_kv)
+    q = g.f32(n_head * 128, 2.0)
+    sc = np.float32(1 / np.sqrt(128))
+    want = np_attention(q.reshape(n_head, 128).astype(np.float64),
+                        k.view(np.float16).astype(np.float64).reshape(n, n_kv, 128),
+                        v.view(np.float16).astype(np.float64).reshape(n, n_kv, 128), float(sc))
+    got = orc.attn_decode_f32(q, k, v, n_kv * 128, n, n_head, n_kv, sc)
+    assert rel_l2(got, want.ravel()) < 1e-5
+    assert rel_l2(got, orc.attn_decode(q, k, v, n_kv * 128, n, n_head, n_kv, sc)) < 1e-6
+
+
 def test_causal_attention_matches_fp64():
     """text.rs:797-830: a batch of 70 queries at pos0 = 9 over the f16 cache, 1e-4 abs"""
     n_head, n_kv, pos0, n_q = 4, 2, 9, 70
@@ -360,14 +377,16 @@ def np_forward(cfg, tok_embd, output_norm, layers, ids, r16=False):
     return np_rms(x, output_norm, eps) @ E.T
 
 
-def test_oracle_decoder_matches_fp64_forward():
-    """the oracle's prefill (F32-path kernels) and steps (fused f16-path kernels) against the independent fp64 forward
-    on the reference's tiny model (text.rs:1297-1323) and its 20-token prompt"""
+@pytest.mark.parametrize("step_f32", [True, False])
+def test_oracle_decoder_matches_fp64_forward(step_f32):
+    """the oracle's prefill (F32-path kernels) and steps — the F32 path's step (text.rs:555-576) and the fused step of
+    the f16 paths (layers_fused, text.rs:630-647) — against the independent fp64 forward on the reference's tiny model
+    (text.rs:1297-1323) and its 20-token prompt"""
     cfg, te, on, layers = tiny_text_model()
     prompt = tiny_prompt()
     extra = [int(t) for t in orc.Lcg(9).bits(6) % cfg["n_vocab"]]
     want = np_forward(cfg, te, on, layers, list(prompt) + extra)
-    s = orc.Session(cfg, te, on, layers, 64)
+    s = orc.Session(cfg, te, on, layers, 64, step_f32=step_f32)
     got = [s.prefill(prompt)]
     for t in extra:
         got.append(s.step(t))
@@ -422,3 +441,48 @@ def test_oracle_step_equals_prefill_row():
     assert rel_l2(la, lb) < 1e-5
     with pytest.raises(ValueError):
         b.step(cfg["n_vocab"])
+
+
+def test_oracle_step_forms_agree_and_kv_rows_round_trip():
+    """the F32 path's step and the fused step are the same function in two f32 orders: rel-L2 ≤ 5e-5 over 6 steps
+    (measured 0.5–1.6e-5 — each step stores its K / V row in f16, where the two orders' last bits now and then round
+    to neighbouring f16 values, 2^-11 apart; the prompt's rows are the same in both);
+    cache rows handed from one session to another (get_kv → set_kv) make the receiver step exactly as the giver; the
+    rows a prefill stores for layer 0 are the f16 of the closed-form K / V (per-head RMS norm + RoPE NEOX of
+    rms_norm(embed)·Wkᵀ; V = rms_norm(embed)·Wvᵀ) within one f16 rounding"""
+    cfg, te, on, layers = tiny_text_model()
+    prompt = tiny_prompt()
+    extra = [int(t) for t in orc.Lcg(9).bits(6) % cfg["n_vocab"]]
+    a = orc.Session(cfg, te, on, layers, 64, step_f32=True)
+    b = orc.Session(cfg, te, on, layers, 64, step_f32=False)
+    a.prefill(prompt)
+    b.prefill(prompt)
+    for t in extra:
+        assert rel_l2(a.step(t), b.step(t)) < 5e-5
+    # the hand-over: a third session gets a's rows and steps bit-identically with a
+    c = orc.Session(cfg, te, on, layers, 64, step_f32=True)
+    n = a.n_past
+    for li in range(cfg["n_layer"]):
+        k, v = a.get_kv(li, 0, n)
+        c.set_kv(li, 0, k, v)
+        k2, v2 = c.get_kv(li, 0, n)
+        assert np.array_equal(k, k2) and np.array_equal(v, v2)
+    c.rewind(n)
+    assert np.array_equal(a.step(7), c.step(7))
+    with pytest.raises(ValueError):
+        c.get_kv(cfg["n_layer"], 0, 1)
+    with pytest.raises(ValueError):
+        c.get_kv(0, 60, 5)
+    # layer 0's rows against the closed form
+    d, nkv = cfg["dim"], cfg["n_kv"]
+    E = np_dequant(te, cfg["n_vocab"], d)
+    x = E[np.asarray(prompt)]
+    h = np_rms(x, layers[0]["attn_norm"], cfg["eps"])
+    kr = (h @ np_dequant(layers[0]["k"], nkv * 128, d).T).reshape(len(prompt), nkv, 128)
+    vr = (h @ np_dequant(layers[0]["v"], nkv * 128, d).T).reshape(len(prompt), nkv * 128)
+    kw = np.stack([np_rope(np_rms(kr[t], layers[0]["k_norm"], cfg["eps"]), t) for t in range(len(prompt))])
+    k0, v0 = a.get_kv(0, 0, len(prompt))
+    kf = k0.view(np.float16).astype(np.float64).reshape(len(prompt), nkv, 128)
+    vf = v0.view(np.float16).astype(np.float64)
+    assert np.all(np.abs(kf - kw) <= 1e-3 * (1 + np.abs(kw)))
+    assert np.all(np.abs(vf - vr) <= 1e-3 * (1 + np.abs(vr)))
