@@ -7,12 +7,19 @@ HIP graphs. Each step rewinds the session to 1023 positions, runs one decode ste
 decodes 512 tokens (so every step is the same read).
 
 Also measured in the same run (one JSON line):
-  roofline      the q8_0 matvec kernel at the 3072 × 1024 projection (W [3072 × 1024], x f32[1024], y f32[3072]) over a rotation
-                of 128 distinct W copies (428 MB > the 256 MB Infinity Cache), 128 matvecs per launch; algorithmic
-                bytes 3,358,720 per matvec; HIP events on the library's stream
-  matvec        the same kernel one matvec per launch over the rotation (and the 64-copy figure)
-  choose        windowed penalty + argmax over 151936 logits, 10k seeded steps over 512 rotating buffers
-  attention     GQA decode attention (16 q / 8 kv heads × 128) at 512 / 2048 / 8192 keys over ≥ 256 MB of rotating caches
+  roofline      the q8_0 matvec kernel's streaming rate at the 3072 × 1024 projection (W [3072 × 1024], x f32[1024],
+                y f32[3072]) over a rotation of 128 distinct W copies (428 MB > the 256 MB Infinity Cache), 128 matvecs
+                per launch; algorithmic bytes 3,358,720 per matvec; HIP events on the library's stream
+  roofline_by_config
+                every workload's fraction of its roofline: the decode (bytes per token × tokens/s), one matvec per
+                graph node over the rotation, the choice per step (graphed) and 512 rows batched, the attention at
+                512 / 2048 / 8192 keys (graphed over ≥ 512 MiB of caches), the vision GEMMs (MFMA)
+  decode.phases the decode step's kernel classes timed alone in graphs (htr_session_profile_step) at the read's mean
+                context
+  matvec        the same kernel one matvec per launch / per graph node over the rotation (and the 64-copy figure)
+  choose        windowed penalty + argmax over 151936 logits: 10k seeded steps over 512 rows of the choice workload
+                (planted maxima, 25 % repeated window ids), launched one by one and replayed as graphs; all rows batched
+  attention     GQA decode attention (16 q / 8 kv heads × 128) at 512 / 2048 / 8192 keys over ≥ 512 MiB of rotating caches
   cpu_baseline  the oracle (oracle/, a C restatement of the reference path, OpenMP) decoding on the host cores
 """
 from __future__ import annotations
@@ -32,6 +39,17 @@ import htr  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MATVEC_UNIT_BYTES = 3072 * 1024 + 3072 * 32 * 2 + 1024 * 4 + 3072 * 4  # W quants + scales + x + y = 3,358,720
+CHOOSE_STEP_BYTES = 151936 * 4 + 64 * 4  # the logits read once + the window's ids
+# one decode token of the 28-layer model at n_keys keys: the q8_0 weights (quants + scales, the tied LM head included),
+# the norm weights, the K / V rows of every layer read and the new one written, the logits written and read back
+DECODE_WEIGHT_BYTES = 633_233_408
+DECODE_NORM_BYTES = 262_144
+KV_BYTES_PER_KEY = 28 * 2 * 8 * 128 * 2  # 114,688
+LOGIT_BYTES = 2 * 151936 * 4
+
+
+def decode_bytes_per_token(mean_keys: float) -> float:
+    return DECODE_WEIGHT_BYTES + DECODE_NORM_BYTES + KV_BYTES_PER_KEY * (mean_keys + 1) + LOGIT_BYTES
 
 
 def log(msg: str) -> None:
@@ -103,9 +121,20 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     dt = time.perf_counter() - t0
     same = all(r == reads[0] for r in reads) and (ref is None or ref == reads[0])
     log(f"decode: {steps} reads × {n_new} tokens in {dt:.3f} s, identical reads: {same}")
+    # the read's steps run at 1024 … 1535 keys (mean 1279.5)
+    mean_keys = (prompt_len + prompt_len + n_new - 1) / 2
+    bpt = decode_bytes_per_token(mean_keys)
+    tok_s = steps * n_new / dt
+    phases = decode_phases(s, prompt_len - 1 + n_new // 2, cfg["n_layer"])
     prefill_f32_s = prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s
     out = {
-        "tok_s": steps * n_new / dt,
+        "tok_s": tok_s,
+        "bytes_per_token": bpt,
+        "mean_keys": mean_keys,
+        "achieved_GBs": bpt * tok_s / 1e9,
+        "frac": bpt * tok_s / 1e9 / HBM_PEAK_GBS,
+        "roofline_tok_s": HBM_PEAK_GBS * 1e9 / bpt,
+        "phases": phases,
         "ms_per_read": dt / steps * 1e3,
         "ms_per_token": dt / (steps * n_new) * 1e3,
         "prefill_ms": prefill_s * 1e3,
@@ -116,6 +145,44 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
         "first_tokens": reads[0][:8],
     }
     return out, (cfg, te, on, layers, prompt), (m, s, ch)
+
+
+def decode_phases(s, pos, n_layer, n_steps=16, reps=20):
+    """the decode step's kernel classes each alone in a graph of n_steps steps at position pos (the read's mean
+    context), and all of them together: µs per step and per layer"""
+    s.rewind(pos)
+    classes = [("embed", htr.STEP_EMBED), ("qkv_matvec", htr.STEP_QKV), ("attention", htr.STEP_ATTENTION),
+               ("o_matvec", htr.STEP_O), ("gate_up_matvec", htr.STEP_FFN), ("down_matvec", htr.STEP_DOWN),
+               ("lm_head", htr.STEP_HEAD), ("step", htr.STEP_ALL)]
+    out = {"position": pos, "keys": pos + 1, "steps_per_graph": n_steps}
+    for name, c in classes:
+        us = s.profile_step(c, n_steps, reps) * 1e3
+        per_layer = c not in (htr.STEP_EMBED, htr.STEP_HEAD, htr.STEP_ALL)
+        out[name + "_us"] = us
+        if per_layer:
+            out[name + "_us_per_layer"] = us / n_layer
+    out["sum_of_classes_us"] = sum(out[n + "_us"] for n, c in classes if c != htr.STEP_ALL)
+    log("decode phases (µs a step, in graphs): " + ", ".join(f"{n} {out[n + '_us']:.1f}" for n, _ in classes))
+    return out
+
+
+def graphed(dev, calls, reps):
+    """µs per call of `calls` (a list of zero-argument functions, each one library entry point) recorded once into a
+    graph and replayed reps times after one untimed replay"""
+    dev.capture_begin()
+    try:
+        for f in calls:
+            f()
+    finally:
+        g = dev.capture_end()
+    g.launch()
+    dev.sync()
+    dev.timer_begin()
+    for _ in range(reps):
+        g.launch()
+    ms = dev.timer_end()
+    g.free()
+    return ms * 1e3 / (reps * len(calls))
 
 
 def bench_matvec(dev, copies=128, reps=10):
@@ -146,6 +213,11 @@ def bench_matvec(dev, copies=128, reps=10):
         ms = dev.timer_end()
         res[f"single_launch_{n_rot}_copies_us"] = ms / n_l * 1e3
         res[f"single_launch_{n_rot}_copies_GBs"] = MATVEC_UNIT_BYTES / (ms / n_l * 1e-3) / 1e9
+        # one matvec per graph node (no host launch between them): the kernel's time with its node overhead
+        us = graphed(dev, [lambda w=w: htr.matvec_q8_0(dev, w, x, ys) for w in ws[:n_rot]], 4)
+        res[f"graph_node_{n_rot}_copies_us"] = us
+        res[f"graph_node_{n_rot}_copies_GBs"] = MATVEC_UNIT_BYTES / (us * 1e-6) / 1e9
+        res[f"graph_node_{n_rot}_copies_frac"] = res[f"graph_node_{n_rot}_copies_GBs"] / HBM_PEAK_GBS
     # all copies in one launch
     htr.matvec_q8_0_many(dev, ws, x, y)
     dev.timer_begin()
@@ -158,80 +230,108 @@ def bench_matvec(dev, copies=128, reps=10):
     res["batched_bytes_per_launch"] = bytes_launch
     for w in ws:
         w.free()
-    log(f"matvec: batched {res['batched_launch_GBs']:.0f} GB/s, single {res[f'single_launch_{copies}_copies_GBs']:.0f} GB/s")
+    res["batched_frac"] = res["batched_launch_GBs"] / HBM_PEAK_GBS
+    log(f"matvec: batched {res['batched_launch_GBs']:.0f} GB/s, single {res[f'single_launch_{copies}_copies_GBs']:.0f} "
+        f"GB/s launched, {res[f'graph_node_{copies}_copies_GBs']:.0f} GB/s as graph nodes "
+        f"({res[f'graph_node_{copies}_copies_us']:.2f} us)")
     return res
 
 
 def bench_choose(dev, n_steps=10000, n_buf=512, n_vocab=151936, window=64):
-    log(f"choose: {n_steps} steps over {n_buf} logits buffers")
+    """the choice workload (htr.synth.choice_inputs: N(0, 3) logits with 8 planted equal maxima, 3 on window ids; 64
+    uniform window ids with 25 % repeats) in 512 rows, 311 MB of logits: 10k single steps over the rows launched one by
+    one, the same replayed as graphs of 512 steps, and all rows in one launch"""
+    from htr import synth
+
+    log(f"choose: {n_steps} steps over {n_buf} rows of the choice workload")
     logits = dev.alloc(n_buf * n_vocab * 4)
-    # rows of N(0, 3) generated on the host once per buffer group
-    block = 16
+    hist_h = np.zeros((n_buf, window + 1), np.uint32)
+    block = 32
     for i in range(0, n_buf, block):
-        a = htr.synth_normal(5000 + i, block * n_vocab, 0.0, 3.0)
-        htr.lib().htr_upload(dev.h, logits.ptr + i * n_vocab * 4, a.ctypes.data, a.nbytes)
-    ids = (np.abs(htr.synth_normal(77, window)) * 1e5).astype(np.int64) % n_vocab
-    hist = dev.upload(np.concatenate([ids, np.zeros(8, np.int64)]).astype(np.uint32))
+        lg, h = synth.choice_inputs(7000 + i, block, n_vocab, window)
+        htr.lib().htr_upload(dev.h, logits.ptr + i * n_vocab * 4, lg.ctypes.data, lg.nbytes)
+        hist_h[i:i + block, :window] = h
+    hist = dev.upload(hist_h)
     tok = dev.alloc(4)
     L = htr.lib()
+    stride = (window + 1) * 4
+
+    def one(i):
+        rc = L.htr_choose(dev.h, logits.ptr + (i % n_buf) * n_vocab * 4, n_vocab, hist.ptr + (i % n_buf) * stride,
+                          window, window, 1.1, 0.0, None, None, tok.ptr)
+        if rc < 0:
+            raise htr.HtrError(htr.last_error())
+
     for i in range(16):
-        L.htr_choose(dev.h, logits.ptr + (i % n_buf) * n_vocab * 4, n_vocab, hist.ptr, window, window, 1.1, 0.0, None,
-                     None, tok.ptr)
+        one(i)
     dev.sync()
     dev.timer_begin()
     for i in range(n_steps):
-        rc = L.htr_choose(dev.h, logits.ptr + (i % n_buf) * n_vocab * 4, n_vocab, hist.ptr, window, window, 1.1, 0.0,
-                          None, None, tok.ptr)
-        if rc < 0:
-            raise htr.HtrError(htr.last_error())
+        one(i)
     ms = dev.timer_end()
-    step_bytes = n_vocab * 4 + window * 4
-    res = {"steps": n_steps, "us_per_step": ms / n_steps * 1e3, "GBs": step_bytes / (ms / n_steps * 1e-3) / 1e9}
-    # the same 512 rows in one launch (independent rows, one history each)
-    rows = n_buf
-    hist_rows = dev.alloc(rows * (window + 1) * 4)
-    toks = dev.alloc(rows * 4)
-    htr.choose_many(dev, logits, n_vocab, rows, hist_rows, window + 1, window, window, 1.1, toks)
+    res = {"steps": n_steps, "us_per_step": ms / n_steps * 1e3,
+           "GBs": CHOOSE_STEP_BYTES / (ms / n_steps * 1e-3) / 1e9}
+    us = graphed(dev, [lambda i=i: one(i) for i in range(n_buf)], max(1, n_steps // n_buf))
+    res["graph_node_us_per_step"] = us
+    res["graph_node_GBs"] = CHOOSE_STEP_BYTES / (us * 1e-6) / 1e9
+    res["graph_node_frac"] = res["graph_node_GBs"] / HBM_PEAK_GBS
+    # the 512 rows in one launch (independent rows, each with its own window)
+    toks = dev.alloc(n_buf * 4)
+    htr.choose_many(dev, logits, n_vocab, n_buf, hist, window + 1, window, window, 1.1, toks)
     dev.timer_begin()
     for _ in range(5):
-        htr.choose_many(dev, logits, n_vocab, rows, hist_rows, window + 1, window, window, 1.1, toks)
+        htr.choose_many(dev, logits, n_vocab, n_buf, hist, window + 1, window, window, 1.1, toks)
     ms = dev.timer_end() / 5
-    res["batched_rows_per_launch"] = rows
-    res["batched_us_per_row"] = ms / rows * 1e3
-    res["batched_GBs"] = rows * step_bytes / (ms * 1e-3) / 1e9
-    logits.free()
-    log(f"choose: {res['us_per_step']:.2f} us/step, batched {res['batched_GBs']:.0f} GB/s")
+    res["batched_rows_per_launch"] = n_buf
+    res["batched_us_per_row"] = ms / n_buf * 1e3
+    res["batched_GBs"] = n_buf * CHOOSE_STEP_BYTES / (ms * 1e-3) / 1e9
+    res["batched_frac"] = res["batched_GBs"] / HBM_PEAK_GBS
+    for b in (logits, hist, tok, toks):
+        b.free()
+    log(f"choose: {res['us_per_step']:.2f} us/step launched, {us:.2f} us as graph nodes, batched "
+        f"{res['batched_GBs']:.0f} GB/s")
     return res
 
 
-def bench_attention(dev, n_head=16, n_kv=8):
+def bench_attention(dev, n_head=16, n_kv=8, rotate_mib=512):
+    """GQA decode attention at 512 / 2048 / 8192 keys, each call on another copy of the caches (≥ 512 MiB of them, past
+    the 256 MB Infinity Cache): launched one by one and replayed as graphs"""
     res = {}
     q = dev.upload(htr.synth_normal(31, n_head * 128))
     out = dev.alloc(n_head * 128 * 4)
+    L_ = htr.lib()
+    sc = float(np.float32(1 / np.sqrt(128)))
     for L in (512, 2048, 8192):
         per = 2 * n_kv * L * 128 * 2
-        copies = max(8, -(-256 * 2 ** 20 // per))
+        copies = max(8, -(-rotate_mib * 2 ** 20 // per))
         kv = dev.alloc(copies * per)
         a = htr.synth_normal(L, 2 * n_kv * L * 128).astype(np.float16)
         for c in range(copies):
-            htr.lib().htr_upload(dev.h, kv.ptr + c * per, a.ctypes.data, a.nbytes)
-        L_ = htr.lib()
-        sc = float(np.float32(1 / np.sqrt(128)))
+            L_.htr_upload(dev.h, kv.ptr + c * per, a.ctypes.data, a.nbytes)
         half = per // 2
+
+        def one(c, L=L, kv=kv, per=per, half=half):
+            rc = L_.htr_decode_attention(dev.h, q.ptr, kv.ptr + c * per, kv.ptr + c * per + half, n_head, n_kv, L, L,
+                                         sc, out.ptr)
+            if rc < 0:
+                raise htr.HtrError(htr.last_error())
+
         for c in range(4):
-            L_.htr_decode_attention(dev.h, q.ptr, kv.ptr + c * per, kv.ptr + c * per + half, n_head, n_kv, L, L, sc,
-                                    out.ptr)
+            one(c)
         n = 4 * copies
         dev.timer_begin()
         for i in range(n):
-            c = i % copies
-            L_.htr_decode_attention(dev.h, q.ptr, kv.ptr + c * per, kv.ptr + c * per + half, n_head, n_kv, L, L, sc,
-                                    out.ptr)
+            one(i % copies)
         ms = dev.timer_end() / n
         byts = 4096 * L + 16384
-        res[str(L)] = {"us": ms * 1e3, "GBs": byts / (ms * 1e-3) / 1e9, "copies": copies}
+        us_g = graphed(dev, [lambda c=c: one(c) for c in range(copies)], max(1, 512 // copies))
+        res[str(L)] = {"us": ms * 1e3, "GBs": byts / (ms * 1e-3) / 1e9, "copies": copies,
+                       "rotation_MiB": copies * per / 2 ** 20, "graph_node_us": us_g,
+                       "graph_node_GBs": byts / (us_g * 1e-6) / 1e9,
+                       "graph_node_frac": byts / (us_g * 1e-6) / 1e9 / HBM_PEAK_GBS}
         kv.free()
-        log(f"attention L={L}: {ms * 1e3:.2f} us, {res[str(L)]['GBs']:.0f} GB/s")
+        log(f"attention L={L}: {ms * 1e3:.2f} us launched, {us_g:.2f} us as graph nodes, "
+            f"{res[str(L)]['graph_node_GBs']:.0f} GB/s")
     return res
 
 
@@ -384,7 +484,7 @@ def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
 
     cfg, te, on, layers, prompt = model_inputs
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    o = orc.Session(cfg, te, on, layers, prompt_n + max_new + 1)
+    o = orc.Session(cfg, te, on, layers, prompt_n + max_new + 1, f16=True)  # the measured path's fused step
     lo = o.prefill(prompt[:prompt_n])
     hist = [int(t) for t in prompt[:prompt_n]]
     t0 = time.perf_counter()
@@ -400,9 +500,42 @@ def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
     log(f"cpu baseline: matvec {per['matvec_w3072x1024']['GBs']:.1f} GB/s, choose {per['choose_151936']['us']:.0f} us, "
         f"attention 8192 keys {per['attention_8192']['us']:.0f} us")
     return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port", "per_config": per,
-            "sample": f"oracle (C restatement, OpenMP) greedy decode of {n} tokens (rp 1.1 / 64) of the same 28-layer q8_0 "
+            "sample": f"oracle (C restatement, OpenMP; the f16 paths' fused step) greedy decode of {n} tokens (rp 1.1 / 64) of the same 28-layer q8_0 "
                       f"model after a {prompt_n}-token prompt: attention context {prompt_n}-{prompt_n + n} keys, shorter "
                       f"than the workload's 1024-1536 (the 633 MB of weights per token dominate either way)"}
+
+
+def roofline_by_config(r: dict) -> dict:
+    """each workload's achieved rate as a fraction of the bound that caps it (HBM 8 TB/s; the vision GEMMs: dense f16
+    MFMA 2.5 PFLOP/s)"""
+    out = {}
+    if "decode" in r:
+        d = r["decode"]
+        out["config3_decode"] = {"bound": "hbm", "achieved_GBs": d["achieved_GBs"], "frac": d["frac"],
+                                 "unit": f"{d['bytes_per_token']:.0f} B a token at {d['mean_keys']} keys on average"}
+    if "matvec" in r:
+        m = r["matvec"]
+        out["config0_matvec_graph_node"] = {"bound": "hbm", "achieved_GBs": m["graph_node_128_copies_GBs"],
+                                            "frac": m["graph_node_128_copies_frac"],
+                                            "unit": "one W [3072 x 1024] matvec a graph node, 128 copies rotated"}
+        out["config0_matvec_batched"] = {"bound": "hbm", "achieved_GBs": m["batched_launch_GBs"],
+                                         "frac": m["batched_frac"],
+                                         "unit": "128 matvecs in one launch (the kernel's streaming rate)"}
+    if "choose" in r:
+        c = r["choose"]
+        out["config1_choice_graph_node"] = {"bound": "hbm", "achieved_GBs": c["graph_node_GBs"],
+                                            "frac": c["graph_node_frac"], "unit": "one step a graph node"}
+        out["config1_choice_batched"] = {"bound": "hbm", "achieved_GBs": c["batched_GBs"], "frac": c["batched_frac"],
+                                         "unit": "512 steps in one launch"}
+    if "attention" in r:
+        for L, a in r["attention"].items():
+            out[f"config2_attention_{L}"] = {"bound": "hbm", "achieved_GBs": a["graph_node_GBs"],
+                                             "frac": a["graph_node_frac"], "unit": "one call a graph node"}
+    if "vision_gemm" in r:
+        v = r["vision_gemm"]
+        out["config4_vision_gemm"] = {"bound": "mfma", "achieved_TFLOPs": v["tflops"], "frac": v["frac_mfma_peak"],
+                                      "unit": "a layer's six GEMMs at 12100 rows"}
+    return out
 
 
 def main():
@@ -457,7 +590,8 @@ def main():
                               "frac": ach / HBM_PEAK_GBS, "traffic": load_traffic(),
                               "kernel": "k_dmv_many: q8_0 matvec W[3072x1024] f32 x[1024] -> y[3072], 128 distinct W "
                                         "copies per launch (430 MB, past the 256 MB Infinity Cache); algorithmic "
-                                        "bytes 3,358,720 per matvec",
+                                        "bytes 3,358,720 per matvec. The matvec kernel's streaming rate: the decode "
+                                        "runs its matvecs one a graph node, see roofline_by_config",
                               "algorithmic_bytes_per_launch": mv["batched_bytes_per_launch"],
                               "avg_launch_us": mv["batched_launch_us"]}
     if want("choose"):
@@ -469,6 +603,7 @@ def main():
     if want("vision"):
         result["vision_gemm"] = bench_vision_gemm(dev)
         result["vision_encode"] = bench_vision_encode(dev)
+    result["roofline_by_config"] = roofline_by_config(result)
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)
     dev.close()

@@ -153,30 +153,37 @@ int record_step_f32(htr_session *s, hipStream_t st) {
 
 // one decode step on the session's stream: token s->tok at position state[0] → s->logits. The f16 paths' fused step
 // (record_step, text.rs:540-552 + layers_fused), or the F32 path's (record_step_f32) for a model of that path.
-int record_step(htr_session *s, hipStream_t st) {
+// `only` (the in-graph timing of htr_session_profile_step) records just the kernels of the HTR_STEP_* classes it
+// names; the decode records them all.
+int record_step(htr_session *s, hipStream_t st, unsigned only = HTR_STEP_ALL) {
     htr_text_model *m = s->m;
     htr_device *dev = s->dev;
     const htr_text_config &c = m->cfg;
     const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const float scale = 1.0f / sqrtf((float)HEAD);
-    HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
+    if (only & HTR_STEP_EMBED) HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
     if (m->compute == HTR_COMPUTE_F32) return record_step_f32(s, st);
     for (int li = 0; li < c.n_layer; li++) {
         const Layer &ly = m->layers[li];
         uint16_t *kc = s->kc + li * s->kv_layer, *vc = s->vc + li * s->kv_layer;
         DmvMat qkv[3] = {{ly.q->q, ly.q->d, qd}, {ly.k->q, ly.k->d, kvd}, {ly.v->q, ly.v->d, kvd}};
-        HTR_TRY(launch_dmv(dev, st, DMV_QKV, qkv, 3, c.dim, s->x, ly.attn_norm, c.eps, s->qkv, 0));
+        if (only & HTR_STEP_QKV)
+            HTR_TRY(launch_dmv(dev, st, DMV_QKV, qkv, 3, c.dim, s->x, ly.attn_norm, c.eps, s->qkv, 0));
         const AttnFuse fz{ly.q_norm, ly.k_norm, s->rope, c.eps, c.n_head, (_Float16 *)kc, (_Float16 *)vc};
-        HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale, s->asc,
-                                   s->attn, &fz));
+        if (only & HTR_STEP_ATTENTION)
+            HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale,
+                                       s->asc, s->attn, &fz));
         DmvMat o = {ly.o->q, ly.o->d, c.dim};
-        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
+        if (only & HTR_STEP_O) HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
         DmvMat gu[2] = {{ly.gate->q, ly.gate->d, c.n_ff}, {ly.up->q, ly.up->d, c.n_ff}};
-        HTR_TRY(launch_dmv(dev, st, DMV_FFN, gu, 2, c.dim, s->x, ly.ffn_norm, c.eps, s->g, 0));
+        if (only & HTR_STEP_FFN)
+            HTR_TRY(launch_dmv(dev, st, DMV_FFN, gu, 2, c.dim, s->x, ly.ffn_norm, c.eps, s->g, 0));
         DmvMat dn = {ly.down->q, ly.down->d, c.dim};
-        HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &dn, 1, c.n_ff, s->g, nullptr, 0.0f, s->x, 1));
+        if (only & HTR_STEP_DOWN)
+            HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &dn, 1, c.n_ff, s->g, nullptr, 0.0f, s->x, 1));
     }
     DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
+    if (!(only & HTR_STEP_HEAD)) return 0;
     return launch_dmv(dev, st, DMV_NORM, &head, 1, c.dim, s->x, m->output_norm, c.eps, s->logits, 0);
 }
 
@@ -643,6 +650,48 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
     if (rc == 0 && h_logits) rc = htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4);
     if (rc < 0) return rc;
     s->n_past += l;
+    return 0;
+}
+
+// the in-graph time of a decode step's kernel classes: n_steps steps at the session's position (nothing advances it:
+// every step re-runs at n_past, writing its KV row there) recorded as one graph with the kernels of `classes` only,
+// replayed reps times after one untimed replay
+extern "C" int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int reps, float *ms_per_step) {
+    if (!s || !ms_per_step) return htr_fail("htr_session_profile_step: null argument");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_session_profile_step"));
+    if (n_steps < 1 || n_steps > 256 || reps < 1 || (classes & ~(unsigned)HTR_STEP_ALL) || !classes)
+        return htr_fail("htr_session_profile_step: %d steps (1 … 256), %d replays, classes 0x%x", n_steps, reps, classes);
+    if (s->n_past < 1 || s->n_past >= s->n_ctx)
+        return htr_fail("htr_session_profile_step: the session is at %d of %d positions", s->n_past, s->n_ctx);
+    if (s->m->compute != HTR_COMPUTE_F16) return htr_fail("htr_session_profile_step: the f16 paths' fused step only");
+    HTR_TRY(set_state(s, s->n_past, 0));
+    hipStream_t st = dev->stream;
+    HTR_TRY(htr_hip(dev, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
+    int rc = 0;
+    for (int i = 0; i < n_steps && rc == 0; i++) rc = record_step(s, st, classes);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &graph);
+    if (rc < 0) {
+        if (graph) hipGraphDestroy(graph);
+        return rc;
+    }
+    HTR_TRY(htr_hip(dev, e, "hipStreamEndCapture"));
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    HTR_TRY(htr_hip(dev, e, "hipGraphInstantiate"));
+    rc = htr_hip(dev, hipGraphLaunch(exec, st), "hipGraphLaunch");
+    if (rc == 0) rc = htr_hip(dev, hipEventRecord(dev->t0, st), "hipEventRecord");
+    for (int r = 0; r < reps && rc == 0; r++) rc = htr_hip(dev, hipGraphLaunch(exec, st), "hipGraphLaunch");
+    float ms = 0.0f;
+    if (rc == 0) rc = htr_hip(dev, hipEventRecord(dev->t1, st), "hipEventRecord");
+    if (rc == 0) rc = htr_hip(dev, hipEventSynchronize(dev->t1), "hipEventSynchronize");
+    if (rc == 0) rc = htr_hip(dev, hipEventElapsedTime(&ms, dev->t0, dev->t1), "hipEventElapsedTime");
+    hipGraphExecDestroy(exec);
+    if (rc < 0) return rc;
+    *ms_per_step = ms / (float)(reps * n_steps);
     return 0;
 }
 

@@ -36,8 +36,9 @@ SYMBOLS = [
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
-    "htr_graph_free",
+    "htr_graph_free", "htr_session_profile_step",
 ]
+STEP_EMBED, STEP_QKV, STEP_ATTENTION, STEP_O, STEP_FFN, STEP_DOWN, STEP_HEAD, STEP_ALL = 1, 2, 4, 8, 16, 32, 64, 127
 
 
 class HtrError(RuntimeError):
@@ -170,6 +171,7 @@ def lib() -> C.CDLL:
             "htr_session_logits": (i32, [vp, vp]),
             "htr_session_rewind": (i32, [vp, sz]),
             "htr_session_kv_cache": (i32, [vp, C.POINTER(KvViewC)]),
+            "htr_session_profile_step": (i32, [vp, C.c_uint, i32, i32, C.POINTER(f32)]),
             "htr_debug_last_kernel": (i32, [vp, C.c_char_p, sz]),
             "htr_capture_begin": (i32, [vp]),
             "htr_capture_end": (i32, [vp, pp]),
@@ -673,6 +675,12 @@ class Session:
 
     def rewind(self, n_past: int) -> None:
         _check(lib().htr_session_rewind(self.h, n_past))
+
+    def profile_step(self, classes: int, n_steps: int = 16, reps: int = 20) -> float:
+        """milliseconds per decode step of the kernels of `classes` (STEP_* bits) alone, in a graph, at n_past"""
+        ms = C.c_float()
+        _check(lib().htr_session_profile_step(self.h, classes, n_steps, reps, C.byref(ms)))
+        return ms.value
 
     def kv_view(self) -> KvViewC:
         v = KvViewC()

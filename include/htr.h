@@ -290,6 +290,17 @@ int htr_session_kv_cache(htr_session *s, htr_kv_view *out);
  * (a read's session only grows, text.rs:242-328); it lets a bench replay one read's decode */
 int htr_session_rewind(htr_session *s, size_t n_past);
 
+/* the in-graph time of the decode step's kernel classes (a measurement entry, no reference counterpart: the
+ * reference's profiler is the per-dispatch timestamps of gpu.rs:1004-1016): n_steps steps (1 … 256) recorded as one
+ * HIP graph holding only the kernels of `classes` (HTR_STEP_* bits), all at the session's position (nothing advances
+ * it; each step rewrites that KV row), replayed reps times after one untimed replay → milliseconds per step. A model of
+ * the f16 paths; the session must be at a position 1 … n_ctx − 1. */
+enum {
+    HTR_STEP_EMBED = 1, HTR_STEP_QKV = 2, HTR_STEP_ATTENTION = 4, HTR_STEP_O = 8, HTR_STEP_FFN = 16,
+    HTR_STEP_DOWN = 32, HTR_STEP_HEAD = 64, HTR_STEP_ALL = 127
+};
+int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int reps, float *ms_per_step);
+
 /* ---- the GPU token choice and the run-ahead decode (text.rs:165-232 Choice, text.rs:587-625 decode_gpu) -------- */
 /* the preset fields the choice reads (ocr-decode presets.rs:17-29) */
 typedef struct {
