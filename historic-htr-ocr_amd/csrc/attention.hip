@@ -750,6 +750,39 @@ int launch_attn_causal(htr_device *dev, hipStream_t st, const float *q, const ui
     return htr_launched(dev, "k_attn_causal<f16>");
 }
 
+// ---- the allocation-free decode attention ----------------------------------------------------------------------------
+//
+// htr_decode_attention_static keeps its split-K partials and ticket counters in one file-scope device array instead
+// of device memory the library allocates. Every GPU the library runs on holds its own copy (STATIC_SCRATCH_BYTES,
+// until the process ends); its address on a device is looked up once, when the device is opened
+// (attn_static_scratch_init), and kept in the device object — host code passes that address, never the array's name
+// (which on the host is a stand-in, not a device address). Layout: the tickets of up to STATIC_MAX_KV KV heads (one
+// 128-byte line each), then the partials [n_head][max_chunk][130] f32. Every call clears the tickets it uses with a
+// fill kernel first; calls that overlap on one GPU share the array and race.
+namespace {
+
+constexpr size_t STATIC_SCRATCH_BYTES = 4u << 20;
+constexpr int STATIC_MAX_KV = 64;
+constexpr size_t STATIC_CNT_BYTES = (size_t)STATIC_MAX_KV * CNT_STRIDE * 4;
+static __device__ __align__(256) unsigned char scratch[STATIC_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void k_zero_u32(uint32_t *p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
+int attn_static_scratch_init(htr_device *dev) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return htr_fail("hipGetSymbolAddress of the static attention scratch on device %d: %s", dev->ordinal,
+                        hipGetErrorString(e));
+    dev->static_scratch = p;
+    return 0;
+}
+
 // ---- ABI ------------------------------------------------------------------------------------------------------------
 
 extern "C" int htr_qkv_post(htr_device *dev, float *d_qkv, const float *d_q_norm, const float *d_k_norm,
@@ -786,5 +819,34 @@ extern "C" int htr_decode_attention(htr_device *dev, const float *d_q, const uin
     sc.max_chunk = (n_ctx + sc.chunk - 1) / sc.chunk;
     HTR_TRY(htr_scratch(dev, SCR_ATTN_PART, attn_part_bytes(n_head, sc.max_chunk), (void **)&sc.part));
     HTR_TRY(htr_scratch(dev, SCR_ATTN_CNT, attn_counter_bytes(n_kv), (void **)&sc.counters));
+    return launch_attn_decode(dev, dev->stream, d_q, d_k, d_v, n_head, n_kv, n_ctx, nullptr, n_keys, scale, sc, d_out);
+}
+
+extern "C" int htr_decode_attention_static(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v,
+                                           int n_head, int n_kv, int n_ctx, int n_keys, float scale, float *d_out) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!d_q || !d_k || !d_v || !d_out) return htr_fail("htr_decode_attention_static: null argument");
+    if (n_keys < 1 || n_keys > n_ctx)
+        return htr_fail("htr_decode_attention_static: %d keys in a %d-row cache", n_keys, n_ctx);
+    if (n_ctx > MAX_CHUNKS * MAX_CHUNK_KEYS)
+        return htr_fail("htr_decode_attention_static: a %d-row cache (at most %d)", n_ctx, MAX_CHUNKS * MAX_CHUNK_KEYS);
+    if (n_kv < 1 || n_kv > STATIC_MAX_KV)
+        return htr_fail("htr_decode_attention_static: %d KV heads (the static scratch has tickets for %d)", n_kv,
+                        STATIC_MAX_KV);
+    if (!dev->static_scratch) return htr_fail("htr_decode_attention_static: the device has no static scratch address");
+    AttnScratch sc{};
+    sc.chunk = attn_chunk_for(n_ctx);
+    sc.max_chunk = (n_ctx + sc.chunk - 1) / sc.chunk;
+    const size_t part = attn_part_bytes(n_head, sc.max_chunk);
+    if (part > STATIC_SCRATCH_BYTES - STATIC_CNT_BYTES)
+        return htr_fail("htr_decode_attention_static: %d heads x %d chunks need %zu bytes of partials, the static scratch "
+                        "holds %zu",
+                        n_head, sc.max_chunk, part, STATIC_SCRATCH_BYTES - STATIC_CNT_BYTES);
+    unsigned char *base = (unsigned char *)dev->static_scratch;
+    sc.counters = (uint32_t *)base;
+    sc.part = (float *)(base + STATIC_CNT_BYTES);
+    const int n_cnt = n_kv * CNT_STRIDE;
+    hipLaunchKernelGGL(k_zero_u32, dim3((n_cnt + 255) / 256), dim3(256), 0, dev->stream, sc.counters, n_cnt);
+    HTR_TRY(htr_launched(dev, "k_zero_u32"));
     return launch_attn_decode(dev, dev->stream, d_q, d_k, d_v, n_head, n_kv, n_ctx, nullptr, n_keys, scale, sc, d_out);
 }

@@ -45,7 +45,12 @@ struct htr_device {
     bool capturing = false;
     // the last kernel launched (its instance: template arguments included), for tests that check the dispatch
     std::string last_kernel;
+    // this device's address of the file-scope scratch array of htr_decode_attention_static (attention.hip)
+    void *static_scratch = nullptr;
 };
+
+// looks up this device's address of the allocation-free attention's scratch array (the device must be current)
+int attn_static_scratch_init(htr_device *dev);
 
 // -1 with a message when the device's stream is being captured by the caller (allocation and synchronisation are not
 // part of a graph), else 0

@@ -116,6 +116,16 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
         delete dev;
         return htr_fail("hipEventCreate: %s", hipGetErrorString(e));
     }
+    // with the device current: its address of the allocation-free attention's scratch array
+    if (attn_static_scratch_init(dev) < 0) {
+        std::string keep = htr_last_error();
+        hipEventDestroy(dev->t0);
+        hipEventDestroy(dev->t1);
+        hipHostFree(dev->pinned);
+        hipStreamDestroy(dev->stream);
+        delete dev;
+        return htr_fail("%s", keep.c_str());
+    }
     *out = dev;
     return 0;
 }

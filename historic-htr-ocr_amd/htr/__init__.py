@@ -36,7 +36,7 @@ SYMBOLS = [
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
-    "htr_graph_free", "htr_session_profile_step",
+    "htr_graph_free", "htr_decode_attention_static", "htr_session_profile_step",
 ]
 STEP_EMBED, STEP_QKV, STEP_ATTENTION, STEP_O, STEP_FFN, STEP_DOWN, STEP_HEAD, STEP_ALL = 1, 2, 4, 8, 16, 32, 64, 127
 
@@ -135,6 +135,7 @@ def lib() -> C.CDLL:
             "htr_matvec_ffn": (i32, [vp, vp, vp, vp, vp, f32, vp]),
             "htr_qkv_post": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, f32, vp, vp]),
             "htr_decode_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
+            "htr_decode_attention_static": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, f32, vp]),
             "htr_causal_attention": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, vp]),
             "htr_choose": (i32, [vp, vp, i32, vp, i32, i32, f32, f32, vp, vp, vp]),
             "htr_choose_many": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, f32, vp]),

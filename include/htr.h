@@ -139,6 +139,14 @@ int htr_qkv_post(htr_device *dev, float *d_qkv, const float *d_q_norm, const flo
  * head-major f16 caches [n_kv][n_ctx][128], n_keys keys, scale → out [n_head·128] f32. GQA group 2. */
 int htr_decode_attention(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v, int n_head,
                          int n_kv, int n_ctx, int n_keys, float scale, float *d_out);
+/* htr_decode_attention without allocation: no counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid it): the same kernel and result,
+ * bit for bit, with its split-K partials and tickets in a file-scope device array of 4 MiB per GPU (held until the
+ * process ends) instead of library-allocated scratch. Shapes whose partials exceed it (n_head × chunks × 520 bytes
+ * > 4 MiB − 8 KiB: 16 heads fit every cache size, 32 heads up to 64,256 rows) and more than 64 KV heads are
+ * refused with an error. Calls that overlap on one GPU share the array and race; each call clears its tickets. */
+int htr_decode_attention_static(htr_device *dev, const float *d_q, const uint16_t *d_k, const uint16_t *d_v,
+                                int n_head, int n_kv, int n_ctx, int n_keys, float scale, float *d_out);
 /* causal GQA prefill attention (attention_causal.wgsl, text.rs:484-499): q [n_q][n_head·128] f32 (normed and roped)
  * at positions pos0 …, the head-major f16 caches [n_kv][n_ctx][128] holding the keys 0 … pos0 + n_q − 1 → out
  * [n_q][n_head·128] f32 = softmax(q·scale·Kᵀ over the keys ≤ each query's position)·V. GQA group 2. */
