@@ -125,7 +125,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     mean_keys = (prompt_len + prompt_len + n_new - 1) / 2
     bpt = decode_bytes_per_token(mean_keys)
     tok_s = steps * n_new / dt
-    phases = decode_phases(s, prompt_len - 1 + n_new // 2, cfg["n_layer"])
+    phases = decode_phases(s, prompt_len - 1 + n_new // 2, cfg["n_layer"]) if GRAPHS else None
     prefill_f32_s = prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s
     out = {
         "tok_s": tok_s,
@@ -166,9 +166,14 @@ def decode_phases(s, pos, n_layer, n_steps=16, reps=20):
     return out
 
 
+GRAPHS = True  # --no-graphs: the graph-recording legs are skipped (None in the line)
+
+
 def graphed(dev, calls, reps):
     """µs per call of `calls` (a list of zero-argument functions, each one library entry point) recorded once into a
     graph and replayed reps times after one untimed replay"""
+    if not GRAPHS:
+        return float("nan")
     dev.capture_begin()
     try:
         for f in calls:
@@ -505,6 +510,17 @@ def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
                       f"than the workload's 1024-1536 (the 633 MB of weights per token dominate either way)"}
 
 
+def no_nan(v):
+    """NaN (a leg skipped with --no-graphs) → null, so that the line is strict JSON"""
+    if isinstance(v, float) and v != v:
+        return None
+    if isinstance(v, dict):
+        return {k: no_nan(x) for k, x in v.items()}
+    if isinstance(v, list):
+        return [no_nan(x) for x in v]
+    return v
+
+
 def roofline_by_config(r: dict) -> dict:
     """each workload's achieved rate as a fraction of the bound that caps it (HBM 8 TB/s; the vision GEMMs: dense f16
     MFMA 2.5 PFLOP/s)"""
@@ -547,7 +563,12 @@ def main():
     ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, vision")
     ap.add_argument("--choose-steps", type=int, default=10000,
                     help="single-launch steps of the choose leg (a counter run takes fewer: every launch is sampled)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="skip the legs that record graphs (decode phases, graph-node timings): for profilers that "
+                         "cannot follow stream capture (with HTR_GRAPHS=0 the decode launches its kernels one by one)")
     args = ap.parse_args()
+    global GRAPHS
+    GRAPHS = not args.no_graphs
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this path has no multi-GPU sharding (asked for {args.gpus})", file=sys.stderr)
         sys.exit(2)
@@ -607,7 +628,7 @@ def main():
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)
     dev.close()
-    print(json.dumps(result), flush=True)
+    print(json.dumps(no_nan(result)), flush=True)
 
 
 if __name__ == "__main__":

@@ -10,8 +10,9 @@
 //     CPU loop `if l > logits[best]` starting at best = 0 decides; every logit NaN → 0.
 //
 // Schedule: grid (groups, rows); a workgroup owns SP consecutive logits of one row (2048 for a single row: 75
-// workgroups over 151,936; 4096 for many), stages them in LDS, applies the penalties of the window ids that fall in
-// its range, and reduces (value, index) to its best. The row's best of all
+// workgroups over 151,936; 4096 for many), stages them in LDS, marks the logits whose id is in the window (a mark per
+// logit in LDS: an id repeated in the window marks the same logit, so each distinct id is penalised once with no
+// search for its first occurrence), applies the penalty as it reduces (value, index) to its best. The row's best of all
 // workgroups is one 64-bit atomic max on an order-preserving key (value bits mapped to unsigned order, −0 as +0, then
 // the complemented index, so ties go to the lowest index); the last workgroup of the row (atomic ticket) reads it,
 // writes the token, appends it to the history and updates the counts. One launch per choice; the key and the ticket
@@ -28,7 +29,6 @@ namespace {
 
 constexpr int CW = 256;
 constexpr int LINE = 16;            // u64 words between rows' best keys / u32 between tickets: one 128-byte line each
-constexpr int WIN_LDS = CW;  // windows up to this many ids are staged in LDS (longer ones are read from memory)
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float w, uint32_t j) { return v > w || (v == w && i < j); }
 
@@ -82,19 +82,17 @@ __device__ __forceinline__ void block_best(float &v, uint32_t &i) {
 template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
     constexpr int PER_ = SP / CW;  // logits a thread
     __shared__ float s_l[SP];
-    __shared__ uint32_t s_win[WIN_LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_pen[SP];  // the span's logits whose id is in the window
     __shared__ int s_last;
     const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lo = g * SP, hi = min(a.n_vocab, lo + SP);
     float *logits = a.logits + (size_t)row * a.n_vocab;
     uint32_t *hist = a.hist + (size_t)row * a.hist_stride;
     const int len = a.len_dev ? *a.len_dev : a.len;
-
-    // the window (≤ WIN_LDS ids) → LDS with one load per thread, issued with the logits' loads
     const int start = len - min(len, a.window);
     const int n_win = a.rp != 1.0f ? len - start : 0;
-    const bool win_lds = n_win <= WIN_LDS;
-    if (win_lds && tid < n_win) s_win[tid] = hist[start + tid];
+    // the window's first ids (one load a thread), issued with the logits' loads
+    const uint32_t w0 = tid < n_win ? hist[start + tid] : 0xffffffffu;
     // the span's logits → LDS: every load issued before the first store (16-byte loads when the row is aligned)
     if ((((uintptr_t)(logits + lo)) & 15) == 0) {
         float4 lv[PER_ / 4];
@@ -118,39 +116,41 @@ template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArg
 #pragma unroll
         for (int i = 0; i < PER_; i++) s_l[tid + CW * i] = lv[i];
     }
-    __syncthreads();
-    // the window's distinct ids in [lo, hi): the first occurrence of each applies the penalty
+    // the penalty marks: cleared, then every window id in [lo, hi) sets its logit's mark. An id that occurs several
+    // times in the window sets the same mark: each DISTINCT id is penalised once, as its first occurrence is in
+    // sampling.rs:39-48 (the order of the window does not matter)
     if (n_win > 0) {
-        for (int j = tid; j < n_win; j += CW) {
-            const uint32_t t = win_lds ? s_win[j] : hist[start + j];
-            if (t < (uint32_t)lo || t >= (uint32_t)hi) continue;
-            bool first = true;
-            for (int i = 0; i < j; i++)
-                if ((win_lds ? s_win[i] : hist[start + i]) == t) {
-                    first = false;
-                    break;
-                }
-            if (!first) continue;
-            const float x = s_l[t - lo];
-            const float y = x < 0.0f ? x * a.rp : x / a.rp;
-            s_l[t - lo] = y;
-            logits[t] = y;
-        }
+        for (int u = tid; u < SP / 16; u += CW) reinterpret_cast<uint4 *>(s_pen)[u] = make_uint4(0, 0, 0, 0);
         __syncthreads();
+        if (w0 >= (uint32_t)lo && w0 < (uint32_t)hi) s_pen[w0 - lo] = 1;
+        for (int j = tid + CW; j < n_win; j += CW) {
+            const uint32_t t = hist[start + j];
+            if (t >= (uint32_t)lo && t < (uint32_t)hi) s_pen[t - lo] = 1;
+        }
     }
-    // pass 1: this workgroup's best (NaN never wins: `better` is false for it)
-    // (a fixed count of LDS reads, all issued before the first compare)
+    __syncthreads();
+    // pass 1: the penalties (rp on the marked logits, written back in place; then fp) and this workgroup's best
+    // (NaN never wins: `better` is false for it); a fixed count of LDS reads, all issued before the first compare
     float bv = -INFINITY;
     uint32_t bi = 0xffffffffu;
     float xs[PER_];
+    bool pen[PER_];
 #pragma unroll
-    for (int i = 0; i < PER_; i++) xs[i] = s_l[tid + CW * i];
+    for (int i = 0; i < PER_; i++) {
+        xs[i] = s_l[tid + CW * i];
+        pen[i] = n_win > 0 && s_pen[tid + CW * i];
+    }
 #pragma unroll
     for (int i = 0; i < PER_; i++) {
         const int e = tid + CW * i;
         if (lo + e < hi) {
             float x = xs[i];
             const uint32_t k = (uint32_t)(lo + e);
+            if (pen[i]) {
+                x = x < 0.0f ? x * a.rp : x / a.rp;
+                logits[k] = x;
+                if (e == 0) s_l[0] = x;  // the NaN-at-index-0 rule below reads the penalised value
+            }
             if (a.fp != 0.0f && a.counts[k] != 0u) x = x - a.fpen[k];
             if (better(x, k, bv, bi)) {
                 bv = x;

@@ -112,3 +112,34 @@ def test_choose_rejects_bad_penalty(dev):
         htr.choose(dev, dev.alloc(16), 4, dev.alloc(16), 1, 1, 0.0, tok)
     with pytest.raises(htr.HtrError, match="repetition penalty"):
         htr.choose(dev, dev.alloc(16), 4, dev.alloc(16), 1, 1, 1e-40, tok)
+
+
+@pytest.mark.parametrize("window,n_hist", [(600, 700), (300, 250), (257, 1000)])
+def test_long_windows_penalise_each_distinct_id_once(dev, window, n_hist):
+    """windows longer than a workgroup (256 threads: the ids past the first 256 are marked in a second pass), with
+    ids repeated up to 5 times and some landing on the planted maxima, 151936 logits, rp 1.1 and 0.8: the token and
+    the penalised logits (written back in place) equal the oracle's choose bit for bit"""
+    n_vocab = 151936
+    g = np.random.default_rng(window + n_hist)
+    base, _ = synth_choice(window + 7, 1, n_vocab, 64)
+    hist = g.integers(0, n_vocab, n_hist).astype(np.int32)
+    rep = g.integers(0, n_hist, n_hist // 3)
+    hist[rep] = hist[g.integers(0, n_hist, rep.size)]
+    top = np.flatnonzero(base[0] == base[0].max())
+    hist[-3:] = top[:3]  # the planted maxima inside the window
+    hb = dev.upload(np.concatenate([hist, np.zeros(1, np.int32)]).astype(np.uint32))
+    tok = dev.alloc(4)
+    for rp in (1.1, 0.8):
+        lb = dev.upload(base[0])
+        htr.choose(dev, lb, n_vocab, hb, n_hist, window, rp, tok)
+        ref = base[0].copy()
+        want = orc.choose(ref, rp, window, 0.0, list(hist))
+        assert int(tok.download(np.uint32)[0]) == want, rp
+        assert np.array_equal(lb.download(np.float32).view(np.uint32), ref.view(np.uint32)), rp
+        lb.free()
+
+
+def synth_choice(seed, rows, n_vocab, window):
+    from htr import synth
+
+    return synth.choice_inputs(seed, rows, n_vocab, window)
