@@ -596,6 +596,7 @@ def main():
                    "device": name},
     }
     decode_inputs = None
+    dev.phase("decode")
     if want("decode"):
         d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup)
         result["value"] = d["tok_s"]
@@ -603,6 +604,7 @@ def main():
         result["decode"] = d
         for obj in keep[::-1]:
             obj.free()
+    dev.phase("matvec")
     if want("matvec"):
         mv = bench_matvec(dev)
         result["matvec"] = mv
@@ -615,15 +617,20 @@ def main():
                                         "runs its matvecs one a graph node, see roofline_by_config",
                               "algorithmic_bytes_per_launch": mv["batched_bytes_per_launch"],
                               "avg_launch_us": mv["batched_launch_us"]}
+    dev.phase("choose")
     if want("choose"):
         result["choose"] = bench_choose(dev, n_steps=args.choose_steps)
+    dev.phase("attention")
     if want("attention"):
         result["attention"] = bench_attention(dev)
+    dev.phase("copy")
     if want("copy"):
         result["copy"] = bench_copy(dev)
+    dev.phase("vision")
     if want("vision"):
         result["vision_gemm"] = bench_vision_gemm(dev)
         result["vision_encode"] = bench_vision_encode(dev)
+    dev.phase("-")
     result["roofline_by_config"] = roofline_by_config(result)
     if decode_inputs is not None and not args.skip_cpu:
         result["cpu_baseline"] = cpu_baseline(decode_inputs)

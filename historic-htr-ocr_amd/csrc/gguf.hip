@@ -16,6 +16,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <exception>
 #include <cstring>
 #include <map>
 #include <string>
@@ -120,7 +121,7 @@ std::string parse_value(Cursor &c, uint32_t ty, int depth, Value &v) {
         if (depth > 0) return "GGUF nested arrays are not part of the format";
         v.elem = c.le<uint32_t>();
         const uint64_t n = c.le<uint64_t>();
-        if (n > c.n) throw NeedMore{};  // every element takes at least a byte
+        if (n > c.n - c.pos) throw NeedMore{};  // every element takes at least a byte of what is left
         v.arr.resize((size_t)n);
         for (uint64_t k = 0; k < n; k++) {
             std::string e = parse_value(c, v.elem, depth + 1, v.arr[(size_t)k]);
@@ -199,6 +200,7 @@ std::string parse_header(const uint8_t *b, size_t n, htr_gguf &g) {
                 elems *= t.shape[d];
             }
             t.n_elements = elems;
+            if (elems / blk.first > UINT64_MAX / blk.second) return "tensor " + name + ": size overflows";
             t.n_bytes = elems / blk.first * blk.second;
             snprintf(t.name, sizeof t.name, "%s", name.c_str());
             if (name.size() >= sizeof t.name) return "tensor name " + name + " is too long";
@@ -215,20 +217,34 @@ std::string parse_header(const uint8_t *b, size_t n, htr_gguf &g) {
 
 int open_parsed(htr_gguf *g, htr_gguf **out) {
     size_t want = FIRST_PREFIX;
-    for (;;) {
-        const size_t n = (size_t)std::min<uint64_t>(want, g->len);
-        std::vector<uint8_t> prefix(n);
-        if (src_read(g, 0, prefix.data(), n) < 0) return -1;
-        const std::string e = parse_header(prefix.data(), n, *g);
-        if (e.empty()) break;
-        if (e != "more") return htr_fail("%s", e.c_str());
-        if (n >= g->len) return htr_fail("GGUF truncated: the header runs past the end of the file");
-        want *= 2;
+    // a hostile header (counts, lengths) must end in an error, not in an exception through the C ABI
+    try {
+        for (;;) {
+            const size_t n = (size_t)std::min<uint64_t>(want, g->len);
+            std::vector<uint8_t> prefix(n);
+            if (src_read(g, 0, prefix.data(), n) < 0) return -1;
+            const std::string e = parse_header(prefix.data(), n, *g);
+            if (e.empty()) break;
+            if (e != "more") return htr_fail("%s", e.c_str());
+            if (n >= g->len) return htr_fail("GGUF truncated: the header runs past the end of the file");
+            want *= 2;
+        }
+    } catch (const std::exception &x) {
+        return htr_fail("GGUF header: %s", x.what());
     }
-    for (const GgufTensor &t : g->tensors)
-        if (t.file_offset + t.n_bytes > g->len)
-            return htr_fail("tensor %s ends at byte %llu, the file has %llu", t.name,
-                            (unsigned long long)(t.file_offset + t.n_bytes), (unsigned long long)g->len);
+    // every tensor inside the file (lib.rs:328-334), its end computed without overflowing
+    const uint64_t len = g->len;
+    for (const GgufTensor &t : g->tensors) {
+        if (g->data_offset > len || t.offset > len - g->data_offset || t.n_bytes > len - g->data_offset - t.offset) {
+            const uint64_t a = g->data_offset, b = t.offset, c = t.n_bytes;
+            if (b > UINT64_MAX - a || c > UINT64_MAX - a - b)
+                return htr_fail("tensor %s ends past byte 2^64 (%llu + %llu + %llu), the file has %llu", t.name,
+                                (unsigned long long)a, (unsigned long long)b, (unsigned long long)c,
+                                (unsigned long long)len);
+            return htr_fail("tensor %s ends at byte %llu, the file has %llu", t.name, (unsigned long long)(a + b + c),
+                            (unsigned long long)len);
+        }
+    }
     *out = g;
     return 0;
 }

@@ -47,6 +47,8 @@ struct htr_device {
     std::string last_kernel;
     // this device's address of the file-scope scratch array of htr_decode_attention_static (attention.hip)
     void *static_scratch = nullptr;
+    // htr_phase has a roctx range open on the calling thread
+    bool phase_open = false;
 };
 
 // looks up this device's address of the allocation-free attention's scratch array (the device must be current)

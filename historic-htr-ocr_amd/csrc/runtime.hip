@@ -8,6 +8,8 @@
 #include <thread>
 #include <vector>
 
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include "htr_internal.h"
 
 // ---- errors ---------------------------------------------------------------------------------------------------------
@@ -161,6 +163,7 @@ extern "C" int htr_timer_end(htr_device *dev, float *ms) {
 
 extern "C" int htr_device_close(htr_device *dev) {
     if (!dev) return 0;
+    if (dev->phase_open) roctxRangePop();
     hipSetDevice(dev->ordinal);
     if (dev->capturing) {  // a capture left open: end it and drop what it recorded
         hipGraph_t g = nullptr;
@@ -254,9 +257,20 @@ extern "C" int htr_device_info(htr_device *dev, char *name, size_t name_len, int
     return 0;
 }
 
+// gpu.rs:1349-1358 Gpu::phase: the label of the following work. Here a roctx range on the calling thread (what
+// rocprofv3 --marker-trace records): the device's open range, if any, ends; a name other than NULL, "" or "-" opens
+// the next one
 extern "C" int htr_phase(htr_device *dev, const char *name) {
-    (void)name;
-    return htr_check_alive(dev);
+    HTR_TRY(htr_check_alive(dev));
+    if (dev->phase_open) {
+        roctxRangePop();
+        dev->phase_open = false;
+    }
+    if (name && *name && strcmp(name, "-") != 0) {
+        roctxRangePushA(name);
+        dev->phase_open = true;
+    }
+    return 0;
 }
 
 // ---- memory ---------------------------------------------------------------------------------------------------------

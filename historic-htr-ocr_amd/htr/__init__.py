@@ -327,6 +327,10 @@ class Device:
     def mark_lost(self, why: str = "") -> None:
         _check(lib().htr_debug_mark_lost(self.h, why.encode()))
 
+    def phase(self, name: str) -> None:
+        """Gpu::phase: the label of the following work (a roctx range; "-" ends it)"""
+        _check(lib().htr_phase(self.h, name.encode()))
+
     def last_kernel(self) -> str:
         """the instance name of the last kernel this device launched (e.g. 'k_dmv_full<4,1,qkv>')"""
         buf = C.create_string_buffer(96)

@@ -100,7 +100,8 @@ int htr_download(htr_device *dev, void *h_dst, const void *d_src, size_t bytes);
 /* d_dst[0 … bytes) = d_src[0 … bytes) on the device's stream, both 16-byte aligned, not overlapping (gpu.rs:2102-2110
  * Batch::copy). Also the plain copy of known size that calibrates the HBM byte counters. */
 int htr_copy(htr_device *dev, void *d_dst, const void *d_src, size_t bytes);
-/* a phase label for the profiler ranges (gpu.rs:1349-1358 Gpu::phase) */
+/* the phase of the following work (gpu.rs:1349-1358 Gpu::phase: "vision", "prefill", "decode", "-" = none): a roctx
+ * range on the calling thread that rocprofv3 --marker-trace records; the device's previous phase range ends */
 int htr_phase(htr_device *dev, const char *name);
 
 /* ---- weights (gpu.rs:1595-1677 upload_tensor with WeightType::Q8_0; text.rs:101-110 weight) -------------------- */

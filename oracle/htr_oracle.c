@@ -32,6 +32,24 @@ void or_lcg_fill(uint64_t *state, float *out, size_t n, float scale) {
     }
 }
 
+/* the logits of gpu_choice_matches_choose (text.rs:1021-1027), one LCG draw order per mode: 0 round(lcg·3), 1 lcg·20,
+ * 2 −inf when a draw is > 0.9, else a second draw → round(lcg·2) − 1, 3 lcg·1e-3. Rust's f32::round rounds half away
+ * from zero, as C's roundf does; the products are f32 */
+void or_choice_matrix_logits(uint64_t *state, int mode, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) {
+        switch (mode) {
+        case 0: out[i] = roundf(lcg_next(state) * 3.0f); break;
+        case 1: out[i] = lcg_next(state) * 20.0f; break;
+        case 2: {
+            const float u = lcg_next(state);
+            out[i] = u > 0.9f ? -INFINITY : roundf(lcg_next(state) * 2.0f) - 1.0f;
+            break;
+        }
+        default: out[i] = lcg_next(state) * 1e-3f; break;
+        }
+    }
+}
+
 /* text.rs:1070-1073 */
 void or_lcg_bits(uint64_t *state, uint32_t *out, size_t n) {
     for (size_t i = 0; i < n; i++) {

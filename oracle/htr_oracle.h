@@ -41,6 +41,9 @@ extern "C" {
 /* the reference tests' 64-bit LCG (text.rs:670-673): s = s·6364136223846793005 + 1442695040888963407 (mod 2^64),
  * value = ((s >> 40) / 2^24)·2 − 1, times `scale` */
 void or_lcg_fill(uint64_t *state, float *out, size_t n, float scale);
+/* the logits of the reference's GPU-choice test matrix (text.rs:1021-1027), `mode` 0 … 3, n values, LCG draws in its
+ * order (mode 2 draws the second value only when the first is ≤ 0.9) */
+void or_choice_matrix_logits(uint64_t *state, int mode, size_t n, float *out);
 /* the raw 32-bit draws of choose_pen_is_exact (text.rs:1070-1073): (s >> 32) */
 void or_lcg_bits(uint64_t *state, uint32_t *out, size_t n);
 

@@ -26,6 +26,7 @@ def lib() -> C.CDLL:
         sig = {
             "or_lcg_fill": (None, [C.POINTER(C.c_uint64), vp, sz, f32]),
             "or_lcg_bits": (None, [C.POINTER(C.c_uint64), vp, sz]),
+            "or_choice_matrix_logits": (None, [C.POINTER(C.c_uint64), i32, sz, vp]),
             "or_f16_from_f32": (C.c_uint16, [f32]),
             "or_f32_from_f16": (f32, [C.c_uint16]),
             "or_f16_from_f32_n": (None, [vp, vp, sz]),
@@ -97,6 +98,12 @@ class Lcg:
     def f32(self, n: int, scale: float = 1.0) -> np.ndarray:
         out = np.empty(n, dtype=np.float32)
         lib().or_lcg_fill(C.byref(self.s), _p(out), n, scale)
+        return out
+
+    def choice_matrix(self, mode: int, n: int) -> np.ndarray:
+        """the logits of text.rs:1021-1027 for one step's mode (0 … 3), drawn in the reference's order"""
+        out = np.empty(n, dtype=np.float32)
+        lib().or_choice_matrix_logits(C.byref(self.s), mode, n, _p(out))
         return out
 
     def bits(self, n: int) -> np.ndarray:

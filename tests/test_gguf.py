@@ -191,3 +191,23 @@ def test_read_small_refuses_large_tensors():
     with htr.Gguf(data=gguf_bytes([], [("big", GGML_Q8_0, [32 * 40_000], big)])) as g:
         with pytest.raises(htr.HtrError, match="not small"):
             g.read_small("big")
+
+
+def test_hostile_counts_and_offsets_are_errors():
+    """a header whose numbers would overflow or ask for absurd memory ends in the reader's error, not in a crash: an
+    array count far beyond the bytes left (2^62 elements), and a tensor offset near 2^64 (offset + bytes wraps)"""
+    base = [("a.n", U32, 7)]
+    t = [("q", GGML_Q8_0, [32], bytes(34))]
+    b = bytearray(gguf_bytes(base + [("a.arr", ARR, (U32, [1, 2, 3]))], t))
+    # the array's count (u64 after its element type u32 = 4) → 2^62
+    key = b"a.arr"
+    pos = bytes(b).index(key) + len(key) + 4 + 4  # key, value type ARR (u32), element type (u32)
+    b[pos:pos + 8] = (1 << 62).to_bytes(8, "little")
+    with pytest.raises(htr.HtrError, match="truncated"):
+        htr.Gguf(data=bytes(b))
+    # the tensor's offset (u64 after name, n_dims, dims, type) → 2^64 − 64 (aligned): data offset + offset wraps
+    b = bytearray(gguf_bytes(base, t))
+    pos = bytes(b).index(b"\x01\x00\x00\x00\x20\x00\x00\x00\x00\x00\x00\x00\x08\x00\x00\x00") + 16
+    b[pos:pos + 8] = ((1 << 64) - 64).to_bytes(8, "little")
+    with pytest.raises(htr.HtrError, match="ends past byte 2\\^64"):
+        htr.Gguf(data=bytes(b))

@@ -287,16 +287,9 @@ def test_choose_penalty_is_ieee_exact():
 
 
 def _matrix_logits(g, n_vocab, mode, i, last):
-    if mode == 0:
-        l = np.round(g.f32(n_vocab, 3.0))  # ties everywhere, −0 / +0 among them
-    elif mode == 1:
-        l = g.f32(n_vocab, 20.0)
-    elif mode == 2:
-        a = g.f32(2 * n_vocab).reshape(n_vocab, 2)
-        l = np.where(a[:, 0] > 0.9, -np.inf, np.round(a[:, 1] * 2) - 1).astype(np.float32)
-    else:
-        l = g.f32(n_vocab, 1e-3)
-    l = l.astype(np.float32)
+    """text.rs:1021-1035: the mode's values in the reference's draw order (the oracle's restatement, pinned below
+    against a Python loop of the same draws), all −inf at step 7, the last chosen token made the maximum + 0.05"""
+    l = g.choice_matrix(mode, n_vocab)
     if i == 7:
         l[:] = -np.inf
     if last is not None:
@@ -317,6 +310,42 @@ def gpu_choice_matrix_inputs(case, steps=None):
         yield l, list(history), dict(counts), want
         history.append(want)
         counts[want] = counts.get(want, 0) + 1
+
+
+def test_choice_matrix_logits_follow_the_reference_draws():
+    """text.rs:1021-1027 restated in Python from the reference LCG (text.rs:670-673) one draw at a time: mode 0 rounds
+    half away from zero (2.5 → 3, −2.5 → −3, as Rust's f32::round), mode 2 draws its second value only when the first
+    is ≤ 0.9; the oracle's generator gives the same f32 values and leaves the LCG in the same state"""
+    def lcg(s):
+        s = (s * 6364136223846793005 + 1442695040888963407) % (1 << 64)
+        return s, np.float32(np.float32(s >> 40) / np.float32(1 << 24)) * np.float32(2.0) - np.float32(1.0)
+
+    def rnd(x):  # half away from zero, in f64 on the f32 value
+        x = float(x)
+        return np.float32(np.copysign(np.floor(abs(x) + 0.5), x))
+
+    for mode in range(4):
+        s = 12345 + mode
+        want = []
+        for _ in range(3000):
+            s, u = lcg(s)
+            if mode == 0:
+                want.append(rnd(u * np.float32(3.0)))
+            elif mode == 1:
+                want.append(u * np.float32(20.0))
+            elif mode == 2:
+                if u > np.float32(0.9):
+                    want.append(np.float32(-np.inf))
+                else:
+                    s, v = lcg(s)
+                    want.append(rnd(v * np.float32(2.0)) - np.float32(1.0))
+            else:
+                want.append(u * np.float32(1e-3))
+        g = orc.Lcg(12345 + mode)
+        got = g.choice_matrix(mode, 3000)
+        assert np.array_equal(got.view(np.uint32), np.array(want, np.float32).view(np.uint32)), mode
+        assert g.s.value == s, mode
+    assert rnd(np.float32(2.5)) == 3.0 and rnd(np.float32(-2.5)) == -3.0 and np.round(2.5) == 2.0
 
 
 def test_choose_matches_numpy_restatement_on_reference_matrix():

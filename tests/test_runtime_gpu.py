@@ -42,3 +42,17 @@ def test_memory_ledger_counts_per_kind(dev):
     a.free()
     b.free()
     assert dev.mem_live() == before
+
+
+def test_phase_ranges(dev):
+    """gpu.rs:1349-1358 Gpu::phase: each name opens a roctx range on this thread and ends the previous one ("-" ends
+    it); on a dead device the call fails with the sticky reason"""
+    for name in ("vision", "prefill", "decode", "-", "-", "decode"):
+        dev.phase(name)
+    dev.phase("-")
+    d = htr.Device(0)
+    d.phase("prefill")
+    d.mark_lost("test: device.destroy()")
+    with pytest.raises(htr.HtrError, match="device.destroy"):
+        d.phase("decode")
+    d.close()
