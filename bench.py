@@ -344,19 +344,20 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
 def bench_vision_gemm(dev, reps=5, m=12100, dim=1024, ff=4096):
-    """the vision encoder layer's GEMMs on the matrix cores at one page's 12100 patch rows: q, k, v, o [1024 x 1024],
-    gate + up fused with SwiGLU [4096 x 1024] x 2, down [1024 x 4096] (q8_0 weights dequantised to f16 at load)"""
+    """the vision encoder layer's GEMMs on the matrix cores at one page's 12100 patch rows, as the encoder runs them:
+    Q / K / V as one GEMM over the stacked [3072 x 1024] weights, o [1024 x 1024] onto the residual, gate + up
+    [4096 x 1024] x 2 fused with SwiGLU, down [1024 x 4096] onto the residual (q8_0 weights dequantised to f16 at
+    load)"""
     x16 = dev.upload(synth_normal_f16(71, m * ff))
-    y = dev.alloc(m * dim * 4)
+    y = dev.alloc(m * 3 * dim * 4)
     g16 = dev.alloc(m * ff * 2)
     ws = {name: htr.Weight(dev, htr.synth_q8_0(600 + i, rows, cols), rows, cols, f16=True,
                            scale=64.0 if name == "down" else 1.0)
-          for i, (name, rows, cols) in enumerate([("q", dim, dim), ("k", dim, dim), ("v", dim, dim), ("o", dim, dim),
-                                                  ("gate", ff, dim), ("up", ff, dim), ("down", dim, ff)])}
+          for i, (name, rows, cols) in enumerate([("qkv", 3 * dim, dim), ("o", dim, dim), ("gate", ff, dim),
+                                                  ("up", ff, dim), ("down", dim, ff)])}
 
     def layer():
-        for name in ("q", "k", "v"):
-            htr.gemm_f16(dev, x16, m, ws[name], y)
+        htr.gemm_f16(dev, x16, m, ws["qkv"], y)
         htr.gemm_f16(dev, x16, m, ws["o"], y, acc=True)
         htr.gemm_ffn_f16(dev, x16, m, ws["gate"], ws["up"], 1.0 / 64, g16)
         htr.gemm_f16(dev, g16, m, ws["down"], y, acc=True)

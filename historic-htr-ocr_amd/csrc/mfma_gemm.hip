@@ -142,7 +142,14 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float *part, int spl
     }
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// silu(g) = g / (1 + e^−g) on the hardware's 2^x and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each, as the
+// reference's WGSL exp and division are not correctly rounded either): ffn_coopd's epilogue evaluates it for every
+// one of the tile's 32K outputs, where an exact expf and an IEEE division cost about 40 VALU instructions each value.
+// Large −g: 2^x → inf, 1 / inf = 0, g·0 = −0; large g: 1 / 1 → g; NaN stays NaN
+__device__ __forceinline__ float silu(float g) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // the 16-byte chunk slot of (row r, chunk c) in a stage region
 __device__ __forceinline__ int chunk_slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
@@ -270,14 +277,29 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
 
     // epilogue: lane ℓ, register r → row 8(r/4) + 4(ℓ/32) + r%4, column ℓ%32 of each 32 × 32 tile
     if constexpr (EPI == GEMM_FFN) {
-        const int col = tn * (BN / 2) + wn * 32 + (lane & 31);  // gate tile j = 0, up tile j = 1
+        // the wave's TM·32 × 32 f16 outputs go through its own region of the (now idle) stage ring — rows of 32 values
+        // 80 bytes apart, so that the two half-waves' rows 4 apart fall on different banks — and leave it as 16-byte
+        // row chunks: 2·TM stores a lane instead of 16·TM two-byte ones
+        constexpr int RS = 40;                                         // halves a staged row
+        static_assert(NW * TM * 32 * RS * 2 <= ST * SCH * 16, "the staging fits the ring");
+        __syncthreads();                                               // every wave is done with the ring
+        _Float16 *stg = reinterpret_cast<_Float16 *>(s_t) + wave * TM * 32 * RS;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int row = row0 + wm * TM * 32 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < m) a.y16[(size_t)row * a.rows[0] + col] = (_Float16)(silu(acc[i][0][r]) * acc[i][1][r] * a.scale);
+                const int rr = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                stg[rr * RS + (lane & 31)] = (_Float16)(silu(acc[i][0][r]) * acc[i][1][r] * a.scale);
             }
+        __builtin_amdgcn_wave_barrier();
+        const int col0 = tn * (BN / 2) + wn * 32;  // gate tile j = 0, up tile j = 1: the same 32 outputs
+#pragma unroll
+        for (int t = 0; t < 2 * TM; t++) {
+            const int u = lane + 64 * t, rr = u >> 2, c = u & 3;
+            const int row = row0 + wm * TM * 32 + rr;
+            const int4 v = *reinterpret_cast<const int4 *>(stg + rr * RS + 8 * c);
+            if (row < m) *reinterpret_cast<int4 *>(a.y16 + (size_t)row * a.rows[0] + col0 + 8 * c) = v;
+        }
         return;
     }
     // SPLIT: this part of K's product into its own slice [sp][M][N] (k_split_reduce adds the slices)
