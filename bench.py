@@ -102,38 +102,61 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     log(f"prefill {prompt_len - 1} tokens ({path} path): {prefill_s * 1e3:.1f} ms (first call {prefill_cold_s * 1e3:.1f} ms)")
     preset = htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new)
     ch = s.choice(preset, prompt, chunk=16, depth=2)
+    fused = s.fused_step
+    form = "one launch a token (embed + 28 layers), then the LM head and the choice" if fused else "per kernel"
 
-    def one_read():
-        s.rewind(prompt_len - 1)
-        s.step(int(prompt[-1]))
-        return s.decode_gpu(ch, n_new)
+    def reads_of(sess, chc, n_reads, n_warm):
+        def one_read():
+            sess.rewind(prompt_len - 1)
+            sess.step(int(prompt[-1]))
+            return sess.decode_gpu(chc, n_new)
 
-    ref = None
-    for i in range(warmup):
-        toks = one_read()
-        ref = ref or toks
-    dev.sync()
-    t0 = time.perf_counter()
-    reads = []
-    for i in range(steps):
-        reads.append(one_read())
-    dev.sync()
-    dt = time.perf_counter() - t0
+        ref = None
+        for i in range(n_warm):
+            toks = one_read()
+            ref = ref or toks
+        dev.sync()
+        t0 = time.perf_counter()
+        got = [one_read() for _ in range(n_reads)]
+        dev.sync()
+        return got, time.perf_counter() - t0, ref
+
+    reads, dt, ref = reads_of(s, ch, steps, warmup)
     same = all(r == reads[0] for r in reads) and (ref is None or ref == reads[0])
-    log(f"decode: {steps} reads × {n_new} tokens in {dt:.3f} s, identical reads: {same}")
+    log(f"decode ({form}): {steps} reads × {n_new} tokens in {dt:.3f} s, identical reads: {same}")
     # the read's steps run at 1024 … 1535 keys (mean 1279.5)
     mean_keys = (prompt_len + prompt_len + n_new - 1) / 2
     bpt = decode_bytes_per_token(mean_keys)
     tok_s = steps * n_new / dt
-    phases = decode_phases(s, prompt_len - 1 + n_new // 2, cfg["n_layer"]) if GRAPHS else None
+    mid = prompt_len - 1 + n_new // 2
+    fused_phases = fused_step_phases(s, mid, int(prompt[5]), cfg["n_layer"]) if fused else None
+    # the same read on the per-kernel step (A/B in one run), and its kernel classes in graphs
+    per_kernel = None
+    if fused:
+        sk = m.session(prompt_len + n_new)
+        sk.fused_step = False
+        sk.prefill(prompt[:-1])
+        chk = sk.choice(preset, prompt, chunk=16, depth=2)
+        rk, dtk, _ = reads_of(sk, chk, max(1, steps // 2), 1)
+        per_kernel = {"tok_s": len(rk) * n_new / dtk, "ms_per_token": dtk / (len(rk) * n_new) * 1e3,
+                      "same_tokens": rk[0] == reads[0]}
+        log(f"decode (per kernel): {per_kernel['tok_s']:.1f} tok/s, the same tokens: {per_kernel['same_tokens']}")
+        phases = decode_phases(sk, mid, cfg["n_layer"]) if GRAPHS else None
+        chk.free()
+        sk.free()
+    else:
+        phases = decode_phases(s, mid, cfg["n_layer"]) if GRAPHS else None
     prefill_f32_s = prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s
     out = {
+        "step_form": form,
         "tok_s": tok_s,
         "bytes_per_token": bpt,
         "mean_keys": mean_keys,
         "achieved_GBs": bpt * tok_s / 1e9,
         "frac": bpt * tok_s / 1e9 / HBM_PEAK_GBS,
         "roofline_tok_s": HBM_PEAK_GBS * 1e9 / bpt,
+        "fused_step_phases": fused_phases,
+        "per_kernel_step": per_kernel,
         "phases": phases,
         "ms_per_read": dt / steps * 1e3,
         "ms_per_token": dt / (steps * n_new) * 1e3,
@@ -163,6 +186,25 @@ def decode_phases(s, pos, n_layer, n_steps=16, reps=20):
             out[name + "_us_per_layer"] = us / n_layer
     out["sum_of_classes_us"] = sum(out[n + "_us"] for n, c in classes if c != htr.STEP_ALL)
     log("decode phases (µs a step, in graphs): " + ", ".join(f"{n} {out[n + '_us']:.1f}" for n, _ in classes))
+    return out
+
+
+def fused_step_phases(s, pos, tok, n_layer):
+    """the one-launch step at position pos, timed from inside by workgroup 0's wall-clock stamps: per phase (qkv,
+    attention, merge, o, gate/up, down) the wait for its input (from the previous phase's output written) and its own
+    work (to its output written), µs averaged over the layers; and the step as a graph alone (profile_step)"""
+    s.rewind(pos)
+    us = s.profile_fused_step(tok)
+    d = np.diff(us).reshape(n_layer, 12)
+    names = ["qkv", "attention", "merge", "o", "gate_up", "down"]
+    out = {"position": pos, "keys": pos + 1, "kernel_us": float(us[-1])}
+    for i, n in enumerate(names):
+        out[n + "_wait_us"] = float(d[:, 2 * i].mean())
+        out[n + "_work_us"] = float(d[:, 2 * i + 1].mean())
+    out["layer_us"] = float(d.sum(1).mean())
+    out["step_in_graph_us"] = s.profile_step(htr.STEP_ALL, 16, 20) * 1e3 if GRAPHS else float("nan")
+    log("one-launch step (µs a layer): " + ", ".join(f"{n} wait {out[n + '_wait_us']:.2f} work {out[n + '_work_us']:.2f}"
+                                                   for n in names) + f"; kernel {out['kernel_us']:.1f} µs")
     return out
 
 

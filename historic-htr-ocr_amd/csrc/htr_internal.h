@@ -255,3 +255,32 @@ int launch_gelu(htr_device *dev, hipStream_t st, float *x, size_t n);
 // x f32 [m][k] → f16 rows of nseg segments of kp values: hi = f16(x), or lo = f16(x − hi) in the segments of lo_mask
 int launch_split_f16(htr_device *dev, hipStream_t st, const float *x, int m, int k, int kp, int nseg, int lo_mask,
                      _Float16 *out);
+
+// the decode step of the 1024 / 2048 / 3072 decoder as one launch per token (token_step.hip)
+struct TokLayer {
+    const int8_t *q[7];  // quant planes: q, k, v, o, gate, up, down
+    const _Float16 *d[7];  // their scale planes
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm;
+    _Float16 *kc, *vc;  // the layer's f16 caches [n_kv][n_ctx][128]
+};
+struct TokArgs {
+    const TokLayer *layers;  // device table, one entry a layer
+    int n_layer, n_ctx, n_vocab;
+    const int8_t *emb_q;
+    const _Float16 *emb_d;
+    const uint32_t *tok;  // the token (device)
+    const int *state;     // state[0]: its position
+    const float *rope;    // [n_ctx][64] (cos, sin)
+    float eps, scale;
+    uint64_t *xw;         // exchange words (token_step_words of them)
+    uint32_t *seq, *err;  // the session's token counter (tags); set when a wait ran past spin_ticks
+    float *x_out;         // the residual after the last layer
+    unsigned long long *prof;  // optional: workgroup 0's wall-clock stamps, 1 + 12·n_layer of them
+    long long spin_ticks;      // a wait's limit in wall-clock ticks
+};
+size_t token_step_words();
+int token_step_ni(int n_ctx);  // keys a thread of the attention phase, 0 past 8192 rows
+bool token_step_shape(const htr_text_config &c);
+// 1 when the launch's 256 workgroups fit the device at once for this cache length, else 0 with the reason
+int token_step_fits(htr_device *dev, int n_ctx, const char **why);
+int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArgs &a);

@@ -9,7 +9,9 @@
 // Position and history length live in device memory (state[0] = pos, state[1] = len), so one captured HIP graph of
 // `chunk` steps is replayed for the whole read: the choice kernel advances both, the next step's embed reads the
 // chosen token from device memory. Only the chosen ids (4 bytes a token) come back to the host.
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <vector>
@@ -70,6 +72,14 @@ struct htr_session {
     void *kvb = nullptr;
     size_t kvb_bytes = 0;
     size_t pre_cap = 0;
+    // the one-launch step (token_step.hip) for the 1024 / 2048 / 3072 decoder: its layer table, exchange words and
+    // [seq, err] words; `fused` selects it for the decode step (fused_why: why it cannot be, when it cannot)
+    TokLayer *tl = nullptr;
+    uint64_t *xw = nullptr;
+    uint32_t *tseq = nullptr;
+    bool fused = false;
+    const char *fused_why = nullptr;
+    long long spin_ticks = 0;
 };
 
 struct htr_choice {
@@ -84,6 +94,7 @@ struct htr_choice {
     uint32_t *h_ids = nullptr;  // pinned [depth][chunk]
     std::vector<hipEvent_t> events;
     hipGraphExec_t g_first = nullptr, g_one = nullptr, g_chunk = nullptr;
+    bool graphs_fused = false;  // the step form the graphs were captured with
 };
 
 namespace {
@@ -151,6 +162,99 @@ int record_step_f32(htr_session *s, hipStream_t st) {
     return launch_dmv(dev, st, DMV_PLAIN, &head, 1, c.dim, s->h, nullptr, 0.0f, s->logits, 0);
 }
 
+TokArgs token_args(htr_session *s, unsigned long long *prof) {
+    const htr_text_config &c = s->m->cfg;
+    TokArgs a{};
+    a.layers = s->tl;
+    a.n_layer = c.n_layer;
+    a.n_ctx = s->n_ctx;
+    a.n_vocab = c.n_vocab;
+    a.emb_q = s->m->tok_embd->q;
+    a.emb_d = s->m->tok_embd->d;
+    a.tok = s->tok;
+    a.state = s->state;
+    a.rope = s->rope;
+    a.eps = c.eps;
+    a.scale = 1.0f / sqrtf((float)HEAD);
+    a.xw = s->xw;
+    a.seq = s->tseq;
+    a.err = s->tseq + 1;
+    a.x_out = s->x;
+    a.prof = prof;
+    a.spin_ticks = s->spin_ticks;
+    return a;
+}
+
+// the one-launch step's pieces for a session of the 1024 / 2048 / 3072 decoder on the f16 paths: the layer table (the
+// model's planes, the session's caches), the exchange words (zero: no tag of a token), seq = 1, err = 0. Sets
+// s->fused_why instead when the session cannot take it.
+int token_step_setup(htr_session *s) {
+    htr_text_model *m = s->m;
+    htr_device *dev = s->dev;
+    const htr_text_config &c = m->cfg;
+    if (m->compute != HTR_COMPUTE_F16) {
+        s->fused_why = "the F32 path runs the reference's own kernel sequence";
+        return 0;
+    }
+    if (!token_step_shape(c)) {
+        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128)";
+        return 0;
+    }
+    if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;
+    std::vector<TokLayer> tl(c.n_layer);
+    for (int i = 0; i < c.n_layer; i++) {
+        const Layer &l = m->layers[i];
+        const htr_weight *w[7] = {l.q, l.k, l.v, l.o, l.gate, l.up, l.down};
+        for (int k = 0; k < 7; k++) {
+            tl[i].q[k] = w[k]->q;
+            tl[i].d[k] = w[k]->d;
+        }
+        tl[i].attn_norm = l.attn_norm;
+        tl[i].q_norm = l.q_norm;
+        tl[i].k_norm = l.k_norm;
+        tl[i].ffn_norm = l.ffn_norm;
+        tl[i].kc = (_Float16 *)(s->kc + i * s->kv_layer);
+        tl[i].vc = (_Float16 *)(s->vc + i * s->kv_layer);
+    }
+    HTR_TRY(htr_dev_alloc(dev, tl.size() * sizeof(TokLayer), HTR_MEM_WORK, (void **)&s->tl));
+    HTR_TRY(htr_upload(dev, s->tl, tl.data(), tl.size() * sizeof(TokLayer)));
+    const size_t xbytes = token_step_words() * 8;
+    HTR_TRY(htr_dev_alloc(dev, xbytes, HTR_MEM_WORK, (void **)&s->xw));
+    HTR_TRY(htr_hip(dev, hipMemsetAsync(s->xw, 0, xbytes, dev->stream), "hipMemsetAsync"));
+    HTR_TRY(htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->tseq));
+    const uint32_t init[2] = {1, 0};
+    HTR_TRY(htr_upload(dev, s->tseq, init, sizeof init));
+    // a wait's limit: 0.2 s of the device's wall clock (a hand-over takes microseconds)
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev->ordinal) != hipSuccess || khz <= 0)
+        khz = 100000;
+    s->spin_ticks = (long long)khz * 200;
+    // HTR_FUSED_SPIN_US: another limit, in µs (tests of the error path set a tiny one: every wait then runs out)
+    if (const char *e = getenv("HTR_FUSED_SPIN_US")) {
+        const long long us = atoll(e);
+        if (us > 0) s->spin_ticks = std::max(1LL, (long long)khz * us / 1000);
+    }
+    s->fused = true;
+    return 0;
+}
+
+// after a one-launch step ran (the stream synchronised): its err word, cleared for the next call
+int token_step_check(htr_session *s) {
+    if (!s->tl) return 0;
+    uint32_t err = 0;
+    HTR_TRY(htr_download(s->dev, &err, s->tseq + 1, 4));
+    if (!err) return 0;
+    // a workgroup that ran out of time may have started after workgroup 0 advanced seq and tagged its words with the
+    // next token's seq: skip that one as well, and clear err
+    uint32_t w[2];
+    HTR_TRY(htr_download(s->dev, w, s->tseq, sizeof w));
+    w[0] += 1;
+    w[1] = 0;
+    HTR_TRY(htr_upload(s->dev, s->tseq, w, sizeof w));
+    return htr_fail("decode step: a workgroup of the one-launch step waited past its limit (the 256 workgroups did not "
+                    "all run at once); the step's logits and cache rows are invalid");
+}
+
 // one decode step on the session's stream: token s->tok at position state[0] → s->logits. The f16 paths' fused step
 // (record_step, text.rs:540-552 + layers_fused), or the F32 path's (record_step_f32) for a model of that path.
 // `only` (the in-graph timing of htr_session_profile_step) records just the kernels of the HTR_STEP_* classes it
@@ -161,6 +265,11 @@ int record_step(htr_session *s, hipStream_t st, unsigned only = HTR_STEP_ALL) {
     const htr_text_config &c = m->cfg;
     const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const float scale = 1.0f / sqrtf((float)HEAD);
+    if (s->fused && only == HTR_STEP_ALL) {
+        HTR_TRY(launch_decode_token(dev, st, s->n_ctx, token_args(s, nullptr)));
+        DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
+        return launch_dmv(dev, st, DMV_NORM, &head, 1, c.dim, s->x, m->output_norm, c.eps, s->logits, 0);
+    }
     if (only & HTR_STEP_EMBED) HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
     if (m->compute == HTR_COMPUTE_F32) return record_step_f32(s, st);
     for (int li = 0; li < c.n_layer; li++) {
@@ -458,7 +567,8 @@ extern "C" int htr_session_free(htr_session *s) {
     if (s->step_graph) hipGraphExecDestroy(s->step_graph);
     for (void *p : {(void *)s->kc, (void *)s->vc, (void *)s->rope, (void *)s->x, (void *)s->qkv, (void *)s->attn,
                     (void *)s->g, (void *)s->logits, (void *)s->tok, (void *)s->state, (void *)s->asc.part,
-                    (void *)s->asc.counters, s->pre, s->kvb, (void *)s->h, (void *)s->u})
+                    (void *)s->asc.counters, s->pre, s->kvb, (void *)s->h, (void *)s->u, (void *)s->tl, (void *)s->xw,
+                    (void *)s->tseq})
         if (p) htr_dev_free(dev, p);
     delete s;
     return 0;
@@ -500,6 +610,12 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
     if (rc == 0)
         rc = htr_dev_alloc(dev, attn_part_bytes(c.n_head, s->asc.max_chunk), HTR_MEM_WORK, (void **)&s->asc.part);
     if (rc == 0) rc = htr_dev_alloc(dev, attn_counter_bytes(c.n_kv), HTR_MEM_WORK, (void **)&s->asc.counters);
+    if (rc == 0) rc = token_step_setup(s);
+    if (rc == 0 && s->fused) {
+        // HTR_FUSED_STEP=0 keeps the per-kernel step (A/B timing); htr_session_set_fused_step switches per session
+        const char *env = getenv("HTR_FUSED_STEP");
+        if (env && env[0] == '0') s->fused = false;
+    }
     if (rc == 0) rc = htr_sync(dev);
     if (rc < 0) {
         std::string keep = htr_last_error();
@@ -540,6 +656,57 @@ extern "C" int htr_session_rewind(htr_session *s, size_t n_past) {
     if (!s) return htr_fail("htr_session_rewind: null session");
     if (n_past > (size_t)s->n_past) return htr_fail("rewind to %zu: the session is at %d", n_past, s->n_past);
     s->n_past = (int)n_past;
+    return 0;
+}
+
+extern "C" int htr_session_set_fused_step(htr_session *s, int on) {
+    if (!s) return htr_fail("htr_session_set_fused_step: null session");
+    if (on && !s->tl) return htr_fail("the one-launch decode step is not available: %s", s->fused_why);
+    if (s->fused != (on != 0) && s->step_graph) {  // captured with the other step form
+        hipGraphExecDestroy(s->step_graph);
+        s->step_graph = nullptr;
+    }
+    s->fused = on != 0;
+    return 0;
+}
+
+extern "C" int htr_session_fused_step(htr_session *s, int *on, const char **why_not) {
+    if (!s || !on) return htr_fail("htr_session_fused_step: null argument");
+    *on = s->fused ? 1 : 0;
+    if (why_not) *why_not = s->tl ? nullptr : s->fused_why;
+    return 0;
+}
+
+// one one-launch step at the session's position (not advanced; its KV row is written there), timed from inside:
+// workgroup 0's wall-clock stamps, as microseconds after the first (after the embed): per layer 12 — the input of A
+// (qkv) taken, A's output written, B's input (the KV head's q / k / v rows) taken, B's partials written, C's partials
+// taken, C's output written, D's input taken, D's output written, E's, E's, F's, F's
+extern "C" int htr_session_profile_fused_step(htr_session *s, int32_t token, double *us, int n) {
+    if (!s || !us) return htr_fail("htr_session_profile_fused_step: null argument");
+    htr_device *dev = s->dev;
+    HTR_TRY(htr_check_alive(dev));
+    HTR_TRY(htr_check_not_capturing(dev, "htr_session_profile_fused_step"));
+    if (!s->tl) return htr_fail("the one-launch decode step is not available: %s", s->fused_why);
+    const int n_stamp = 1 + 12 * s->m->cfg.n_layer;
+    if (n != n_stamp) return htr_fail("htr_session_profile_fused_step: %d stamps asked, the step makes %d", n, n_stamp);
+    if (s->n_past >= s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
+    if (token < 0 || token >= s->m->cfg.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
+    uint32_t t = (uint32_t)token;
+    HTR_TRY(htr_upload(dev, s->tok, &t, 4));
+    HTR_TRY(set_state(s, s->n_past, 0));
+    unsigned long long *prof = nullptr;
+    HTR_TRY(htr_dev_alloc(dev, (size_t)n_stamp * 8, HTR_MEM_WORK, (void **)&prof));
+    int rc = launch_decode_token(dev, dev->stream, s->n_ctx, token_args(s, prof));
+    if (rc == 0) rc = htr_sync(dev);
+    if (rc == 0) rc = token_step_check(s);
+    std::vector<unsigned long long> st(n_stamp);
+    if (rc == 0) rc = htr_download(dev, st.data(), prof, (size_t)n_stamp * 8);
+    htr_dev_free(dev, prof);
+    if (rc < 0) return rc;
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev->ordinal) != hipSuccess || khz <= 0)
+        khz = 100000;
+    for (int i = 0; i < n_stamp; i++) us[i] = (double)(long long)(st[i] - st[0]) * 1000.0 / (double)khz;
     return 0;
 }
 
@@ -709,6 +876,7 @@ extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
     HTR_TRY(set_state(s, s->n_past, 0));
     HTR_TRY(run_steps(s, nullptr, 1, true, &s->step_graph));
     HTR_TRY(htr_sync(dev));
+    if (s->fused) HTR_TRY(token_step_check(s));
     s->n_past += 1;
     if (h_logits) HTR_TRY(htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4));
     return 0;
@@ -797,6 +965,14 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         return htr_fail("%zu choices need %zu positions, the session holds %d", max, s->n_past + max - 1, s->n_ctx);
     hipStream_t st = dev->stream;
     HTR_TRY(set_state(s, s->n_past, ch->seed_len));
+    if (ch->graphs_fused != s->fused) {  // captured with the other step form
+        for (hipGraphExec_t *g : {&ch->g_first, &ch->g_one, &ch->g_chunk})
+            if (*g) {
+                hipGraphExecDestroy(*g);
+                *g = nullptr;
+            }
+        ch->graphs_fused = s->fused;
+    }
 
     struct Pending {
         size_t slot, n;
@@ -851,6 +1027,7 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         }
     }
     if (rc == 0) rc = htr_sync(dev);
+    if (rc == 0 && s->fused) rc = token_step_check(s);
     if (rc < 0) return rc;
     // the steps launched: every choice but the first of the read advanced the position by one
     s->n_past += (int)(next - 1);

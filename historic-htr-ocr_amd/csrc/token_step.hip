@@ -1,0 +1,663 @@
+// The decode step of the 1024-dim decoder (LightOnOCR's text model: dim 1024, 16 q / 8 KV heads of 128, SwiGLU 3072)
+// as ONE launch per token: embed → 28 × (qkv, attention, merge, o, gate/up, down) → the residual for the LM head.
+//
+// Reference semantics: the f16 paths' fused step, text.rs:540-552 + layers_fused (text.rs:630-647): dmv_qkv.wgsl
+// (attn_norm fused), qkv_post.wgsl (per-head norms, RoPE NEOX, f16 KV store), attn_decode.wgsl + attn_merge.wgsl
+// (q·scale, f32 softmax), dmv.wgsl (o, down: + residual), dmv_ffn.wgsl (ffn_norm, SwiGLU), embed_q8_0.wgsl. The same
+// arithmetic as the per-kernel step of q8_0.hip / attention.hip (dot16 group sums times the block scale, wave sums,
+// the fused attention's butterfly and softmax); only the split-K merge sums its chunks in another order.
+//
+// Why one launch: at batch 1 every projection is a few MB spread over 256 CUs, so a kernel of the per-kernel step
+// spends most of its time in the launch itself and in the first load's latency; a layer is 5 such launches. Here
+// 256 workgroups (one a CU, all resident together) run every phase of the token, and each phase hands its outputs
+// to the next through an exchange area instead of a kernel boundary:
+//
+//   words     every value handed over is one 64-bit word, the f32 value in the low half and a tag in the high half,
+//             stored and loaded as one agent-scope 64-bit atomic (single-copy atomic: a reader sees the old word or the
+//             new one, never half of each). A reader polls its words until each carries the tag it expects, so the
+//             value arrives with its own proof of being current: no flag, no fence, no counter. Tags are
+//             seq·256 + (6·layer + exchange): seq counts the session's tokens (read by every workgroup at start,
+//             advanced by workgroup 0 at the end, after every workgroup has read it), so no tag repeats within 2^24
+//             tokens, and every word a phase reads is rewritten every token (idle attention workgroups write empty
+//             partials), so a stale word is at most one token old;
+//   phases   A qkv (16 rows a workgroup, attn_norm fused) → B attention (workgroup = KV head × chunk of C keys,
+//            32 a KV head; the q / k norms, RoPE and the new KV row made from the exchanged raw rows) → C merge (each
+//            workgroup 8 dims of one q head over the head's chunks) → D o (4 rows, + residual) → E gate / up
+//            (12 + 12 rows, ffn_norm, SwiGLU) → F down (4 rows, + residual) → A of the next layer;
+//   overlap  a phase issues its weight loads (and B its K / V loads) first, then waits for its input: the HBM latency
+//            of the weights runs under the hand-over's;
+//   reuse    one word area per exchange, rewritten every layer. A workgroup writes exchange e of layer l + 1 only after
+//            it has read inputs that every workgroup produced after reading exchange e of layer l (checked per
+//            exchange in the comment of k_decode_token), so no word is overwritten before all its readers are done;
+//   waits    every wait is bounded by the wall clock: past `spin_ticks` the thread sets *err, stops waiting for the
+//            rest of the launch and the launch runs out (wrong values, no hang). The host refuses the path unless the
+//            256 workgroups fit the device at once, and reports *err after the step.
+#include "htr_internal.h"
+#include "wave.h"
+
+namespace {
+
+constexpr int NWG = 256;  // workgroups, all resident together
+constexpr int TPB = 256;  // threads a workgroup
+constexpr int D = 128;    // head dim
+constexpr int DIM = 1024, QD = 2048, KVD = 1024, NFF = 3072, NQKV = QD + 2 * KVD;
+constexpr int NKV = KVD / D;       // 8
+constexpr int WPK = NWG / NKV;     // 32 workgroups a KV head
+constexpr int XPL = 6;             // exchanges a layer
+constexpr int PART_W = 2 * (D + 2);  // a chunk's partials: two heads × (m, l, o[128])
+// word offsets of the exchanges
+constexpr int OFF_QKV = 0;
+constexpr int OFF_PART = OFF_QKV + NQKV;
+constexpr int OFF_ATT = OFF_PART + NWG * PART_W;
+constexpr int OFF_H1 = OFF_ATT + QD;
+constexpr int OFF_FF = OFF_H1 + DIM;
+constexpr int OFF_H2 = OFF_FF + NFF;
+constexpr int XWORDS = OFF_H2 + DIM;
+static_assert(NQKV / NWG == 16 && DIM / NWG == 4 && NFF / NWG == 12, "rows a workgroup");
+
+typedef int gint4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld16_stream(const void *p) {
+    const gint4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) gint4 *)(uintptr_t)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+typedef float gfloat4 __attribute__((ext_vector_type(4)));
+// global loads (pointers read from the layer table have lost their address space: these are not flat loads)
+__device__ __forceinline__ float4 ld16f(const float *p) {
+    const gfloat4 v = *(const __attribute__((address_space(1))) gfloat4 *)(uintptr_t)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float ld_half(const _Float16 *p) {
+    return (float)*(const __attribute__((address_space(1))) _Float16 *)(uintptr_t)p;
+}
+__device__ __forceinline__ uint64_t ld_word(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_word(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float dot16(const int4 q, const float *x) {
+    const int w[4] = {q.x, q.y, q.z, q.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) s = fmaf((float)(int8_t)(w[i] >> (8 * b)), x[4 * i + b], s);
+    return s;
+}
+
+__device__ __forceinline__ void unpack8(const int4 w, float (&f)[8]) {
+    const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        _Float16 lo, hi;
+        const uint16_t a = (uint16_t)(u[i] & 0xffff), b = (uint16_t)(u[i] >> 16);
+        __builtin_memcpy(&lo, &a, 2);
+        __builtin_memcpy(&hi, &b, 2);
+        f[2 * i] = (float)lo;
+        f[2 * i + 1] = (float)hi;
+    }
+}
+__device__ __forceinline__ int4 pack8(const float (&f)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const _Float16 lo = (_Float16)f[2 * i], hi = (_Float16)f[2 * i + 1];
+        uint16_t a, b;
+        __builtin_memcpy(&a, &lo, 2);
+        __builtin_memcpy(&b, &hi, 2);
+        u[i] = (uint32_t)a | ((uint32_t)b << 16);
+    }
+    return make_int4((int)u[0], (int)u[1], (int)u[2], (int)u[3]);
+}
+
+struct Waiter {
+    long long limit;  // wall-clock ticks a wait may take
+    uint32_t *err;
+    bool broken;  // this thread ran out of time once: it waits no more in this launch
+    int polls;    // of the current wait
+    // true when the wait that began at t0 (0: not yet) has run out — past the limit on the wall clock, or past 2^22
+    // polls (seconds: each is a memory round trip) should the clock not advance; then err is set and the thread waits
+    // no more
+    __device__ __forceinline__ bool expired(long long &t0) {
+        const long long now = wall_clock64();
+        if (t0 == 0) {
+            t0 = now;
+            polls = 0;
+            return false;
+        }
+        if (now - t0 <= limit && ++polls < (1 << 22)) return false;
+        broken = true;
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+};
+
+// The NP words idx = tid + 256·k (k < NP, idx < n) of src, each once it carries `tag`, → dst[idx] (LDS); then a
+// workgroup barrier. The first loads of every word go out together; a word that is not there yet is loaded again
+// until it is, or until the wall clock passes the limit.
+template <int NP>
+__device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uint32_t tag, float *dst) {
+    const int tid = threadIdx.x;
+    uint64_t v[NP];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int idx = tid + TPB * k;
+        v[k] = idx < n ? ld_word(src + idx) : (uint64_t)tag << 32;
+    }
+    long long t0 = 0;
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < NP; k++) all = all && (uint32_t)(v[k] >> 32) == tag;
+        if (all || wt.broken || wt.expired(t0)) break;
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int idx = tid + TPB * k;
+            if ((uint32_t)(v[k] >> 32) != tag) v[k] = ld_word(src + idx);
+        }
+    }
+    __syncthreads();  // the previous readers of dst are done
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int idx = tid + TPB * k;
+        if (idx < n) dst[idx] = __uint_as_float((uint32_t)v[k]);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void stamp(unsigned long long *prof, int at) {
+    if (prof && blockIdx.x == 0 && threadIdx.x == 0) prof[at] = (unsigned long long)wall_clock64();
+}
+
+// the fused RMS norm of a lane's 16·NG inputs (the wave holds all K of them): x·1/sqrt(Σx²/K + eps)·w
+template <int NG>
+__device__ __forceinline__ void norm16(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k, int lane) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) s = fmaf(xv[i][e], xv[i][e], s);
+    const float scale = 1.0f / sqrtf(wave_sum(s, lane) / (float)k + eps);
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) xv[i][e] = (xv[i][e] * scale) * wv[i][e];
+}
+
+// lane's inputs x[16g … 16g + 15], g = lane + 64·i, from LDS
+template <int NG> __device__ __forceinline__ void lds_x(float (&xv)[NG][16], const float *s, int lane) {
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 v = *reinterpret_cast<const float4 *>(s + 16 * (lane + 64 * i) + 4 * q);
+            xv[i][4 * q] = v.x, xv[i][4 * q + 1] = v.y, xv[i][4 * q + 2] = v.z, xv[i][4 * q + 3] = v.w;
+        }
+}
+template <int NG> __device__ __forceinline__ void glob_x(float (&xv)[NG][16], const float *s, int lane) {
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 v = ld16f(s + 16 * (lane + 64 * i) + 4 * q);
+            xv[i][4 * q] = v.x, xv[i][4 * q + 1] = v.y, xv[i][4 * q + 2] = v.z, xv[i][4 * q + 3] = v.w;
+        }
+}
+
+// a row's quants and scales for the lane's groups g = lane + 64·i of a K = 1024·NG matrix (repacked planes)
+template <int NG> struct RowW {
+    int4 q[NG];
+    float d[NG];
+};
+template <int NG> __device__ __forceinline__ void row_issue(RowW<NG> &r, const int8_t *q, const _Float16 *d, int row,
+                                                            int lane) {
+    constexpr int K = 1024 * NG;
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = lane + 64 * i;
+        r.q[i] = ld16_stream(q + (size_t)row * K + 16 * g);
+        r.d[i] = ld_half(d + (size_t)row * (K / 32) + (g >> 1));
+    }
+}
+template <int NG> __device__ __forceinline__ float row_dot(const RowW<NG> &r, const float (&xv)[NG][16]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NG; i++) s = fmaf(dot16(r.q[i], xv[i]), r.d[i], s);
+    return s;
+}
+
+// the q / k norm and RoPE NEOX of one head's raw row (LDS) for the 8 dims 8j … 8j + 7 (partners in slice j ^ 8; the
+// 16 lanes j of a lane row hold the head: Σx² over them), rope pairs cs of indices 8(j % 8) … + 7
+// nw: the norm weights of those dims and of the partner dims (NormW, loaded before the wait)
+struct NormW {
+    float4 a[2], b[2];
+    __device__ __forceinline__ void issue(const float *w, int j) {
+        a[0] = ld16f(w + 8 * j), a[1] = ld16f(w + 8 * j + 4);
+        b[0] = ld16f(w + 8 * (j ^ 8)), b[1] = ld16f(w + 8 * (j ^ 8) + 4);
+    }
+};
+__device__ __forceinline__ void head_post(const float *raw, const NormW &nw, const float (&cs)[16], int j, int lane,
+                                          float eps, float (&out)[8]) {
+    const int jp = j ^ 8;
+    float a8[8], b8[8];
+    const float wa[8] = {nw.a[0].x, nw.a[0].y, nw.a[0].z, nw.a[0].w, nw.a[1].x, nw.a[1].y, nw.a[1].z, nw.a[1].w};
+    const float wb[8] = {nw.b[0].x, nw.b[0].y, nw.b[0].z, nw.b[0].w, nw.b[1].x, nw.b[1].y, nw.b[1].z, nw.b[1].w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        a8[e] = raw[8 * j + e];
+        b8[e] = raw[8 * jp + e];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss = fmaf(a8[e], a8[e], ss);
+    ss = group_sum<8>(ss, lane);
+    const float scale = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float ya = (a8[e] * scale) * wa[e], yb = (b8[e] * scale) * wb[e];
+        const float c = cs[2 * e], s = cs[2 * e + 1];
+        out[e] = j < 8 ? ya * c - yb * s : yb * s + ya * c;
+    }
+}
+
+// k_decode_token: grid 256 × 256 threads; NI: keys a thread in the attention (chunks of C = 16·NI keys, 32 a KV
+// head: n_ctx ≤ 512·NI).
+//
+// Reuse of the exchange words, layer l → l + 1 (each arrow: "waited for the words of"):
+//   QKV  written in A(l+1), read in B(l): A(l+1) waits for H2(l) from every workgroup, written after its D(l), which
+//        waited for every workgroup's C(l), which came after its B(l);
+//   PART written in B(l+1), read in C(l): B(l+1) follows A(l+1) → H2(l) of all → D(l) of all → C(l) of all;
+//   ATT  written in C(l+1), read in D(l): C(l+1) follows A(l+1) → H2(l) of all, each written after its D(l);
+//   H1   written in D(l+1), read in E(l): D(l+1) follows ATT of all → C(l+1) … A(l+1) of all → H2(l) of all, each
+//        written after its E(l);
+//   FF   written in E(l+1), read in F(l): E(l+1) follows H1(l+1) of all → D(l+1) → ATT of all → … → A(l+1) of all,
+//        each after its F(l) read;
+//   H2   written in F(l+1), read in A(l+1): F(l+1) follows FF(l+1) of all, each written after its A(l+1).
+template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const TokArgs a) {
+    constexpr int C = 16 * NI;
+    constexpr int N = 2 * NI;
+    constexpr int KL = C >= 64 ? C / 64 : 1;
+    __shared__ __attribute__((aligned(16))) float s_x[DIM];   // the residual, as of its last exchange
+    __shared__ __attribute__((aligned(16))) float s_v[NFF];   // an exchanged input (attention output, SwiGLU)
+    __shared__ __attribute__((aligned(16))) float s_raw[4][D];  // B: raw q (two heads), k, v rows of the KV head
+    __shared__ float s_sc[2][C];
+    __shared__ float s_pw[4][2][C];
+    __shared__ float s_lw[2];
+    __shared__ float s_o[4][2][D];
+    __shared__ float s_ml[2][WPK];
+    __shared__ float s_mo[WPK][8];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int w = blockIdx.x;
+    Waiter wt{a.spin_ticks, a.err, false, 0};
+    const int pos = *a.state;
+    if (pos < 0 || pos >= a.n_ctx) return;  // every workgroup alike (the host checks positions first)
+    const uint32_t seq = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    uint64_t *xw = a.xw;
+
+    // embed (every workgroup the whole row): x = dequant(token_embd[tok]); an id out of range leaves x as it was
+    {
+        const uint32_t id = *a.tok;
+        const int c = 4 * tid;
+        if (id < (uint32_t)a.n_vocab) {
+            const char4 q4 = *reinterpret_cast<const char4 *>(a.emb_q + (size_t)id * DIM + c);
+            const float d = (float)a.emb_d[((size_t)id * DIM + c) >> 5];
+            s_x[c] = (float)q4.x * d, s_x[c + 1] = (float)q4.y * d, s_x[c + 2] = (float)q4.z * d,
+            s_x[c + 3] = (float)q4.w * d;
+        } else {
+            const float4 v = ld16f(a.x_out + c);
+            s_x[c] = v.x, s_x[c + 1] = v.y, s_x[c + 2] = v.z, s_x[c + 3] = v.w;
+        }
+        __syncthreads();
+    }
+    stamp(a.prof, 0);
+
+    const int kvh = w / WPK, cw = w % WPK, h0 = 2 * kvh;
+    const int n_keys = pos + 1, n_chunk = (n_keys + C - 1) / C;
+    const int j = tid & 15, kk = tid >> 4;
+
+    for (int l = 0; l < a.n_layer; l++) {
+        const TokLayer &L = a.layers[l];
+        const uint32_t tbase = seq * 256u + (uint32_t)(XPL * l);
+
+        // ---- A: q | k | v rows 16w … 16w + 15 (one matrix: the boundaries 2048, 3072 are multiples of 16), attn_norm
+        {
+            const int mat = w < QD / 16 ? 0 : w < (QD + KVD) / 16 ? 1 : 2;
+            const int lr0 = 16 * w - (mat == 0 ? 0 : mat == 1 ? QD : QD + KVD);
+            const int8_t *q = mat == 0 ? L.q[0] : mat == 1 ? L.q[1] : L.q[2];
+            const _Float16 *d = mat == 0 ? L.d[0] : mat == 1 ? L.d[1] : L.d[2];
+            RowW<1> rw[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) row_issue<1>(rw[r], q, d, lr0 + 4 * wave + r, lane);
+            float wv[1][16];
+            glob_x<1>(wv, L.attn_norm, lane);
+            if (l > 0) take<4>(wt, xw + OFF_H2, DIM, tbase - 1, s_x);  // F of the layer before
+            stamp(a.prof, 1 + 12 * l);
+            float xv[1][16];
+            lds_x<1>(xv, s_x, lane);
+            norm16<1>(xv, wv, a.eps, DIM, lane);
+            float acc[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = row_dot<1>(rw[r], xv);
+            const float v = wave_sum_rows<4>(acc, lane);
+            if ((lane & 15) == 0) put_word(xw + OFF_QKV + 16 * w + 4 * wave + (lane >> 4), v, tbase + 0);
+        }
+        stamp(a.prof, 2 + 12 * l);
+
+        // ---- B: attention of KV head kvh over keys cw·C … cw·C + C − 1
+        {
+            const bool busy = cw < n_chunk;  // uniform
+            const int k0 = cw * C;
+            const _Float16 *kb = L.kc + (size_t)kvh * a.n_ctx * D, *vb = L.vc + (size_t)kvh * a.n_ctx * D;
+            int4 kr[NI], vr[NI];
+            float4 rope4[4];
+            NormW qnw, knw;
+            if (busy) {
+#pragma unroll
+                for (int i = 0; i < NI; i++) kr[i] = ld16_stream(kb + (size_t)min(k0 + kk + 16 * i, pos) * D + 8 * j);
+#pragma unroll
+                for (int i = 0; i < NI; i++) vr[i] = ld16_stream(vb + (size_t)min(k0 + kk + 16 * i, pos) * D + 8 * j);
+                const float *rr = a.rope + (size_t)pos * D + 16 * (j & 7);
+#pragma unroll
+                for (int i = 0; i < 4; i++) rope4[i] = ld16f(rr + 4 * i);
+                qnw.issue(L.q_norm, j);
+                knw.issue(L.k_norm, j);
+                // the KV head's raw rows: q heads h0, h0 + 1, then k, v → s_raw (512 words, 2 a thread)
+                const uint64_t *src0 = xw + OFF_QKV;
+                uint64_t vv[2];
+                int at[2];
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const int idx = tid + TPB * k, part = idx >> 7, dd = idx & 127;
+                    at[k] = part < 2 ? (h0 + part) * D + dd : part == 2 ? QD + kvh * D + dd : QD + KVD + kvh * D + dd;
+                    vv[k] = ld_word(src0 + at[k]);
+                }
+                long long t0 = 0;
+                for (;;) {
+                    const bool all = (uint32_t)(vv[0] >> 32) == tbase && (uint32_t)(vv[1] >> 32) == tbase;
+                    if (all || wt.broken || wt.expired(t0)) break;
+#pragma unroll
+                    for (int k = 0; k < 2; k++)
+                        if ((uint32_t)(vv[k] >> 32) != tbase) vv[k] = ld_word(src0 + at[k]);
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < 2; k++) (&s_raw[0][0])[tid + TPB * k] = __uint_as_float((uint32_t)vv[k]);
+                __syncthreads();
+            }
+            stamp(a.prof, 3 + 12 * l);
+            if (busy) {
+                float cs[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    cs[4 * i] = rope4[i].x, cs[4 * i + 1] = rope4[i].y, cs[4 * i + 2] = rope4[i].z,
+                    cs[4 * i + 3] = rope4[i].w;
+                float ta[8], tb[8], kn8[8], v8[8], qa[8], qb[8];
+                head_post(s_raw[0], qnw, cs, j, lane, a.eps, ta);
+                head_post(s_raw[1], qnw, cs, j, lane, a.eps, tb);
+                head_post(s_raw[2], knw, cs, j, lane, a.eps, kn8);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    v8[e] = s_raw[3][8 * j + e];
+                    qa[e] = ta[e] * a.scale;
+                    qb[e] = tb[e] * a.scale;
+                }
+                const int4 knew = pack8(kn8), vnew = pack8(v8);
+                if (cw == pos / C && kk == 0) {  // the new row into the cache (no workgroup of this launch reads it)
+                    *reinterpret_cast<int4 *>(L.kc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = knew;
+                    *reinterpret_cast<int4 *>(L.vc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = vnew;
+                }
+                // scores: keys at or past pos take the new row (past pos they are masked below)
+                float v[N];
+#pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    float kf[8];
+                    unpack8(k0 + kk + 16 * i >= pos ? knew : kr[i], kf);
+                    float da = 0.0f, db = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        da = fmaf(qa[e], kf[e], da);
+                        db = fmaf(qb[e], kf[e], db);
+                    }
+                    v[2 * i] = da;
+                    v[2 * i + 1] = db;
+                }
+                if constexpr (N >= 16) {
+                    halve<N, 8, 4>(v, lane);
+#pragma unroll
+                    for (int r = 0; r < N / 16; r++) {
+                        const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
+                        const int key = kk + 16 * i;
+                        s_sc[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
+                    }
+                } else {
+                    constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;
+                    halve<N, 8, S>(v, lane);
+                    const float t = group_sum<(8 >> S)>(v[0], lane);
+                    if ((j & ((16 >> S) - 1)) == 0) {
+                        const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
+                        const int key = kk + 16 * i;
+                        s_sc[h][key] = k0 + key < n_keys ? t : -INFINITY;
+                    }
+                }
+                __syncthreads();
+                float l_h[2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float sv[KL], mx = -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < KL; i++) {
+                        const int key = lane + 64 * i;
+                        sv[i] = key < C ? s_sc[h][key] : -INFINITY;
+                        mx = fmaxf(mx, sv[i]);
+                    }
+                    mx = wave_max(mx, lane);
+                    float ls = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < KL; i++) {
+                        const int key = lane + 64 * i;
+                        const float p = expf(sv[i] - mx);
+                        if (key < C) s_pw[wave][h][key] = p;
+                        ls += p;
+                    }
+                    l_h[h] = wave_sum(ls, lane);
+                    if (wave == 0 && lane == 0) s_lw[h] = mx;
+                }
+                __builtin_amdgcn_wave_barrier();
+                float o[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) o[e] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    float vf[8];
+                    unpack8(k0 + kk + 16 * i >= pos ? vnew : vr[i], vf);
+                    const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        o[e] = fmaf(pa, vf[e], o[e]);
+                        o[8 + e] = fmaf(pb, vf[e], o[8 + e]);
+                    }
+                }
+                halve<16, 32, 2>(o, lane);
+                {
+                    const int base = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int idx = base + r, h = idx >> 3, e = idx & 7;
+                        s_o[wave][h][8 * j + e] = o[r];
+                    }
+                }
+                __syncthreads();
+                const int hh = tid >> 7, dd = tid & 127;
+                const float oc = (s_o[0][hh][dd] + s_o[1][hh][dd]) + (s_o[2][hh][dd] + s_o[3][hh][dd]);
+                uint64_t *pc = xw + OFF_PART + (size_t)w * PART_W + hh * (D + 2);
+                put_word(pc + 2 + dd, oc, tbase + 1);
+                if (dd == 0) put_word(pc, s_lw[hh], tbase + 1);
+                if (dd == 1) put_word(pc + 1, l_h[hh], tbase + 1);
+            } else {
+                // an idle chunk: empty partials (no reader merges them; written so every word stays current)
+                const int hh = tid >> 7, dd = tid & 127;
+                uint64_t *pc = xw + OFF_PART + (size_t)w * PART_W + hh * (D + 2);
+                put_word(pc + 2 + dd, 0.0f, tbase + 1);
+                if (dd == 0) put_word(pc, -INFINITY, tbase + 1);
+                if (dd == 1) put_word(pc + 1, 0.0f, tbase + 1);
+            }
+        }
+        stamp(a.prof, 4 + 12 * l);
+
+        // ---- C: merge — workgroup (kvh, cw) → head h0 + cw / 16, dims 8·(cw % 16) … + 7, over the head's n_chunk
+        // chunks: M = max m_c, w_c = e^(m_c − M), out = Σ o_c·w_c / Σ l_c·w_c
+        {
+            const int hh = cw >> 4, d0 = 8 * (cw & 15);
+            const uint64_t *pk = xw + OFF_PART + (size_t)(kvh * WPK) * PART_W + hh * (D + 2);
+            const int cc = tid >> 3, e = tid & 7;  // o word of chunk cc, dim d0 + e
+            const bool has_o = cc < n_chunk;
+            const int cm = tid >> 1;  // threads < 2·n_chunk: m (even) / l (odd) of chunk tid / 2
+            const bool has_m = tid < 2 * n_chunk;
+            uint64_t vo = has_o ? ld_word(pk + (size_t)cc * PART_W + 2 + d0 + e) : (uint64_t)(tbase + 1) << 32;
+            uint64_t vm = has_m ? ld_word(pk + (size_t)cm * PART_W + (tid & 1)) : (uint64_t)(tbase + 1) << 32;
+            long long t0 = 0;
+            for (;;) {
+                const bool all = (uint32_t)(vo >> 32) == tbase + 1 && (uint32_t)(vm >> 32) == tbase + 1;
+                if (all || wt.broken || wt.expired(t0)) break;
+                if ((uint32_t)(vo >> 32) != tbase + 1) vo = ld_word(pk + (size_t)cc * PART_W + 2 + d0 + e);
+                if ((uint32_t)(vm >> 32) != tbase + 1) vm = ld_word(pk + (size_t)cm * PART_W + (tid & 1));
+            }
+            if (has_o) s_mo[cc][e] = __uint_as_float((uint32_t)vo);
+            if (has_m) s_ml[tid & 1][cm] = __uint_as_float((uint32_t)vm);
+            __syncthreads();
+            stamp(a.prof, 5 + 12 * l);
+            if (wave == 0) {
+                // lane = chunk (n_chunk ≤ 32)
+                const float m = lane < n_chunk ? s_ml[0][lane] : -INFINITY;
+                const float M = wave_max(m, lane);
+                const float wc = lane < n_chunk ? expf(m - M) : 0.0f;
+                const float Lsum = wave_sum(lane < n_chunk ? s_ml[1][lane] * wc : 0.0f, lane);
+                float ov[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) ov[q] = lane < n_chunk ? s_mo[lane][q] * wc : 0.0f;
+                const float O = wave_sum_rows<8>(ov, lane);  // lane 8q holds dim q
+                if ((lane & 7) == 0) put_word(xw + OFF_ATT + (h0 + hh) * D + d0 + (lane >> 3), O / Lsum, tbase + 2);
+            }
+        }
+        stamp(a.prof, 6 + 12 * l);
+
+        // ---- D: o rows 4w + wave (K = 2048), + residual
+        {
+            const int row = 4 * w + wave;
+            RowW<2> rw;
+            row_issue<2>(rw, L.q[3], L.d[3], row, lane);
+            take<8>(wt, xw + OFF_ATT, QD, tbase + 2, s_v);
+            stamp(a.prof, 7 + 12 * l);
+            float xv[2][16];
+            lds_x<2>(xv, s_v, lane);
+            const float v = wave_sum(row_dot<2>(rw, xv), lane);
+            if (lane == 0) put_word(xw + OFF_H1 + row, s_x[row] + v, tbase + 3);
+        }
+        stamp(a.prof, 8 + 12 * l);
+
+        // ---- E: gate / up rows 12w + 3·wave + r (K = 1024), ffn_norm, SwiGLU
+        {
+            RowW<1> rg[3], ru[3];
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const int row = 12 * w + 3 * wave + r;
+                row_issue<1>(rg[r], L.q[4], L.d[4], row, lane);
+                row_issue<1>(ru[r], L.q[5], L.d[5], row, lane);
+            }
+            float wv[1][16];
+            glob_x<1>(wv, L.ffn_norm, lane);
+            take<4>(wt, xw + OFF_H1, DIM, tbase + 3, s_x);
+            stamp(a.prof, 9 + 12 * l);
+            float xv[1][16];
+            lds_x<1>(xv, s_x, lane);
+            norm16<1>(xv, wv, a.eps, DIM, lane);
+            float ag[4], au[4];
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                ag[r] = row_dot<1>(rg[r], xv);
+                au[r] = row_dot<1>(ru[r], xv);
+            }
+            ag[3] = 0.0f, au[3] = 0.0f;
+            const float g = wave_sum_rows<4>(ag, lane), u = wave_sum_rows<4>(au, lane);
+            if ((lane & 15) == 0 && (lane >> 4) < 3)
+                put_word(xw + OFF_FF + 12 * w + 3 * wave + (lane >> 4), (g / (1.0f + expf(-g))) * u, tbase + 4);
+        }
+        stamp(a.prof, 10 + 12 * l);
+
+        // ---- F: down rows 4w + wave (K = 3072), + residual
+        {
+            const int row = 4 * w + wave;
+            RowW<3> rw;
+            row_issue<3>(rw, L.q[6], L.d[6], row, lane);
+            take<12>(wt, xw + OFF_FF, NFF, tbase + 4, s_v);
+            stamp(a.prof, 11 + 12 * l);
+            float xv[3][16];
+            lds_x<3>(xv, s_v, lane);
+            const float v = wave_sum(row_dot<3>(rw, xv), lane);
+            const float xn = s_x[row] + v;
+            if (lane == 0) {
+                if (l + 1 < a.n_layer)
+                    put_word(xw + OFF_H2 + row, xn, tbase + 5);
+                else
+                    a.x_out[row] = xn;  // the LM head's input (read after this launch)
+            }
+        }
+        stamp(a.prof, 12 + 12 * l);
+    }
+    // every workgroup has read seq: workgroup 0 has waited for the last layer's FF words of all of them
+    if (w == 0 && tid == 0) __hip_atomic_store(a.seq, seq + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+size_t token_step_words() { return XWORDS; }
+
+int token_step_ni(int n_ctx) {
+    for (int ni = 2; ni <= 16; ni *= 2)
+        if (n_ctx <= 16 * ni * WPK) return ni;
+    return 0;
+}
+
+bool token_step_shape(const htr_text_config &c) {
+    return c.dim == DIM && c.n_head * c.d_head == QD && c.n_kv * c.d_head == KVD && c.n_ff == NFF && c.d_head == D &&
+           c.n_head == 2 * c.n_kv && c.n_layer * XPL + XPL <= 256;
+}
+
+int token_step_fits(htr_device *dev, int n_ctx, const char **why) {
+    const int ni = token_step_ni(n_ctx);
+    if (!ni) {
+        *why = "the cache is longer than 8192 rows";
+        return 0;
+    }
+    int per_cu = 0;
+    hipError_t e = hipSuccess;
+    switch (ni) {
+    case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_token<2>, TPB, 0); break;
+    case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_token<4>, TPB, 0); break;
+    case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_token<8>, TPB, 0); break;
+    default: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_token<16>, TPB, 0); break;
+    }
+    if (e != hipSuccess) {
+        *why = "the occupancy query failed";
+        return 0;
+    }
+    if (per_cu * dev->n_cu < NWG) {
+        *why = "its 256 workgroups do not fit the device at once";
+        return 0;
+    }
+    return 1;
+}
+
+int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArgs &a) {
+    switch (token_step_ni(n_ctx)) {
+    case 2: hipLaunchKernelGGL(k_decode_token<2>, dim3(NWG), dim3(TPB), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(k_decode_token<4>, dim3(NWG), dim3(TPB), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(k_decode_token<8>, dim3(NWG), dim3(TPB), 0, st, a); break;
+    case 16: hipLaunchKernelGGL(k_decode_token<16>, dim3(NWG), dim3(TPB), 0, st, a); break;
+    default: return htr_fail("decode token: a %d-row cache (at most 8192)", n_ctx);
+    }
+    return htr_launched(dev, "k_decode_token");
+}

@@ -36,7 +36,8 @@ SYMBOLS = [
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
-    "htr_graph_free", "htr_decode_attention_static", "htr_session_profile_step",
+    "htr_graph_free", "htr_decode_attention_static", "htr_session_profile_step", "htr_session_set_fused_step",
+    "htr_session_fused_step", "htr_session_profile_fused_step",
 ]
 STEP_EMBED, STEP_QKV, STEP_ATTENTION, STEP_O, STEP_FFN, STEP_DOWN, STEP_HEAD, STEP_ALL = 1, 2, 4, 8, 16, 32, 64, 127
 
@@ -173,6 +174,9 @@ def lib() -> C.CDLL:
             "htr_session_rewind": (i32, [vp, sz]),
             "htr_session_kv_cache": (i32, [vp, C.POINTER(KvViewC)]),
             "htr_session_profile_step": (i32, [vp, C.c_uint, i32, i32, C.POINTER(f32)]),
+            "htr_session_set_fused_step": (i32, [vp, i32]),
+            "htr_session_fused_step": (i32, [vp, C.POINTER(i32), C.POINTER(C.c_char_p)]),
+            "htr_session_profile_fused_step": (i32, [vp, i32, C.POINTER(C.c_double), i32]),
             "htr_debug_last_kernel": (i32, [vp, C.c_char_p, sz]),
             "htr_capture_begin": (i32, [vp]),
             "htr_capture_end": (i32, [vp, pp]),
@@ -686,6 +690,32 @@ class Session:
         ms = C.c_float()
         _check(lib().htr_session_profile_step(self.h, classes, n_steps, reps, C.byref(ms)))
         return ms.value
+
+    @property
+    def fused_step(self) -> bool:
+        """whether the decode step runs as one launch per token (the 1024 / 2048 / 3072 decoder on the f16 paths)"""
+        on, why = C.c_int(), C.c_char_p()
+        _check(lib().htr_session_fused_step(self.h, C.byref(on), C.byref(why)))
+        return bool(on.value)
+
+    @fused_step.setter
+    def fused_step(self, on: bool) -> None:
+        _check(lib().htr_session_set_fused_step(self.h, 1 if on else 0))
+
+    def fused_step_unavailable(self) -> str | None:
+        """why the one-launch step is not available to this session (None when it is)"""
+        on, why = C.c_int(), C.c_char_p()
+        _check(lib().htr_session_fused_step(self.h, C.byref(on), C.byref(why)))
+        return why.value.decode() if why.value else None
+
+    def profile_fused_step(self, tok: int) -> np.ndarray:
+        """one one-launch step of `tok` at n_past (not advanced): workgroup 0's stamps in µs after the embed,
+        [1 + 12·n_layer] (per layer: each phase's input taken and output written — qkv, attention, merge, o, ffn,
+        down)"""
+        n = 1 + 12 * self.m.cfg.n_layer
+        us = np.zeros(n, np.float64)
+        _check(lib().htr_session_profile_fused_step(self.h, int(tok), us.ctypes.data_as(C.POINTER(C.c_double)), n))
+        return us
 
     def kv_view(self) -> KvViewC:
         v = KvViewC()

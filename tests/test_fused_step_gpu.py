@@ -1,0 +1,201 @@
+"""The decode step as one launch per token (token_step.hip) against the per-kernel step and the oracle.
+
+The one-launch step computes what the per-kernel fused step computes (text.rs:540-552 + layers_fused,
+text.rs:630-647) with the same arithmetic, except that the split-K attention merge sums its chunks in another order.
+So: its KV rows of layer 0 are the per-kernel step's bit for bit (nothing before them differs), later layers' within
+f16 rounding; its logits are the per-kernel step's within 1e-5 rel-L2 and the oracle's (stepping from the same cache
+rows) within 2e-4 — the per-kernel step's own bar; its greedy tokens are the oracle's, teacher-forced, except logged
+near-ties (< 1e-6 relative). Positions cover the chunk edges of the attention phase (64 keys a chunk at n_ctx 2048: 1,
+64, 65, 128 keys), a long context (1024 keys) and the last row of the cache (2048 keys, every chunk of every KV head
+busy).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import htr
+import oracle as orc
+from helpers import near_tie, rel_l2, synth_text_model, to_htr_cfg
+
+pytestmark = pytest.mark.gpu
+
+N_LAYER, N_VOCAB, CTX = 3, 4096, 2048
+
+
+@pytest.fixture(scope="module")
+def small_decoder():
+    """the decoder's shape (dim 1024, 16 / 8 heads of 128, SwiGLU 3072) with 3 layers and a 4096-id vocabulary"""
+    return synth_text_model(n_layer=N_LAYER, n_vocab=N_VOCAB, seed=2024)
+
+
+@pytest.fixture(scope="module")
+def model(dev, small_decoder):
+    cfg, te, on, layers = small_decoder
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F16
+    try:
+        m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+    yield m
+    m.free()
+
+
+def hand_over(s, o, n, n_layer):
+    for li in range(n_layer):
+        k, v = s.kv_rows(li, 0, n)
+        o.set_kv(li, 0, k, v)
+    o.rewind(n)
+
+
+def test_fused_step_is_the_default_for_the_decoder_shape(dev, model):
+    s = model.session(CTX)
+    try:
+        if os.environ.get("HTR_FUSED_STEP", "1") != "0":
+            assert s.fused_step and s.fused_step_unavailable() is None
+        s.fused_step = False
+        assert not s.fused_step
+        s.fused_step = True
+        assert s.fused_step
+    finally:
+        s.free()
+
+
+def test_fused_step_refused_where_it_does_not_apply(dev):
+    """another shape (the tiny model): the per-kernel step, and the reason"""
+    from helpers import tiny_text_model
+
+    cfg, te, on, layers = tiny_text_model()
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F16
+    try:
+        m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+    s = m.session(64)
+    assert not s.fused_step and "1024 / 2048 / 3072" in s.fused_step_unavailable()
+    with pytest.raises(htr.HtrError, match="not available"):
+        s.fused_step = True
+    s.free()
+    m.free()
+
+
+def test_fused_step_refused_past_8192_rows(dev, model):
+    s = model.session(8193)
+    assert not s.fused_step and "8192" in s.fused_step_unavailable()
+    s.free()
+
+
+@pytest.mark.parametrize("n_past", [0, 63, 64, 127, 1023, CTX - 1])
+def test_fused_step_matches_per_kernel_step_and_oracle(dev, model, small_decoder, n_past):
+    cfg, te, on, layers = small_decoder
+    from htr import synth
+
+    prompt = synth.prompt_ids(77, CTX, N_VOCAB)
+    sf, sk = model.session(CTX), model.session(CTX)
+    sk.fused_step = False
+    assert sf.fused_step
+    print(f"\n[fused step] position {n_past} ({n_past + 1} keys)", flush=True)
+    for s in (sf, sk):
+        if n_past:
+            s.prefill(prompt[:n_past])
+    tok = int(prompt[n_past])
+    lf, lk = sf.step(tok), sk.step(tok)
+    e_k = rel_l2(lf, lk)
+    # layer 0's new rows: the same values; every layer's within f16 rounding
+    for li in range(N_LAYER):
+        kf, vf = sf.kv_rows(li, n_past, 1)
+        kk, vk = sk.kv_rows(li, n_past, 1)
+        if li == 0:
+            assert np.array_equal(kf, kk) and np.array_equal(vf, vk)
+        for a, b in ((kf, kk), (vf, vk)):
+            fa, fb = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
+            assert np.all(np.abs(fa - fb) <= 2e-3 * (1 + np.abs(fb))), li
+    o = orc.Session(cfg, te, on, layers, CTX, f16=True)
+    hand_over(sk, o, n_past, N_LAYER)
+    lo = o.step(tok)
+    e_o = rel_l2(lf, lo)
+    print(f"[fused step] rel-L2 vs the per-kernel step {e_k:.2e}, vs the oracle {e_o:.2e} "
+          f"(per-kernel vs oracle {rel_l2(lk, lo):.2e})", flush=True)
+    assert e_k < 1e-5
+    assert e_o < 2e-4
+    sf.free()
+    sk.free()
+
+
+def test_fused_decode_gpu_teacher_forced(dev, model, small_decoder):
+    """decode_gpu on the one-launch step (graph of [step, LM head, choice] × 16, 2 in flight) and on the per-kernel
+    step: 96 greedy tokens with rp 1.1 over 64 after a 700-token prompt, each the oracle's choice given the read's
+    earlier ones (near-ties logged)"""
+    cfg, te, on, layers = small_decoder
+    from htr import synth
+
+    prompt = synth.prompt_ids(91, 700, N_VOCAB)
+    new, rp, window = 96, 1.1, 64
+    reads = []
+    for fused in (True, False):
+        s = model.session(CTX)
+        s.fused_step = fused
+        s.prefill(prompt[:-1])
+        first = s.step(int(prompt[-1]))
+        ch = s.choice(htr.Preset(repetition_penalty=rp, repetition_window=window, max_new_tokens=new), prompt,
+                      chunk=16, depth=2)
+        toks = s.decode_gpu(ch, new)
+        assert len(toks) == new and s.n_past == len(prompt) + new - 1
+        o = orc.Session(cfg, te, on, layers, CTX, f16=True)
+        hand_over(s, o, len(prompt) - 1, N_LAYER)
+        ch.free()
+        s.free()
+        lo = o.step(int(prompt[-1]))
+        assert rel_l2(first, lo) < 2e-4
+        hist, ties = [int(t) for t in prompt], []
+        for i, t in enumerate(toks):
+            pen = lo.copy()
+            want = orc.choose(pen, rp, window, 0.0, hist)
+            if want != t:
+                assert near_tie(pen, want, t), f"{'fused' if fused else 'per-kernel'} token {i}: oracle {want}, GPU {t}"
+                ties.append(i)
+            hist.append(int(t))
+            if i + 1 < len(toks):
+                lo = o.step(int(t))
+        reads.append(list(toks))
+        print(f"\n[{'fused' if fused else 'per-kernel'} decode] {new} tokens teacher-forced, near-ties {ties}",
+              flush=True)
+    print(f"[decode] the two reads agree: {reads[0] == reads[1]}", flush=True)
+
+
+def test_fused_step_profile_stamps(dev, model):
+    from htr import synth
+
+    s = model.session(CTX)
+    s.prefill(synth.prompt_ids(5, 1279, N_VOCAB))
+    us = s.profile_fused_step(17)
+    assert us.shape == (1 + 12 * N_LAYER,) and us[0] == 0.0
+    assert np.all(np.diff(us) >= 0.0) and us[-1] < 1e4
+    print(f"\n[fused step] stamps (µs): {np.round(us, 2).tolist()}", flush=True)
+    assert s.n_past == 1279
+    s.free()
+
+
+def test_fused_step_reports_a_wait_that_ran_out(dev, model, monkeypatch):
+    """a 1 µs limit (HTR_FUSED_SPIN_US, read when the session is made): the waits run out, the launch still ends, and
+    the step reports it; with the normal limit the next session steps as before"""
+    from htr import synth
+
+    prompt = synth.prompt_ids(3, 40, N_VOCAB)
+    monkeypatch.setenv("HTR_FUSED_SPIN_US", "1")
+    s = model.session(CTX)
+    monkeypatch.delenv("HTR_FUSED_SPIN_US")
+    assert s.fused_step
+    s.prefill(prompt[:-1])
+    with pytest.raises(htr.HtrError, match="waited past its limit"):
+        s.step(int(prompt[-1]))
+    s.free()
+    s2, s3 = model.session(CTX), model.session(CTX)
+    s3.fused_step = False
+    for x in (s2, s3):
+        x.prefill(prompt[:-1])
+    assert rel_l2(s2.step(int(prompt[-1])), s3.step(int(prompt[-1]))) < 1e-5
+    s2.free()
+    s3.free()
