@@ -111,6 +111,12 @@ __device__ __forceinline__ int4 pack8(const float (&f)[8]) {
     return make_int4((int)u[0], (int)u[1], (int)u[2], (int)u[3]);
 }
 
+// A wait's first loads go out this long after the workgroup's own outputs (s_sleep units of 64 clocks: ≈ 0.4 µs):
+// the producers' words take about that long to become visible, and a first poll that comes back with old words
+// costs a whole round trip more. Measured on one MI355X at the 28-layer read (µs a token): no pause 482 … 488,
+// 8 → 465, 12 → 461, 16 → 460 … 469, 24 → 466, 32 → 479; two polls in flight instead (more traffic) 523.
+constexpr int POLL_SLEEP = 12;
+
 struct Waiter {
     long long limit;  // wall-clock ticks a wait may take
     uint32_t *err;
@@ -140,6 +146,7 @@ template <int NP>
 __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uint32_t tag, float *dst) {
     const int tid = threadIdx.x;
     uint64_t v[NP];
+    __builtin_amdgcn_s_sleep(POLL_SLEEP);
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int idx = tid + TPB * k;
@@ -166,8 +173,12 @@ __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uin
     __syncthreads();
 }
 
-__device__ __forceinline__ void stamp(unsigned long long *prof, int at) {
-    if (prof && blockIdx.x == 0 && threadIdx.x == 0) prof[at] = (unsigned long long)wall_clock64();
+// workgroup 0's wall-clock stamps, kept in LDS (a store to memory here would wait for the phase's own stores) and
+// written out at the end of the launch
+constexpr int MAX_LAYERS = 42;
+constexpr int N_STAMPS = 1 + 12 * MAX_LAYERS;
+__device__ __forceinline__ void stamp(unsigned long long *s_stamp, bool on, int at) {
+    if (on && threadIdx.x == 0) s_stamp[at] = (unsigned long long)wall_clock64();
 }
 
 // the fused RMS norm of a lane's 16·NG inputs (the wave holds all K of them): x·1/sqrt(Σx²/K + eps)·w
@@ -287,9 +298,11 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
     __shared__ float s_o[4][2][D];
     __shared__ float s_ml[2][WPK];
     __shared__ float s_mo[WPK][8];
+    __shared__ unsigned long long s_stamp[N_STAMPS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int w = blockIdx.x;
+    const bool prof_on = a.prof && w == 0;
     Waiter wt{a.spin_ticks, a.err, false, 0};
     const int pos = *a.state;
     if (pos < 0 || pos >= a.n_ctx) return;  // every workgroup alike (the host checks positions first)
@@ -312,7 +325,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
         }
         __syncthreads();
     }
-    stamp(a.prof, 0);
+    stamp(s_stamp, prof_on, 0);
 
     const int kvh = w / WPK, cw = w % WPK, h0 = 2 * kvh;
     const int n_keys = pos + 1, n_chunk = (n_keys + C - 1) / C;
@@ -334,7 +347,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             float wv[1][16];
             glob_x<1>(wv, L.attn_norm, lane);
             if (l > 0) take<4>(wt, xw + OFF_H2, DIM, tbase - 1, s_x);  // F of the layer before
-            stamp(a.prof, 1 + 12 * l);
+            stamp(s_stamp, prof_on, 1 + 12 * l);
             float xv[1][16];
             lds_x<1>(xv, s_x, lane);
             norm16<1>(xv, wv, a.eps, DIM, lane);
@@ -344,7 +357,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const float v = wave_sum_rows<4>(acc, lane);
             if ((lane & 15) == 0) put_word(xw + OFF_QKV + 16 * w + 4 * wave + (lane >> 4), v, tbase + 0);
         }
-        stamp(a.prof, 2 + 12 * l);
+        stamp(s_stamp, prof_on, 2 + 12 * l);
 
         // ---- B: attention of KV head kvh over keys cw·C … cw·C + C − 1
         {
@@ -368,6 +381,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 const uint64_t *src0 = xw + OFF_QKV;
                 uint64_t vv[2];
                 int at[2];
+                __builtin_amdgcn_s_sleep(POLL_SLEEP);
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
                     const int idx = tid + TPB * k, part = idx >> 7, dd = idx & 127;
@@ -387,7 +401,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 for (int k = 0; k < 2; k++) (&s_raw[0][0])[tid + TPB * k] = __uint_as_float((uint32_t)vv[k]);
                 __syncthreads();
             }
-            stamp(a.prof, 3 + 12 * l);
+            stamp(s_stamp, prof_on, 3 + 12 * l);
             if (busy) {
                 float cs[16];
 #pragma unroll
@@ -505,7 +519,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 if (dd == 1) put_word(pc + 1, 0.0f, tbase + 1);
             }
         }
-        stamp(a.prof, 4 + 12 * l);
+        stamp(s_stamp, prof_on, 4 + 12 * l);
 
         // ---- C: merge — workgroup (kvh, cw) → head h0 + cw / 16, dims 8·(cw % 16) … + 7, over the head's n_chunk
         // chunks: M = max m_c, w_c = e^(m_c − M), out = Σ o_c·w_c / Σ l_c·w_c
@@ -516,6 +530,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const bool has_o = cc < n_chunk;
             const int cm = tid >> 1;  // threads < 2·n_chunk: m (even) / l (odd) of chunk tid / 2
             const bool has_m = tid < 2 * n_chunk;
+            __builtin_amdgcn_s_sleep(POLL_SLEEP);
             uint64_t vo = has_o ? ld_word(pk + (size_t)cc * PART_W + 2 + d0 + e) : (uint64_t)(tbase + 1) << 32;
             uint64_t vm = has_m ? ld_word(pk + (size_t)cm * PART_W + (tid & 1)) : (uint64_t)(tbase + 1) << 32;
             long long t0 = 0;
@@ -528,7 +543,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             if (has_o) s_mo[cc][e] = __uint_as_float((uint32_t)vo);
             if (has_m) s_ml[tid & 1][cm] = __uint_as_float((uint32_t)vm);
             __syncthreads();
-            stamp(a.prof, 5 + 12 * l);
+            stamp(s_stamp, prof_on, 5 + 12 * l);
             if (wave == 0) {
                 // lane = chunk (n_chunk ≤ 32)
                 const float m = lane < n_chunk ? s_ml[0][lane] : -INFINITY;
@@ -542,7 +557,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 if ((lane & 7) == 0) put_word(xw + OFF_ATT + (h0 + hh) * D + d0 + (lane >> 3), O / Lsum, tbase + 2);
             }
         }
-        stamp(a.prof, 6 + 12 * l);
+        stamp(s_stamp, prof_on, 6 + 12 * l);
 
         // ---- D: o rows 4w + wave (K = 2048), + residual
         {
@@ -550,13 +565,13 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             RowW<2> rw;
             row_issue<2>(rw, L.q[3], L.d[3], row, lane);
             take<8>(wt, xw + OFF_ATT, QD, tbase + 2, s_v);
-            stamp(a.prof, 7 + 12 * l);
+            stamp(s_stamp, prof_on, 7 + 12 * l);
             float xv[2][16];
             lds_x<2>(xv, s_v, lane);
             const float v = wave_sum(row_dot<2>(rw, xv), lane);
             if (lane == 0) put_word(xw + OFF_H1 + row, s_x[row] + v, tbase + 3);
         }
-        stamp(a.prof, 8 + 12 * l);
+        stamp(s_stamp, prof_on, 8 + 12 * l);
 
         // ---- E: gate / up rows 12w + 3·wave + r (K = 1024), ffn_norm, SwiGLU
         {
@@ -570,7 +585,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             float wv[1][16];
             glob_x<1>(wv, L.ffn_norm, lane);
             take<4>(wt, xw + OFF_H1, DIM, tbase + 3, s_x);
-            stamp(a.prof, 9 + 12 * l);
+            stamp(s_stamp, prof_on, 9 + 12 * l);
             float xv[1][16];
             lds_x<1>(xv, s_x, lane);
             norm16<1>(xv, wv, a.eps, DIM, lane);
@@ -585,7 +600,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             if ((lane & 15) == 0 && (lane >> 4) < 3)
                 put_word(xw + OFF_FF + 12 * w + 3 * wave + (lane >> 4), (g / (1.0f + expf(-g))) * u, tbase + 4);
         }
-        stamp(a.prof, 10 + 12 * l);
+        stamp(s_stamp, prof_on, 10 + 12 * l);
 
         // ---- F: down rows 4w + wave (K = 3072), + residual
         {
@@ -593,7 +608,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             RowW<3> rw;
             row_issue<3>(rw, L.q[6], L.d[6], row, lane);
             take<12>(wt, xw + OFF_FF, NFF, tbase + 4, s_v);
-            stamp(a.prof, 11 + 12 * l);
+            stamp(s_stamp, prof_on, 11 + 12 * l);
             float xv[3][16];
             lds_x<3>(xv, s_v, lane);
             const float v = wave_sum(row_dot<3>(rw, xv), lane);
@@ -605,10 +620,14 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                     a.x_out[row] = xn;  // the LM head's input (read after this launch)
             }
         }
-        stamp(a.prof, 12 + 12 * l);
+        stamp(s_stamp, prof_on, 12 + 12 * l);
     }
     // every workgroup has read seq: workgroup 0 has waited for the last layer's FF words of all of them
     if (w == 0 && tid == 0) __hip_atomic_store(a.seq, seq + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prof_on) {
+        __syncthreads();
+        for (int i = tid; i <= 12 * a.n_layer; i += TPB) a.prof[i] = s_stamp[i];
+    }
 }
 
 }  // namespace
@@ -623,7 +642,7 @@ int token_step_ni(int n_ctx) {
 
 bool token_step_shape(const htr_text_config &c) {
     return c.dim == DIM && c.n_head * c.d_head == QD && c.n_kv * c.d_head == KVD && c.n_ff == NFF && c.d_head == D &&
-           c.n_head == 2 * c.n_kv && c.n_layer * XPL + XPL <= 256;
+           c.n_head == 2 * c.n_kv && c.n_layer <= MAX_LAYERS;
 }
 
 int token_step_fits(htr_device *dev, int n_ctx, const char **why) {
