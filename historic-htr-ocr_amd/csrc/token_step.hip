@@ -117,6 +117,10 @@ __device__ __forceinline__ int4 pack8(const float (&f)[8]) {
 // 8 → 465, 12 → 461, 16 → 460 … 469, 24 → 466, 32 → 479; two polls in flight instead (more traffic) 523.
 constexpr int POLL_SLEEP = 12;
 
+template <bool B> struct BoolC {
+    static constexpr bool value = B;
+};
+
 struct Waiter {
     long long limit;  // wall-clock ticks a wait may take
     uint32_t *err;
@@ -292,12 +296,13 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
     __shared__ __attribute__((aligned(16))) float s_x[DIM];   // the residual, as of its last exchange
     __shared__ __attribute__((aligned(16))) float s_v[NFF];   // an exchanged input (attention output, SwiGLU)
     __shared__ __attribute__((aligned(16))) float s_raw[4][D];  // B: raw q (two heads), k, v rows of the KV head
+    __shared__ __attribute__((aligned(16))) float s_post[3][D];  // B: q (× scale, two heads) and k, normed and roped
     __shared__ float s_sc[2][C];
     __shared__ float s_pw[4][2][C];
     __shared__ float s_lw[2];
     __shared__ float s_o[4][2][D];
     __shared__ float s_ml[2][WPK];
-    __shared__ float s_mo[WPK][8];
+    __shared__ __attribute__((aligned(16))) float s_mo[WPK][8];
     __shared__ unsigned long long s_stamp[N_STAMPS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -366,7 +371,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const _Float16 *kb = L.kc + (size_t)kvh * a.n_ctx * D, *vb = L.vc + (size_t)kvh * a.n_ctx * D;
             int4 kr[NI], vr[NI];
             float4 rope4[4];
-            NormW qnw, knw;
+            NormW hnw;  // the norm weights of this wave's head (waves 0, 1: q; 2: k)
             if (busy) {
 #pragma unroll
                 for (int i = 0; i < NI; i++) kr[i] = ld16_stream(kb + (size_t)min(k0 + kk + 16 * i, pos) * D + 8 * j);
@@ -375,8 +380,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 const float *rr = a.rope + (size_t)pos * D + 16 * (j & 7);
 #pragma unroll
                 for (int i = 0; i < 4; i++) rope4[i] = ld16f(rr + 4 * i);
-                qnw.issue(L.q_norm, j);
-                knw.issue(L.k_norm, j);
+                hnw.issue(wave == 2 ? L.k_norm : L.q_norm, j);
                 // the KV head's raw rows: q heads h0, h0 + 1, then k, v → s_raw (512 words, 2 a thread)
                 const uint64_t *src0 = xw + OFF_QKV;
                 uint64_t vv[2];
@@ -403,113 +407,131 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             }
             stamp(s_stamp, prof_on, 3 + 12 * l);
             if (busy) {
-                float cs[16];
+                // the per-head norms and RoPE, one head a wave (waves 0, 1: the q heads, times the softmax scale;
+                // wave 2: k; the four 16-lane rows of a wave compute the same values, the first writes them)
+                if (wave < 3) {
+                    float cs[16];
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    cs[4 * i] = rope4[i].x, cs[4 * i + 1] = rope4[i].y, cs[4 * i + 2] = rope4[i].z,
-                    cs[4 * i + 3] = rope4[i].w;
-                float ta[8], tb[8], kn8[8], v8[8], qa[8], qb[8];
-                head_post(s_raw[0], qnw, cs, j, lane, a.eps, ta);
-                head_post(s_raw[1], qnw, cs, j, lane, a.eps, tb);
-                head_post(s_raw[2], knw, cs, j, lane, a.eps, kn8);
+                    for (int i = 0; i < 4; i++)
+                        cs[4 * i] = rope4[i].x, cs[4 * i + 1] = rope4[i].y, cs[4 * i + 2] = rope4[i].z,
+                        cs[4 * i + 3] = rope4[i].w;
+                    float t8[8];
+                    head_post(s_raw[wave], hnw, cs, j, lane, a.eps, t8);
+                    if (lane < 16) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) s_post[wave][8 * j + e] = wave < 2 ? t8[e] * a.scale : t8[e];
+                    }
+                }
+                __syncthreads();
+                float qa[8], qb[8], kn8[8], v8[8];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
+                    qa[e] = s_post[0][8 * j + e];
+                    qb[e] = s_post[1][8 * j + e];
+                    kn8[e] = s_post[2][8 * j + e];
                     v8[e] = s_raw[3][8 * j + e];
-                    qa[e] = ta[e] * a.scale;
-                    qb[e] = tb[e] * a.scale;
                 }
                 const int4 knew = pack8(kn8), vnew = pack8(v8);
-                if (cw == pos / C && kk == 0) {  // the new row into the cache (no workgroup of this launch reads it)
-                    *reinterpret_cast<int4 *>(L.kc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = knew;
-                    *reinterpret_cast<int4 *>(L.vc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = vnew;
-                }
-                // scores: keys at or past pos take the new row (past pos they are masked below)
-                float v[N];
-#pragma unroll
-                for (int i = 0; i < NI; i++) {
-                    float kf[8];
-                    unpack8(k0 + kk + 16 * i >= pos ? knew : kr[i], kf);
-                    float da = 0.0f, db = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        da = fmaf(qa[e], kf[e], da);
-                        db = fmaf(qb[e], kf[e], db);
+                // the chunk that holds pos: its keys at or past pos take the new row (past pos they are masked), and
+                // it stores the row into the cache (no workgroup of this launch reads it); the other chunks' keys are
+                // all cache rows below pos
+                auto attend = [&](auto last_c) {
+                    constexpr bool LAST = decltype(last_c)::value;
+                    if (LAST && kk == 0) {
+                        *reinterpret_cast<int4 *>(L.kc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = knew;
+                        *reinterpret_cast<int4 *>(L.vc + ((size_t)kvh * a.n_ctx + pos) * D + 8 * j) = vnew;
                     }
-                    v[2 * i] = da;
-                    v[2 * i + 1] = db;
-                }
-                if constexpr (N >= 16) {
-                    halve<N, 8, 4>(v, lane);
+                    float v[N];
 #pragma unroll
-                    for (int r = 0; r < N / 16; r++) {
-                        const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
-                        const int key = kk + 16 * i;
-                        s_sc[h][key] = k0 + key < n_keys ? v[r] : -INFINITY;
+                    for (int i = 0; i < NI; i++) {
+                        float kf[8];
+                        unpack8(LAST && k0 + kk + 16 * i >= pos ? knew : kr[i], kf);
+                        float da = 0.0f, db = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            da = fmaf(qa[e], kf[e], da);
+                            db = fmaf(qb[e], kf[e], db);
+                        }
+                        v[2 * i] = da;
+                        v[2 * i + 1] = db;
                     }
-                } else {
-                    constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;
-                    halve<N, 8, S>(v, lane);
-                    const float t = group_sum<(8 >> S)>(v[0], lane);
-                    if ((j & ((16 >> S) - 1)) == 0) {
-                        const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
-                        const int key = kk + 16 * i;
-                        s_sc[h][key] = k0 + key < n_keys ? t : -INFINITY;
+                    if constexpr (N >= 16) {
+                        halve<N, 8, 4>(v, lane);
+#pragma unroll
+                        for (int r = 0; r < N / 16; r++) {
+                            const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
+                            const int key = kk + 16 * i;
+                            s_sc[h][key] = !LAST || k0 + key < n_keys ? v[r] : -INFINITY;
+                        }
+                    } else {
+                        constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;
+                        halve<N, 8, S>(v, lane);
+                        const float t = group_sum<(8 >> S)>(v[0], lane);
+                        if ((j & ((16 >> S) - 1)) == 0) {
+                            const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
+                            const int key = kk + 16 * i;
+                            s_sc[h][key] = !LAST || k0 + key < n_keys ? t : -INFINITY;
+                        }
                     }
-                }
-                __syncthreads();
-                float l_h[2];
+                    __syncthreads();
+                    float l_h[2];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    float sv[KL], mx = -INFINITY;
+                    for (int h = 0; h < 2; h++) {
+                        float sv[KL], mx = -INFINITY;
 #pragma unroll
-                    for (int i = 0; i < KL; i++) {
-                        const int key = lane + 64 * i;
-                        sv[i] = key < C ? s_sc[h][key] : -INFINITY;
-                        mx = fmaxf(mx, sv[i]);
+                        for (int i = 0; i < KL; i++) {
+                            const int key = (lane + 64 * i) % C;  // C < 64: lanes past C read a key twice
+                            sv[i] = s_sc[h][key];
+                            if (lane + 64 * i >= C) sv[i] = -INFINITY;
+                            mx = fmaxf(mx, sv[i]);
+                        }
+                        mx = wave_max(mx, lane);
+                        float ls = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < KL; i++) {
+                            const float p = expf(sv[i] - mx);  // masked keys: e^(−inf) = 0
+                            if (lane + 64 * i < C) s_pw[wave][h][lane + 64 * i] = p;
+                            ls += p;
+                        }
+                        l_h[h] = wave_sum(ls, lane);
+                        if (wave == 0 && lane == 0) s_lw[h] = mx;
                     }
-                    mx = wave_max(mx, lane);
-                    float ls = 0.0f;
+                    __builtin_amdgcn_wave_barrier();
+                    float o[16];
 #pragma unroll
-                    for (int i = 0; i < KL; i++) {
-                        const int key = lane + 64 * i;
-                        const float p = expf(sv[i] - mx);
-                        if (key < C) s_pw[wave][h][key] = p;
-                        ls += p;
+                    for (int e = 0; e < 16; e++) o[e] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < NI; i++) {
+                        float vf[8];
+                        unpack8(LAST && k0 + kk + 16 * i >= pos ? vnew : vr[i], vf);
+                        const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            o[e] = fmaf(pa, vf[e], o[e]);
+                            o[8 + e] = fmaf(pb, vf[e], o[8 + e]);
+                        }
                     }
-                    l_h[h] = wave_sum(ls, lane);
-                    if (wave == 0 && lane == 0) s_lw[h] = mx;
-                }
-                __builtin_amdgcn_wave_barrier();
-                float o[16];
+                    halve<16, 32, 2>(o, lane);
+                    {
+                        const int base = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1);
 #pragma unroll
-                for (int e = 0; e < 16; e++) o[e] = 0.0f;
-#pragma unroll
-                for (int i = 0; i < NI; i++) {
-                    float vf[8];
-                    unpack8(k0 + kk + 16 * i >= pos ? vnew : vr[i], vf);
-                    const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        o[e] = fmaf(pa, vf[e], o[e]);
-                        o[8 + e] = fmaf(pb, vf[e], o[8 + e]);
+                        for (int r = 0; r < 4; r++) {
+                            const int idx = base + r, h = idx >> 3, e = idx & 7;
+                            s_o[wave][h][8 * j + e] = o[r];
+                        }
                     }
-                }
-                halve<16, 32, 2>(o, lane);
-                {
-                    const int base = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int idx = base + r, h = idx >> 3, e = idx & 7;
-                        s_o[wave][h][8 * j + e] = o[r];
-                    }
-                }
-                __syncthreads();
-                const int hh = tid >> 7, dd = tid & 127;
-                const float oc = (s_o[0][hh][dd] + s_o[1][hh][dd]) + (s_o[2][hh][dd] + s_o[3][hh][dd]);
-                uint64_t *pc = xw + OFF_PART + (size_t)w * PART_W + hh * (D + 2);
-                put_word(pc + 2 + dd, oc, tbase + 1);
-                if (dd == 0) put_word(pc, s_lw[hh], tbase + 1);
-                if (dd == 1) put_word(pc + 1, l_h[hh], tbase + 1);
+                    __syncthreads();
+                    const int hh = tid >> 7, dd = tid & 127;
+                    const float oc = (s_o[0][hh][dd] + s_o[1][hh][dd]) + (s_o[2][hh][dd] + s_o[3][hh][dd]);
+                    uint64_t *pc = xw + OFF_PART + (size_t)w * PART_W + hh * (D + 2);
+                    put_word(pc + 2 + dd, oc, tbase + 1);
+                    if (dd == 0) put_word(pc, s_lw[hh], tbase + 1);
+                    if (dd == 1) put_word(pc + 1, l_h[hh], tbase + 1);
+                };
+                if (cw == n_chunk - 1)
+                    attend(BoolC<true>{});
+                else
+                    attend(BoolC<false>{});
             } else {
                 // an idle chunk: empty partials (no reader merges them; written so every word stays current)
                 const int hh = tid >> 7, dd = tid & 127;
@@ -545,16 +567,29 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             __syncthreads();
             stamp(s_stamp, prof_on, 5 + 12 * l);
             if (wave == 0) {
-                // lane = chunk (n_chunk ≤ 32)
-                const float m = lane < n_chunk ? s_ml[0][lane] : -INFINITY;
-                const float M = wave_max(m, lane);
-                const float wc = lane < n_chunk ? expf(m - M) : 0.0f;
-                const float Lsum = wave_sum(lane < n_chunk ? s_ml[1][lane] * wc : 0.0f, lane);
-                float ov[8];
-#pragma unroll
-                for (int q = 0; q < 8; q++) ov[q] = lane < n_chunk ? s_mo[lane][q] * wc : 0.0f;
-                const float O = wave_sum_rows<8>(ov, lane);  // lane 8q holds dim q
-                if ((lane & 7) == 0) put_word(xw + OFF_ATT + (h0 + hh) * D + d0 + (lane >> 3), O / Lsum, tbase + 2);
+                // lane ℓ: chunk ℓ % 32 (past n_chunk: weight 0), dims 4·(ℓ / 32) … + 3 of the eight. Every LDS read
+                // is unconditional (in bounds for any chunk index) and issued at once; the sums run over the 32 lanes
+                // of each half (lane bits 4 … 0), so both halves hold M and L
+                const int cl = lane & 31, half = lane >> 5;
+                const bool valid = cl < n_chunk;
+                const float mr = s_ml[0][cl], lr = s_ml[1][cl];
+                const float4 o4 = *reinterpret_cast<const float4 *>(&s_mo[cl][4 * half]);
+                const float m = valid ? mr : -INFINITY;
+                const float M = group_max<16>(m, lane);
+                const float wc = valid ? expf(m - M) : 0.0f;
+                // (chunks past n_chunk: whatever the LDS holds there, selected away — 0·inf would be NaN)
+                const float Lsum = group_sum<16>(valid ? lr * wc : 0.0f, lane);
+                const float o0 = valid ? o4.x * wc : 0.0f, o1 = valid ? o4.y * wc : 0.0f;
+                const float o2 = valid ? o4.z * wc : 0.0f, o3 = valid ? o4.w * wc : 0.0f;
+                // exchange-and-halve across lane bits 4 and 3 (as wave.h's halve, written out on scalars: an array
+                // here would be indexed per lane), then a plain sum over bits 2 … 0: lane keeps dim 2·b4 + b3
+                const bool b4 = (lane & 16) != 0, b3 = (lane & 8) != 0;
+                const float p0 = (b4 ? o2 : o0) + lane_swap<16>(b4 ? o0 : o2, lane);
+                const float p1 = (b4 ? o3 : o1) + lane_swap<16>(b4 ? o1 : o3, lane);
+                const float q = (b3 ? p1 : p0) + lane_swap<8>(b3 ? p0 : p1, lane);
+                const float O = group_sum<4>(q, lane);
+                if ((lane & 7) == 0)
+                    put_word(xw + OFF_ATT + (h0 + hh) * D + d0 + 4 * half + ((lane >> 3) & 3), O / Lsum, tbase + 2);
             }
         }
         stamp(s_stamp, prof_on, 6 + 12 * l);
