@@ -103,7 +103,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     preset = htr.Preset(repetition_penalty=1.1, repetition_window=64, max_new_tokens=n_new)
     ch = s.choice(preset, prompt, chunk=16, depth=2)
     fused = s.fused_step
-    form = "one launch a token (embed + 28 layers), then the LM head and the choice" if fused else "per kernel"
+    form = "one launch a token (embed, 28 layers, LM head, choice)" if fused else "per kernel"
 
     def reads_of(sess, chc, n_reads, n_warm):
         def one_read():
@@ -195,16 +195,19 @@ def fused_step_phases(s, pos, tok, n_layer):
     work (to its output written), µs averaged over the layers; and the step as a graph alone (profile_step)"""
     s.rewind(pos)
     us = s.profile_fused_step(tok)
-    d = np.diff(us).reshape(n_layer, 12)
+    d = np.diff(us[: 1 + 12 * n_layer]).reshape(n_layer, 12)
     names = ["qkv", "attention", "merge", "o", "gate_up", "down"]
     out = {"position": pos, "keys": pos + 1, "kernel_us": float(us[-1])}
     for i, n in enumerate(names):
         out[n + "_wait_us"] = float(d[:, 2 * i].mean())
         out[n + "_work_us"] = float(d[:, 2 * i + 1].mean())
     out["layer_us"] = float(d.sum(1).mean())
+    t = np.diff(us[12 * n_layer:])  # the LM head: its input's wait, its rows, the rest
+    out["lm_head_wait_us"], out["lm_head_rows_us"], out["lm_head_tail_us"] = (float(x) for x in t)
     out["step_in_graph_us"] = s.profile_step(htr.STEP_ALL, 16, 20) * 1e3 if GRAPHS else float("nan")
     log("one-launch step (µs a layer): " + ", ".join(f"{n} wait {out[n + '_wait_us']:.2f} work {out[n + '_work_us']:.2f}"
-                                                   for n in names) + f"; kernel {out['kernel_us']:.1f} µs")
+                                                   for n in names)
+        + f"; LM head wait {out['lm_head_wait_us']:.2f}, rows {out['lm_head_rows_us']:.2f}; kernel {out['kernel_us']:.1f} µs")
     return out
 
 

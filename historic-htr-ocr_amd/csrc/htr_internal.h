@@ -266,18 +266,28 @@ struct TokLayer {
 struct TokArgs {
     const TokLayer *layers;  // device table, one entry a layer
     int n_layer, n_ctx, n_vocab;
-    const int8_t *emb_q;
+    const int8_t *emb_q;  // token_embd: the embedding and the tied LM head
     const _Float16 *emb_d;
-    const uint32_t *tok;  // the token (device)
-    const int *state;     // state[0]: its position
+    uint32_t *tok;        // the token (device); the choice writes the next one here
+    int *state;           // state[0]: its position, state[1]: the history's length (the choice advances both)
     const float *rope;    // [n_ctx][64] (cos, sin)
     float eps, scale;
     uint64_t *xw;         // exchange words (token_step_words of them)
     uint32_t *seq, *err;  // the session's token counter (tags); set when a wait ran past spin_ticks
     float *x_out;         // the residual after the last layer
-    unsigned long long *prof;  // optional: workgroup 0's wall-clock stamps, 1 + 12·n_layer of them
+    const float *out_norm;  // output_norm: the LM head's fused RMS norm
+    float *logits;        // [n_vocab] (penalised in place when the choice runs)
+    // the greedy choice on the logits (choose != 0): the arguments of k_choose for one row (ChooseArgs)
+    int choose;
+    uint32_t *hist;
+    int window;
+    float rp, fp;
+    uint32_t *counts;
+    float *fpen;
+    unsigned long long *prof;  // optional: workgroup 0's wall-clock stamps, token_step_stamps(n_layer) of them
     long long spin_ticks;      // a wait's limit in wall-clock ticks
 };
+int token_step_stamps(int n_layer);
 size_t token_step_words();
 int token_step_ni(int n_ctx);  // keys a thread of the attention phase, 0 past 8192 rows
 bool token_step_shape(const htr_text_config &c);

@@ -162,7 +162,8 @@ int record_step_f32(htr_session *s, hipStream_t st) {
     return launch_dmv(dev, st, DMV_PLAIN, &head, 1, c.dim, s->h, nullptr, 0.0f, s->logits, 0);
 }
 
-TokArgs token_args(htr_session *s, unsigned long long *prof) {
+// the one-launch step's arguments; with ca, the greedy choice of ca runs in the launch's tail
+TokArgs token_args(htr_session *s, unsigned long long *prof, const ChooseArgs *ca) {
     const htr_text_config &c = s->m->cfg;
     TokArgs a{};
     a.layers = s->tl;
@@ -180,6 +181,17 @@ TokArgs token_args(htr_session *s, unsigned long long *prof) {
     a.seq = s->tseq;
     a.err = s->tseq + 1;
     a.x_out = s->x;
+    a.out_norm = s->m->output_norm;
+    a.logits = s->logits;
+    if (ca) {
+        a.choose = 1;
+        a.hist = ca->hist;
+        a.window = ca->window;
+        a.rp = ca->rp;
+        a.fp = ca->fp;
+        a.counts = ca->counts;
+        a.fpen = ca->fpen;
+    }
     a.prof = prof;
     a.spin_ticks = s->spin_ticks;
     return a;
@@ -258,18 +270,16 @@ int token_step_check(htr_session *s) {
 // one decode step on the session's stream: token s->tok at position state[0] → s->logits. The f16 paths' fused step
 // (record_step, text.rs:540-552 + layers_fused), or the F32 path's (record_step_f32) for a model of that path.
 // `only` (the in-graph timing of htr_session_profile_step) records just the kernels of the HTR_STEP_* classes it
-// names; the decode records them all.
-int record_step(htr_session *s, hipStream_t st, unsigned only = HTR_STEP_ALL) {
+// names; the decode records them all. ca: the choice that follows the step — the one-launch step runs it in its own
+// tail (the caller then launches no choice kernel); the per-kernel step leaves it to the caller.
+int record_step(htr_session *s, hipStream_t st, unsigned only = HTR_STEP_ALL, const ChooseArgs *ca = nullptr) {
     htr_text_model *m = s->m;
     htr_device *dev = s->dev;
     const htr_text_config &c = m->cfg;
     const int qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const float scale = 1.0f / sqrtf((float)HEAD);
-    if (s->fused && only == HTR_STEP_ALL) {
-        HTR_TRY(launch_decode_token(dev, st, s->n_ctx, token_args(s, nullptr)));
-        DmvMat head = {m->tok_embd->q, m->tok_embd->d, c.n_vocab};
-        return launch_dmv(dev, st, DMV_NORM, &head, 1, c.dim, s->x, m->output_norm, c.eps, s->logits, 0);
-    }
+    if (s->fused && only == HTR_STEP_ALL)  // embed, the layers, the LM head (and the choice of ca) in one launch
+        return launch_decode_token(dev, st, s->n_ctx, token_args(s, nullptr, ca));
     if (only & HTR_STEP_EMBED) HTR_TRY(launch_embed(dev, st, m->tok_embd, s->tok, 1, s->x));
     if (m->compute == HTR_COMPUTE_F32) return record_step_f32(s, st);
     for (int li = 0; li < c.n_layer; li++) {
@@ -317,16 +327,23 @@ ChooseArgs choice_args(htr_choice *ch, bool advance) {
     return a;
 }
 
+// [step?] then [choice?]: on the one-launch step the choice runs in the step's launch
+int record_with_choice(htr_session *s, htr_choice *ch, bool with_step, hipStream_t st) {
+    if (with_step && ch && s->fused) {
+        const ChooseArgs ca = choice_args(ch, true);
+        return record_step(s, st, HTR_STEP_ALL, &ca);
+    }
+    if (with_step) HTR_TRY(record_step(s, st));
+    return ch ? launch_choose(s->dev, st, choice_args(ch, with_step)) : 0;
+}
+
 // capture `n` repetitions of [step? + choice] into an executable graph
 int capture(htr_session *s, htr_choice *ch, int n, bool with_step, hipGraphExec_t *out) {
     htr_device *dev = s->dev;
     hipStream_t st = dev->stream;
     HTR_TRY(htr_hip(dev, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
     int rc = 0;
-    for (int i = 0; i < n && rc == 0; i++) {
-        if (with_step) rc = record_step(s, st);
-        if (rc == 0 && ch) rc = launch_choose(dev, st, choice_args(ch, with_step));
-    }
+    for (int i = 0; i < n && rc == 0; i++) rc = record_with_choice(s, ch, with_step, st);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(st, &graph);
     if (rc < 0) {
@@ -346,10 +363,7 @@ int run_steps(htr_session *s, htr_choice *ch, int n, bool with_step, hipGraphExe
     htr_device *dev = s->dev;
     hipStream_t st = dev->stream;
     if (!dev->use_graphs) {
-        for (int i = 0; i < n; i++) {
-            if (with_step) HTR_TRY(record_step(s, st));
-            if (ch) HTR_TRY(launch_choose(dev, st, choice_args(ch, with_step)));
-        }
+        for (int i = 0; i < n; i++) HTR_TRY(record_with_choice(s, ch, with_step, st));
         return 0;
     }
     if (!*g) HTR_TRY(capture(s, ch, n, with_step, g));
@@ -687,7 +701,7 @@ extern "C" int htr_session_profile_fused_step(htr_session *s, int32_t token, dou
     HTR_TRY(htr_check_alive(dev));
     HTR_TRY(htr_check_not_capturing(dev, "htr_session_profile_fused_step"));
     if (!s->tl) return htr_fail("the one-launch decode step is not available: %s", s->fused_why);
-    const int n_stamp = 1 + 12 * s->m->cfg.n_layer;
+    const int n_stamp = token_step_stamps(s->m->cfg.n_layer);
     if (n != n_stamp) return htr_fail("htr_session_profile_fused_step: %d stamps asked, the step makes %d", n, n_stamp);
     if (s->n_past >= s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
     if (token < 0 || token >= s->m->cfg.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
@@ -696,7 +710,7 @@ extern "C" int htr_session_profile_fused_step(htr_session *s, int32_t token, dou
     HTR_TRY(set_state(s, s->n_past, 0));
     unsigned long long *prof = nullptr;
     HTR_TRY(htr_dev_alloc(dev, (size_t)n_stamp * 8, HTR_MEM_WORK, (void **)&prof));
-    int rc = launch_decode_token(dev, dev->stream, s->n_ctx, token_args(s, prof));
+    int rc = launch_decode_token(dev, dev->stream, s->n_ctx, token_args(s, prof, nullptr));
     if (rc == 0) rc = htr_sync(dev);
     if (rc == 0) rc = token_step_check(s);
     std::vector<unsigned long long> st(n_stamp);

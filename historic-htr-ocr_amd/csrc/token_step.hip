@@ -32,6 +32,7 @@
 //   waits    every wait is bounded by the wall clock: past `spin_ticks` the thread sets *err, stops waiting for the
 //            rest of the launch and the launch runs out (wrong values, no hang). The host refuses the path unless the
 //            256 workgroups fit the device at once, and reports *err after the step.
+#include "choose_key.h"
 #include "htr_internal.h"
 #include "wave.h"
 
@@ -52,7 +53,8 @@ constexpr int OFF_ATT = OFF_PART + NWG * PART_W;
 constexpr int OFF_H1 = OFF_ATT + QD;
 constexpr int OFF_FF = OFF_H1 + DIM;
 constexpr int OFF_H2 = OFF_FF + NFF;
-constexpr int XWORDS = OFF_H2 + DIM;
+constexpr int OFF_BEST = OFF_H2 + DIM;  // the choice: each workgroup's best key as two words (high, low half)
+constexpr int XWORDS = OFF_BEST + 2 * NWG;
 static_assert(NQKV / NWG == 16 && DIM / NWG == 4 && NFF / NWG == 12, "rows a workgroup");
 
 typedef int gint4 __attribute__((ext_vector_type(4)));
@@ -180,7 +182,8 @@ __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uin
 // workgroup 0's wall-clock stamps, kept in LDS (a store to memory here would wait for the phase's own stores) and
 // written out at the end of the launch
 constexpr int MAX_LAYERS = 42;
-constexpr int N_STAMPS = 1 + 12 * MAX_LAYERS;
+constexpr int N_STAMPS = 1 + 12 * MAX_LAYERS + 3;
+constexpr int MAX_HEAD_ROWS = 1024;  // LM-head rows a workgroup: n_vocab ≤ 256 · 1024
 __device__ __forceinline__ void stamp(unsigned long long *s_stamp, bool on, int at) {
     if (on && threadIdx.x == 0) s_stamp[at] = (unsigned long long)wall_clock64();
 }
@@ -304,6 +307,10 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
     __shared__ float s_ml[2][WPK];
     __shared__ __attribute__((aligned(16))) float s_mo[WPK][8];
     __shared__ unsigned long long s_stamp[N_STAMPS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_pen[MAX_HEAD_ROWS];  // T: the rows whose id is in the window
+    __shared__ float s_bv[4];
+    __shared__ uint32_t s_bi[4];
+    __shared__ int s_nan0;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int w = blockIdx.x;
@@ -649,25 +656,157 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const float v = wave_sum(row_dot<3>(rw, xv), lane);
             const float xn = s_x[row] + v;
             if (lane == 0) {
-                if (l + 1 < a.n_layer)
-                    put_word(xw + OFF_H2 + row, xn, tbase + 5);
-                else
-                    a.x_out[row] = xn;  // the LM head's input (read after this launch)
+                put_word(xw + OFF_H2 + row, xn, tbase + 5);  // the next layer's, or the LM head's, input
+                if (l + 1 == a.n_layer) a.x_out[row] = xn;  // the residual (an out-of-range id's embedding)
             }
         }
         stamp(s_stamp, prof_on, 12 + 12 * l);
     }
-    // every workgroup has read seq: workgroup 0 has waited for the last layer's FF words of all of them
+    // ---- T: the LM head (output_norm fused, dmv_norm over token_embd: the tied head, text.rs:655-658) on workgroup
+    // w's rows [r0, r1) (a 256th of the vocabulary), and with `choose` the greedy choice of k_choose on them
+    // (sampling.rs:38-62: each distinct window id penalised once, in place; fp compared; first maximum; NaN never wins,
+    // NaN at index 0 → token 0): each workgroup's best key (choose_key) goes to workgroup 0 as two tagged words (no
+    // atomics: 256 on one address would queue), which keeps the largest, writes the token, appends it to the history
+    // and advances position and length.
+    {
+        const uint32_t ttag = seq * 256u + (uint32_t)(XPL * a.n_layer - 1);  // F's words of the last layer
+        const uint64_t *xlast = xw;
+        const int nv = a.n_vocab;
+        const int r0 = (int)(((long long)w * nv) / NWG), r1 = (int)(((long long)(w + 1) * nv) / NWG);
+        const int cnt = r1 - r0;
+        const int nb = (cnt + 31) / 32;  // batches of 8 rows a wave: rows r0 + wave + 4·(8b + i)
+        auto issue = [&](RowW<1>(&bt)[8], int b) {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                row_issue<1>(bt[i], a.emb_q, a.emb_d, min(r0 + wave + 4 * (8 * b + i), r1 - 1), lane);
+        };
+        RowW<1> cur[8];
+        issue(cur, 0);
+        float wv[1][16];
+        glob_x<1>(wv, a.out_norm, lane);
+        // the choice's window: ids hist[len − min(len, window) … len) (penalised when rp ≠ 1) that fall in [r0, r1)
+        // mark their rows (a repeated id marks the same row: each distinct id is penalised once)
+        const int len = a.choose ? a.state[1] : 0;
+        const int n_win = a.choose && a.rp != 1.0f ? min(len, a.window) : 0;
+        const uint32_t w_id = tid < n_win ? a.hist[len - n_win + tid] : 0xffffffffu;
+        for (int u = tid; u < MAX_HEAD_ROWS / 16; u += TPB) reinterpret_cast<uint4 *>(s_pen)[u] = make_uint4(0, 0, 0, 0);
+        if (tid == 0) s_nan0 = 0;
+        take<4>(wt, xlast + OFF_H2, DIM, ttag, s_x);  // its barriers also order the clearing before the marks
+        stamp(s_stamp, prof_on, 1 + 12 * a.n_layer);
+        if (w_id >= (uint32_t)r0 && w_id < (uint32_t)r1) s_pen[w_id - r0] = 1;
+        for (int j = tid + TPB; j < n_win; j += TPB) {
+            const uint32_t t = a.hist[len - n_win + j];
+            if (t >= (uint32_t)r0 && t < (uint32_t)r1) s_pen[t - r0] = 1;
+        }
+        float xv[1][16];
+        lds_x<1>(xv, s_x, lane);
+        norm16<1>(xv, wv, a.eps, DIM, lane);
+        __syncthreads();  // the marks
+        float bv = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (int b = 0; b < nb; b++) {
+            RowW<1> nxt[8];
+            issue(nxt, min(b + 1, nb - 1));  // the next batch's loads go out before this one's arithmetic
+            float acc[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] = row_dot<1>(cur[i], xv);
+            const float v = wave_sum_rows<8>(acc, lane);  // lane 8i holds row i of the batch
+            const int row = r0 + wave + 4 * (8 * b + (lane >> 3));
+            if ((lane & 7) == 0 && row < r1) {
+                float x = v;
+                if (a.choose) {
+                    if (s_pen[row - r0]) x = x < 0.0f ? x * a.rp : x / a.rp;
+                    if (row == 0 && x != x) s_nan0 = 1;
+                }
+                a.logits[row] = x;
+                if (a.choose && a.fp != 0.0f && a.counts[row] != 0u) x = x - a.fpen[row];
+                if (better(x, (uint32_t)row, bv, bi)) {
+                    bv = x;
+                    bi = (uint32_t)row;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) cur[i] = nxt[i];
+        }
+        stamp(s_stamp, prof_on, 2 + 12 * a.n_layer);
+        if (a.choose) {
+            // the workgroup's best → its key (NaN at index 0 after the penalty: the top key, token 0) → two words
+            wave_best(bv, bi, lane);
+            if (lane == 0) {
+                s_bv[wave] = bv;
+                s_bi[wave] = bi;
+            }
+            __syncthreads();
+            const uint32_t ctag = seq * 256u + (uint32_t)(XPL * a.n_layer);
+            if (tid == 0) {
+#pragma unroll
+                for (int q = 1; q < 4; q++)
+                    if (better(s_bv[q], s_bi[q], bv, bi)) {
+                        bv = s_bv[q];
+                        bi = s_bi[q];
+                    }
+                const uint64_t key = s_nan0 ? ~0ull : choose_key(bv, bi);
+                put_word(xw + OFF_BEST + 2 * w, __uint_as_float((uint32_t)(key >> 32)), ctag);
+                put_word(xw + OFF_BEST + 2 * w + 1, __uint_as_float((uint32_t)key), ctag);
+            }
+            // workgroup 0 takes the 256 keys, keeps the largest (the first maximum of the whole vocabulary), writes
+            // the token, appends it to the history and advances position and length
+            if (w == 0) {
+                take<2>(wt, xw + OFF_BEST, 2 * NWG, ctag, s_v);
+                if (wave == 0) {
+                    uint64_t k = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int g = lane + 64 * q;
+                        const uint64_t kq = ((uint64_t)__float_as_uint(s_v[2 * g]) << 32) | __float_as_uint(s_v[2 * g + 1]);
+                        k = kq > k ? kq : k;
+                    }
+#pragma unroll
+                    for (int m = 32; m >= 1; m >>= 1) {
+                        uint32_t ohi, olo;
+                        const uint32_t hi = (uint32_t)(k >> 32), lo = (uint32_t)k;
+                        switch (m) {
+                        case 32: ohi = lane_swap_u32<32>(hi, lane), olo = lane_swap_u32<32>(lo, lane); break;
+                        case 16: ohi = lane_swap_u32<16>(hi, lane), olo = lane_swap_u32<16>(lo, lane); break;
+                        case 8: ohi = lane_swap_u32<8>(hi, lane), olo = lane_swap_u32<8>(lo, lane); break;
+                        case 4: ohi = lane_swap_u32<4>(hi, lane), olo = lane_swap_u32<4>(lo, lane); break;
+                        case 2: ohi = lane_swap_u32<2>(hi, lane), olo = lane_swap_u32<2>(lo, lane); break;
+                        default: ohi = lane_swap_u32<1>(hi, lane), olo = lane_swap_u32<1>(lo, lane); break;
+                        }
+                        const uint64_t o = ((uint64_t)ohi << 32) | olo;
+                        k = o > k ? o : k;
+                    }
+                    if (lane == 0) {
+                        const uint32_t t = ~(uint32_t)k;
+                        const uint32_t tk = t < (uint32_t)nv ? t : 0u;  // every logit NaN, or NaN at 0 → 0
+                        a.tok[0] = tk;
+                        a.hist[len] = tk;
+                        if (a.fp != 0.0f) {
+                            const uint32_t c = a.counts[tk] + 1u;
+                            a.counts[tk] = c;
+                            a.fpen[tk] = a.fp * (float)c;
+                        }
+                        a.state[1] = len + 1;
+                        a.state[0] = pos + 1;  // every workgroup read pos at its start, before its key
+                    }
+                }
+            }
+        }
+        stamp(s_stamp, prof_on, 3 + 12 * a.n_layer);
+    }
+    // every workgroup has read seq: workgroup 0 has waited for the last layer's words of all of them
     if (w == 0 && tid == 0) __hip_atomic_store(a.seq, seq + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prof_on) {
         __syncthreads();
-        for (int i = tid; i <= 12 * a.n_layer; i += TPB) a.prof[i] = s_stamp[i];
+        for (int i = tid; i < 1 + 12 * a.n_layer + 3; i += TPB) a.prof[i] = s_stamp[i];
     }
 }
 
 }  // namespace
 
 size_t token_step_words() { return XWORDS; }
+
+int token_step_stamps(int n_layer) { return 1 + 12 * n_layer + 3; }
 
 int token_step_ni(int n_ctx) {
     for (int ni = 2; ni <= 16; ni *= 2)
@@ -677,7 +816,7 @@ int token_step_ni(int n_ctx) {
 
 bool token_step_shape(const htr_text_config &c) {
     return c.dim == DIM && c.n_head * c.d_head == QD && c.n_kv * c.d_head == KVD && c.n_ff == NFF && c.d_head == D &&
-           c.n_head == 2 * c.n_kv && c.n_layer <= MAX_LAYERS;
+           c.n_head == 2 * c.n_kv && c.n_layer <= MAX_LAYERS && c.n_vocab <= NWG * MAX_HEAD_ROWS;
 }
 
 int token_step_fits(htr_device *dev, int n_ctx, const char **why) {

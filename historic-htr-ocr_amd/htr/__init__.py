@@ -710,9 +710,9 @@ class Session:
 
     def profile_fused_step(self, tok: int) -> np.ndarray:
         """one one-launch step of `tok` at n_past (not advanced): workgroup 0's stamps in µs after the embed,
-        [1 + 12·n_layer] (per layer: each phase's input taken and output written — qkv, attention, merge, o, ffn,
-        down)"""
-        n = 1 + 12 * self.m.cfg.n_layer
+        [1 + 12·n_layer + 3] (per layer: each phase's input taken and output written — qkv, attention, merge, o,
+        ffn, down; then the LM head's input taken, its rows done, the end)"""
+        n = 1 + 12 * self.m.cfg.n_layer + 3
         us = np.zeros(n, np.float64)
         _check(lib().htr_session_profile_fused_step(self.h, int(tok), us.ctypes.data_as(C.POINTER(C.c_double)), n))
         return us

@@ -311,17 +311,19 @@ enum {
 int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int reps, float *ms_per_step);
 
 /* The decode step's form (text.rs:540-552 + layers_fused, text.rs:630-647: the same arithmetic either way, the split-K
- * merge summing its chunks in another order). For the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, ≤ 42 layers)
- * on the f16 paths, with a cache of ≤ 8192 rows, a session steps by ONE launch per token (embed and every layer; the
- * LM head and the choice stay their own launches): 256 workgroups, all resident at once, hand each phase's outputs to
- * the next through tagged words in device memory. That is the default when the device holds the 256 workgroups at
- * once (the environment variable HTR_FUSED_STEP=0 makes the per-kernel step the default instead); other models and
- * the F32 path step kernel by kernel. No reference counterpart (the reference records one dispatch per kernel).
+ * merge summing its chunks in another order). For the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, ≤ 42 layers,
+ * ≤ 262144 vocabulary ids) on the f16 paths, with a cache of ≤ 8192 rows, a session steps by ONE launch per token:
+ * the embedding, every layer, the LM head and — in htr_decode_gpu — the greedy choice (the semantics of htr_choose), as
+ * 256 workgroups, all resident at once, that hand each phase's outputs to the next through tagged words in device
+ * memory. That is the default when the device holds the 256 workgroups at once (the environment variable
+ * HTR_FUSED_STEP=0 makes the per-kernel step the default instead); other models and the F32 path step kernel by
+ * kernel. No reference counterpart (the reference records one dispatch per kernel).
  * set_fused_step(1) fails, with the reason, for a session that cannot take the one-launch form; fused_step reports the
  * session's form and, when the one-launch form is not available, why (a static string, or NULL).
  * profile_fused_step runs one one-launch step of `tok` at the session's position (not advanced; its KV row written
- * there) and returns workgroup 0's 1 + 12·n_layer wall-clock stamps in µs after the embed: per layer the input of each
- * phase taken and its output written, for qkv, attention, merge, o, gate/up, down. */
+ * there; no choice) and returns workgroup 0's 1 + 12·n_layer + 3 wall-clock stamps in µs after the embed: per layer
+ * the input of each phase taken and its output written, for qkv, attention, merge, o, gate/up, down; then the LM
+ * head's input taken, its rows done, the end. */
 int htr_session_set_fused_step(htr_session *s, int on);
 int htr_session_fused_step(htr_session *s, int *on, const char **why_not);
 int htr_session_profile_fused_step(htr_session *s, int32_t tok, double *us, int n);

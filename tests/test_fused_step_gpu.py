@@ -124,41 +124,50 @@ def test_fused_step_matches_per_kernel_step_and_oracle(dev, model, small_decoder
     sk.free()
 
 
-def test_fused_decode_gpu_teacher_forced(dev, model, small_decoder):
-    """decode_gpu on the one-launch step (graph of [step, LM head, choice] × 16, 2 in flight) and on the per-kernel
-    step: 96 greedy tokens with rp 1.1 over 64 after a 700-token prompt, each the oracle's choice given the read's
-    earlier ones (near-ties logged)"""
+@pytest.mark.parametrize("rp,window,fp", [(1.1, 64, 0.0), (1.3, 16, 0.4)], ids=["rp1.1_w64", "rp1.3_w16_fp0.4"])
+def test_fused_decode_gpu_teacher_forced(dev, model, small_decoder, rp, window, fp):
+    """decode_gpu on the one-launch step (a graph of 16 launches, each the step with the LM head and the choice in
+    its tail, 2 in flight) and on the per-kernel step: 96 greedy tokens after a 700-token prompt, each the oracle's
+    choice (sampling.rs:38-62: penalty over the window, frequency penalty over the read's counts) given the read's
+    earlier ones (near-ties logged); the read's last logits are the oracle's, with the window penalty applied in place
+    (the frequency penalty only compared, as the reference's GPU choice does)"""
     cfg, te, on, layers = small_decoder
     from htr import synth
 
     prompt = synth.prompt_ids(91, 700, N_VOCAB)
-    new, rp, window = 96, 1.1, 64
+    new = 96
     reads = []
     for fused in (True, False):
         s = model.session(CTX)
         s.fused_step = fused
         s.prefill(prompt[:-1])
         first = s.step(int(prompt[-1]))
-        ch = s.choice(htr.Preset(repetition_penalty=rp, repetition_window=window, max_new_tokens=new), prompt,
-                      chunk=16, depth=2)
+        ch = s.choice(htr.Preset(repetition_penalty=rp, repetition_window=window, frequency_penalty=fp,
+                                 max_new_tokens=new), prompt, chunk=16, depth=2)
         toks = s.decode_gpu(ch, new)
         assert len(toks) == new and s.n_past == len(prompt) + new - 1
+        last = s.logits()
         o = orc.Session(cfg, te, on, layers, CTX, f16=True)
         hand_over(s, o, len(prompt) - 1, N_LAYER)
         ch.free()
         s.free()
         lo = o.step(int(prompt[-1]))
         assert rel_l2(first, lo) < 2e-4
-        hist, ties = [int(t) for t in prompt], []
+        hist, ties, counts = [int(t) for t in prompt], [], {}
         for i, t in enumerate(toks):
+            if i + 1 == len(toks):  # the session's logits after the read: rp applied in place, fp only compared
+                pen_rp = lo.copy()  # (choose_max.wgsl:5-7, 39)
+                orc.choose(pen_rp, rp, window, 0.0, hist)
             pen = lo.copy()
-            want = orc.choose(pen, rp, window, 0.0, hist)
+            want = orc.choose(pen, rp, window, fp, hist, counts)
             if want != t:
                 assert near_tie(pen, want, t), f"{'fused' if fused else 'per-kernel'} token {i}: oracle {want}, GPU {t}"
                 ties.append(i)
             hist.append(int(t))
+            counts[int(t)] = counts.get(int(t), 0) + 1
             if i + 1 < len(toks):
                 lo = o.step(int(t))
+        assert rel_l2(last, pen_rp) < 2e-4
         reads.append(list(toks))
         print(f"\n[{'fused' if fused else 'per-kernel'} decode] {new} tokens teacher-forced, near-ties {ties}",
               flush=True)
@@ -171,7 +180,7 @@ def test_fused_step_profile_stamps(dev, model):
     s = model.session(CTX)
     s.prefill(synth.prompt_ids(5, 1279, N_VOCAB))
     us = s.profile_fused_step(17)
-    assert us.shape == (1 + 12 * N_LAYER,) and us[0] == 0.0
+    assert us.shape == (1 + 12 * N_LAYER + 3,) and us[0] == 0.0
     assert np.all(np.diff(us) >= 0.0) and us[-1] < 1e4
     print(f"\n[fused step] stamps (µs): {np.round(us, 2).tolist()}", flush=True)
     assert s.n_past == 1279
