@@ -124,6 +124,36 @@ def test_fused_step_matches_per_kernel_step_and_oracle(dev, model, small_decoder
     sk.free()
 
 
+@pytest.mark.parametrize("n_ctx,n_past", [(1000, 999), (1000, 500), (4096, 4095), (4096, 2100), (8192, 8191),
+                                          (8192, 5000)])
+def test_fused_step_other_chunk_sizes(dev, model, small_decoder, n_ctx, n_past):
+    """the other instances of the attention phase: chunks of 32 keys (caches ≤ 1024 rows), 128 (≤ 4096) and 256
+    (≤ 8192), at the cache's last row and inside it — against the per-kernel step and the oracle as above"""
+    cfg, te, on, layers = small_decoder
+    from htr import synth
+
+    prompt = synth.prompt_ids(n_ctx + n_past, n_past + 1, N_VOCAB)
+    sf, sk = model.session(n_ctx), model.session(n_ctx)
+    sk.fused_step = False
+    assert sf.fused_step
+    print(f"\n[fused step] {n_ctx}-row cache, position {n_past}", flush=True)
+    for s in (sf, sk):
+        s.prefill(prompt[:n_past])
+    tok = int(prompt[n_past])
+    lf, lk = sf.step(tok), sk.step(tok)
+    o = orc.Session(cfg, te, on, layers, n_ctx, f16=True)
+    hand_over(sk, o, n_past, N_LAYER)
+    lo = o.step(tok)
+    e_k, e_o = rel_l2(lf, lk), rel_l2(lf, lo)
+    print(f"[fused step] rel-L2 vs the per-kernel step {e_k:.2e}, vs the oracle {e_o:.2e}", flush=True)
+    assert e_k < 1e-5 and e_o < 2e-4
+    kf, vf = sf.kv_rows(0, n_past, 1)
+    kk, vk = sk.kv_rows(0, n_past, 1)
+    assert np.array_equal(kf, kk) and np.array_equal(vf, vk)
+    sf.free()
+    sk.free()
+
+
 @pytest.mark.parametrize("rp,window,fp", [(1.1, 64, 0.0), (1.3, 16, 0.4)], ids=["rp1.1_w64", "rp1.3_w16_fp0.4"])
 def test_fused_decode_gpu_teacher_forced(dev, model, small_decoder, rp, window, fp):
     """decode_gpu on the one-launch step (a graph of 16 launches, each the step with the LM head and the choice in
