@@ -188,6 +188,25 @@ __device__ __forceinline__ void stamp(unsigned long long *s_stamp, bool on, int 
     if (on && threadIdx.x == 0) s_stamp[at] = (unsigned long long)wall_clock64();
 }
 
+// wave_max / wave_sum of two values at once, their steps interleaved (the same partners and order as wave.h's, so
+// each result is the single reduction's)
+__device__ __forceinline__ void wave_max2(float &a, float &b, int lane) {
+    a = fmaxf(a, lane_swap<32>(a, lane)), b = fmaxf(b, lane_swap<32>(b, lane));
+    a = fmaxf(a, lane_swap<16>(a, lane)), b = fmaxf(b, lane_swap<16>(b, lane));
+    a = fmaxf(a, lane_swap<8>(a, lane)), b = fmaxf(b, lane_swap<8>(b, lane));
+    a = fmaxf(a, lane_swap<4>(a, lane)), b = fmaxf(b, lane_swap<4>(b, lane));
+    a = fmaxf(a, lane_swap<2>(a, lane)), b = fmaxf(b, lane_swap<2>(b, lane));
+    a = fmaxf(a, lane_swap<1>(a, lane)), b = fmaxf(b, lane_swap<1>(b, lane));
+}
+__device__ __forceinline__ void wave_sum2(float &a, float &b, int lane) {
+    a += lane_swap<32>(a, lane), b += lane_swap<32>(b, lane);
+    a += lane_swap<16>(a, lane), b += lane_swap<16>(b, lane);
+    a += lane_swap<8>(a, lane), b += lane_swap<8>(b, lane);
+    a += lane_swap<4>(a, lane), b += lane_swap<4>(b, lane);
+    a += lane_swap<2>(a, lane), b += lane_swap<2>(b, lane);
+    a += lane_swap<1>(a, lane), b += lane_swap<1>(b, lane);
+}
+
 // the fused RMS norm of a lane's 16·NG inputs (the wave holds all K of them): x·1/sqrt(Σx²/K + eps)·w
 template <int NG>
 __device__ __forceinline__ void norm16(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k, int lane) {
@@ -481,28 +500,30 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                         }
                     }
                     __syncthreads();
-                    float l_h[2];
+                    // both heads' statistics as two interleaved chains (each alone is a string of dependent
+                    // cross-lane steps that one wave a SIMD cannot hide)
+                    float sv[2][KL], mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        float sv[KL], mx = -INFINITY;
+                    for (int h = 0; h < 2; h++)
 #pragma unroll
                         for (int i = 0; i < KL; i++) {
                             const int key = (lane + 64 * i) % C;  // C < 64: lanes past C read a key twice
-                            sv[i] = s_sc[h][key];
-                            if (lane + 64 * i >= C) sv[i] = -INFINITY;
-                            mx = fmaxf(mx, sv[i]);
+                            sv[h][i] = s_sc[h][key];
+                            if (lane + 64 * i >= C) sv[h][i] = -INFINITY;
+                            mx[h] = fmaxf(mx[h], sv[h][i]);
                         }
-                        mx = wave_max(mx, lane);
-                        float ls = 0.0f;
+                    wave_max2(mx[0], mx[1], lane);
+                    float l_h[2] = {0.0f, 0.0f};
 #pragma unroll
-                        for (int i = 0; i < KL; i++) {
-                            const float p = expf(sv[i] - mx);  // masked keys: e^(−inf) = 0
+                    for (int i = 0; i < KL; i++)
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const float p = expf(sv[h][i] - mx[h]);  // masked keys: e^(−inf) = 0
                             if (lane + 64 * i < C) s_pw[wave][h][lane + 64 * i] = p;
-                            ls += p;
+                            l_h[h] += p;
                         }
-                        l_h[h] = wave_sum(ls, lane);
-                        if (wave == 0 && lane == 0) s_lw[h] = mx;
-                    }
+                    wave_sum2(l_h[0], l_h[1], lane);
+                    if (wave == 0 && lane == 0) s_lw[0] = mx[0], s_lw[1] = mx[1];
                     __builtin_amdgcn_wave_barrier();
                     float o[16];
 #pragma unroll
