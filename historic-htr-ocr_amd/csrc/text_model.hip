@@ -57,7 +57,11 @@ struct htr_session {
     htr_text_model *m = nullptr;
     htr_device *dev = nullptr;
     int n_ctx = 0, n_past = 0;
-    size_t kv_layer = 0;  // halves per layer and cache (n_kv · n_ctx · 128)
+    // the KV cache: kv_rows rows allocated (≤ n_ctx; the row stride of its head-major layout), grown by reserve to
+    // the rows asked + kv_grow; kv_gen counts the growths (a choice's graphs hold the layout they were captured with)
+    int kv_rows = 0, kv_grow = 0;
+    unsigned kv_gen = 0;
+    size_t kv_layer = 0;  // halves per layer and cache (n_kv · kv_rows · 128)
     uint16_t *kc = nullptr, *vc = nullptr;
     float *rope = nullptr;
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *g = nullptr, *logits = nullptr;
@@ -95,6 +99,7 @@ struct htr_choice {
     std::vector<hipEvent_t> events;
     hipGraphExec_t g_first = nullptr, g_one = nullptr, g_chunk = nullptr;
     bool graphs_fused = false;  // the step form the graphs were captured with
+    unsigned graphs_gen = 0;    // the session's cache layout (kv_gen) they were captured with
 };
 
 namespace {
@@ -143,9 +148,9 @@ int record_step_f32(htr_session *s, hipStream_t st) {
         HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &q, 1, c.dim, s->h, nullptr, 0.0f, s->qkv, 0));
         HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &k, 1, c.dim, s->h, nullptr, 0.0f, s->qkv + qd, 0));
         HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &v, 1, c.dim, s->h, nullptr, 0.0f, s->qkv + qd + kvd, 0));
-        HTR_TRY(launch_qkv_post(dev, st, s->qkv, ly.q_norm, ly.k_norm, s->rope, c.n_head, c.n_kv, s->state, 0, s->n_ctx,
+        HTR_TRY(launch_qkv_post(dev, st, s->qkv, ly.q_norm, ly.k_norm, s->rope, c.n_head, c.n_kv, s->state, 0, s->kv_rows,
                                 c.eps, kc, vc));
-        HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale, s->asc,
+        HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->kv_rows, s->state, 0, scale, s->asc,
                                    s->attn, nullptr, true));
         const DmvMat o = {ly.o->q, ly.o->d, c.dim};
         HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
@@ -168,7 +173,7 @@ TokArgs token_args(htr_session *s, unsigned long long *prof, const ChooseArgs *c
     TokArgs a{};
     a.layers = s->tl;
     a.n_layer = c.n_layer;
-    a.n_ctx = s->n_ctx;
+    a.n_ctx = s->kv_rows;
     a.n_vocab = c.n_vocab;
     a.emb_q = s->m->tok_embd->q;
     a.emb_d = s->m->tok_embd->d;
@@ -197,24 +202,13 @@ TokArgs token_args(htr_session *s, unsigned long long *prof, const ChooseArgs *c
     return a;
 }
 
-// the one-launch step's pieces for a session of the 1024 / 2048 / 3072 decoder on the f16 paths: the layer table (the
-// model's planes, the session's caches), the exchange words (zero: no tag of a token), seq = 1, err = 0. Sets
-// s->fused_why instead when the session cannot take it.
-int token_step_setup(htr_session *s) {
+// the one-launch step's layer table: the model's planes and the session's caches (uploaded again when the cache
+// grows; nothing reads it before the cache exists)
+int token_step_table(htr_session *s) {
+    if (!s->tl || !s->kc) return 0;
     htr_text_model *m = s->m;
-    htr_device *dev = s->dev;
-    const htr_text_config &c = m->cfg;
-    if (m->compute != HTR_COMPUTE_F16) {
-        s->fused_why = "the F32 path runs the reference's own kernel sequence";
-        return 0;
-    }
-    if (!token_step_shape(c)) {
-        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128)";
-        return 0;
-    }
-    if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;
-    std::vector<TokLayer> tl(c.n_layer);
-    for (int i = 0; i < c.n_layer; i++) {
+    std::vector<TokLayer> tl(m->cfg.n_layer);
+    for (int i = 0; i < m->cfg.n_layer; i++) {
         const Layer &l = m->layers[i];
         const htr_weight *w[7] = {l.q, l.k, l.v, l.o, l.gate, l.up, l.down};
         for (int k = 0; k < 7; k++) {
@@ -228,8 +222,27 @@ int token_step_setup(htr_session *s) {
         tl[i].kc = (_Float16 *)(s->kc + i * s->kv_layer);
         tl[i].vc = (_Float16 *)(s->vc + i * s->kv_layer);
     }
-    HTR_TRY(htr_dev_alloc(dev, tl.size() * sizeof(TokLayer), HTR_MEM_WORK, (void **)&s->tl));
-    HTR_TRY(htr_upload(dev, s->tl, tl.data(), tl.size() * sizeof(TokLayer)));
+    return htr_upload(s->dev, s->tl, tl.data(), tl.size() * sizeof(TokLayer));
+}
+
+// the one-launch step's pieces for a session of the 1024 / 2048 / 3072 decoder on the f16 paths: the layer table, the
+// exchange words (zero: no tag of a token), seq = 1, err = 0. Sets s->fused_why instead when the session cannot take
+// it. The step's instance (keys a thread, chunk size) follows n_ctx, not the rows the cache holds.
+int token_step_setup(htr_session *s) {
+    htr_text_model *m = s->m;
+    htr_device *dev = s->dev;
+    const htr_text_config &c = m->cfg;
+    if (m->compute != HTR_COMPUTE_F16) {
+        s->fused_why = "the F32 path runs the reference's own kernel sequence";
+        return 0;
+    }
+    if (!token_step_shape(c)) {
+        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128)";
+        return 0;
+    }
+    if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;
+    HTR_TRY(htr_dev_alloc(dev, (size_t)c.n_layer * sizeof(TokLayer), HTR_MEM_WORK, (void **)&s->tl));
+    HTR_TRY(token_step_table(s));
     const size_t xbytes = token_step_words() * 8;
     HTR_TRY(htr_dev_alloc(dev, xbytes, HTR_MEM_WORK, (void **)&s->xw));
     HTR_TRY(htr_hip(dev, hipMemsetAsync(s->xw, 0, xbytes, dev->stream), "hipMemsetAsync"));
@@ -290,7 +303,7 @@ int record_step(htr_session *s, hipStream_t st, unsigned only = HTR_STEP_ALL, co
             HTR_TRY(launch_dmv(dev, st, DMV_QKV, qkv, 3, c.dim, s->x, ly.attn_norm, c.eps, s->qkv, 0));
         const AttnFuse fz{ly.q_norm, ly.k_norm, s->rope, c.eps, c.n_head, (_Float16 *)kc, (_Float16 *)vc};
         if (only & HTR_STEP_ATTENTION)
-            HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->n_ctx, s->state, 0, scale,
+            HTR_TRY(launch_attn_decode(dev, st, s->qkv, kc, vc, c.n_head, c.n_kv, s->kv_rows, s->state, 0, scale,
                                        s->asc, s->attn, &fz));
         DmvMat o = {ly.o->q, ly.o->d, c.dim};
         if (only & HTR_STEP_O) HTR_TRY(launch_dmv(dev, st, DMV_PLAIN, &o, 1, qd, s->attn, nullptr, 0.0f, s->x, 1));
@@ -377,6 +390,67 @@ int set_state(htr_session *s, int pos, int len) {
     HTR_TRY(htr_hip(s->dev, hipMemcpyAsync(s->state, s->dev->pinned, sizeof v, hipMemcpyHostToDevice, s->dev->stream),
                     "state upload"));
     return htr_hip(s->dev, hipStreamSynchronize(s->dev->stream), "state upload sync");
+}
+
+// Session::reserve (text.rs:287-327): KV cache rows for positions 0 … rows − 1. When the cache holds fewer it grows to
+// rows + kv_grow (at most n_ctx): the launches in flight end first (they read and write the old cache), the rows held
+// so far move into the larger cache by one strided copy per cache (n_layer · n_kv runs of kv_rows rows each, the
+// head-major layout's stride widening from the old row count to the new), the old cache is freed. What holds the
+// layout follows: the one-launch step's layer table, the captured CPU-choice step (dropped here), a choice's graphs
+// (dropped on their next use, by kv_gen). The attention's chunks and the one-launch step's instance follow n_ctx, not
+// the rows held, so a grown cache computes what a presized one does, bit for bit. The growth's peak is the old cache
+// and the new one together (the reference replaces 4 layers at a time, for a phone's memory).
+int reserve(htr_session *s, size_t rows) {
+    if (rows <= (size_t)s->kv_rows) return 0;
+    if (rows > (size_t)s->n_ctx) return htr_fail("%zu KV cache rows asked, the session holds at most %d", rows, s->n_ctx);
+    htr_device *dev = s->dev;
+    const htr_text_config &c = s->m->cfg;
+    const size_t new_rows = std::min(rows + (size_t)s->kv_grow, (size_t)s->n_ctx);
+    const size_t runs = (size_t)c.n_layer * c.n_kv, row_bytes = (size_t)HEAD * 2;
+    const size_t bytes = runs * new_rows * row_bytes;
+    HTR_TRY(htr_sync(dev));
+    uint16_t *nk = nullptr, *nv = nullptr;
+    int rc = htr_dev_alloc(dev, bytes, HTR_MEM_KV_CACHE, (void **)&nk);
+    if (rc == 0) rc = htr_dev_alloc(dev, bytes, HTR_MEM_KV_CACHE, (void **)&nv);
+    if (rc == 0 && s->kv_rows > 0) {
+        const size_t held = (size_t)s->kv_rows * row_bytes;  // a run's bytes in the old cache: its pitch and width
+        rc = htr_hip(dev, hipMemcpy2DAsync(nk, new_rows * row_bytes, s->kc, held, held, runs, hipMemcpyDeviceToDevice,
+                                           dev->stream), "KV cache growth (k)");
+        if (rc == 0)
+            rc = htr_hip(dev, hipMemcpy2DAsync(nv, new_rows * row_bytes, s->vc, held, held, runs,
+                                               hipMemcpyDeviceToDevice, dev->stream), "KV cache growth (v)");
+        if (rc == 0) rc = htr_sync(dev);
+    }
+    if (rc < 0) {
+        for (void *p : {(void *)nk, (void *)nv})
+            if (p) htr_dev_free(dev, p);
+        return rc;
+    }
+    for (void *p : {(void *)s->kc, (void *)s->vc})
+        if (p) htr_dev_free(dev, p);
+    s->kc = nk;
+    s->vc = nv;
+    s->kv_rows = (int)new_rows;
+    s->kv_layer = (size_t)c.n_kv * new_rows * HEAD;
+    s->kv_gen += 1;
+    if (s->step_graph) {
+        hipGraphExecDestroy(s->step_graph);
+        s->step_graph = nullptr;
+    }
+    return token_step_table(s);
+}
+
+// a choice's graphs hold the step form and the cache layout of their capture: dropped when either changed
+void drop_stale_graphs(htr_choice *ch) {
+    const htr_session *s = ch->s;
+    if (ch->graphs_fused == s->fused && ch->graphs_gen == s->kv_gen) return;
+    for (hipGraphExec_t *g : {&ch->g_first, &ch->g_one, &ch->g_chunk})
+        if (*g) {
+            hipGraphExecDestroy(*g);
+            *g = nullptr;
+        }
+    ch->graphs_fused = s->fused;
+    ch->graphs_gen = s->kv_gen;
 }
 
 }  // namespace
@@ -588,8 +662,13 @@ extern "C" int htr_session_free(htr_session *s) {
     return 0;
 }
 
-extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out) {
+namespace {
+
+// TextModel::session_grown (text.rs:389-434): a session for n_ctx positions whose KV cache grows by kv_grow rows past
+// the need (reserve); `presize`: the whole cache at once, here
+int session_new(htr_text_model *m, size_t n_ctx, size_t kv_grow, bool presize, htr_session **out) {
     if (!m || !out) return htr_fail("htr_session_create: null argument");
+    if (kv_grow == 0) return htr_fail("a KV cache growth of 0 rows");
     htr_device *dev = m->dev;
     HTR_TRY(htr_check_alive(dev));
     const htr_text_config &c = m->cfg;
@@ -603,14 +682,12 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
     s->m = m;
     s->dev = dev;
     s->n_ctx = (int)n_ctx;
-    s->kv_layer = (size_t)c.n_kv * n_ctx * HEAD;
+    s->kv_grow = (int)std::min(kv_grow, n_ctx);
     const size_t qd = (size_t)c.n_head * HEAD, kvd = (size_t)c.n_kv * HEAD;
     s->asc.chunk = attn_chunk_for(s->n_ctx);
     s->asc.max_chunk = (s->n_ctx + s->asc.chunk - 1) / s->asc.chunk;
     std::vector<float> rope = rope_table(c.rope_base, HEAD, s->n_ctx);
-    int rc = htr_dev_alloc(dev, s->kv_layer * c.n_layer * 2, HTR_MEM_KV_CACHE, (void **)&s->kc);
-    if (rc == 0) rc = htr_dev_alloc(dev, s->kv_layer * c.n_layer * 2, HTR_MEM_KV_CACHE, (void **)&s->vc);
-    if (rc == 0) rc = htr_dev_alloc(dev, rope.size() * 4, HTR_MEM_WORK, (void **)&s->rope);
+    int rc = htr_dev_alloc(dev, rope.size() * 4, HTR_MEM_WORK, (void **)&s->rope);
     if (rc == 0) rc = htr_upload(dev, s->rope, rope.data(), rope.size() * 4);
     if (rc == 0) rc = htr_dev_alloc(dev, (size_t)c.dim * 4, HTR_MEM_WORK, (void **)&s->x);
     if (rc == 0) rc = htr_dev_alloc(dev, (qd + 2 * kvd) * 4, HTR_MEM_WORK, (void **)&s->qkv);
@@ -625,6 +702,7 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
         rc = htr_dev_alloc(dev, attn_part_bytes(c.n_head, s->asc.max_chunk), HTR_MEM_WORK, (void **)&s->asc.part);
     if (rc == 0) rc = htr_dev_alloc(dev, attn_counter_bytes(c.n_kv), HTR_MEM_WORK, (void **)&s->asc.counters);
     if (rc == 0) rc = token_step_setup(s);
+    if (rc == 0 && presize) rc = reserve(s, n_ctx);
     if (rc == 0 && s->fused) {
         // HTR_FUSED_STEP=0 keeps the per-kernel step (A/B timing); htr_session_set_fused_step switches per session
         const char *env = getenv("HTR_FUSED_STEP");
@@ -637,6 +715,22 @@ extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session *
         return htr_fail("%s", keep.c_str());
     }
     *out = s;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out) {
+    return session_new(m, n_ctx, n_ctx, true, out);
+}
+
+extern "C" int htr_session_create_grown(htr_text_model *m, size_t n_ctx, size_t kv_grow, htr_session **out) {
+    return session_new(m, n_ctx, kv_grow, false, out);
+}
+
+extern "C" int htr_session_kv_rows(htr_session *s, size_t *out) {
+    if (!s || !out) return htr_fail("htr_session_kv_rows: null argument");
+    *out = (size_t)s->kv_rows;
     return 0;
 }
 
@@ -660,7 +754,7 @@ extern "C" int htr_session_kv_cache(htr_session *s, htr_kv_view *out) {
     out->d_v = s->vc;
     out->n_layer = c.n_layer;
     out->n_kv = c.n_kv;
-    out->n_ctx = s->n_ctx;
+    out->n_ctx = s->kv_rows;
     out->d_head = HEAD;
     out->layer_stride = s->kv_layer;
     return 0;
@@ -705,6 +799,7 @@ extern "C" int htr_session_profile_fused_step(htr_session *s, int32_t token, dou
     if (n != n_stamp) return htr_fail("htr_session_profile_fused_step: %d stamps asked, the step makes %d", n, n_stamp);
     if (s->n_past >= s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
     if (token < 0 || token >= s->m->cfg.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
+    HTR_TRY(reserve(s, (size_t)s->n_past + 1));
     uint32_t t = (uint32_t)token;
     HTR_TRY(htr_upload(dev, s->tok, &t, 4));
     HTR_TRY(set_state(s, s->n_past, 0));
@@ -740,6 +835,7 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         if (ids[i] < 0 || ids[i] >= c.n_vocab) return htr_fail("token %d is outside the vocabulary", ids[i]);
         tok[i] = (uint32_t)ids[i];
     }
+    HTR_TRY(reserve(s, (size_t)s->n_past + n));
     const int l = (int)n, d = c.dim, f = c.n_ff, qd = c.n_head * HEAD, kvd = c.n_kv * HEAD;
     const int pos0 = s->n_past;
     hipStream_t st = dev->stream;
@@ -791,9 +887,9 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         rc = launch_gemm_f16_qkv(dev, st, h16, l, ly.q, ly.k, ly.v, q, k, v);
         if (rc == 0)
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
-                                          s->n_ctx, c.eps, kc, vc);
+                                          s->kv_rows, c.eps, kc, vc);
         if (rc == 0)
-            rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, s->kvb, nullptr,
+            rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->kv_rows, scale, s->kvb, nullptr,
                                     a16);
         if (rc == 0) rc = launch_gemm_f16_acc_norm(dev, st, a16, l, ly.o, x, ly.ffn_norm, c.eps, h16);
         if (rc == 0) rc = launch_gemm_f16(dev, st, GEMM_FFN, h16, l, ly.gate, ly.up, nullptr, g16, 1.0f);
@@ -813,8 +909,8 @@ extern "C" int htr_prefill(htr_session *s, const int32_t *ids, size_t n, float *
         if (rc == 0) rc = gemm(dev, st, h, ly.v, v, l, 0);
         if (rc == 0)
             rc = launch_qk_norm_rope_rows(dev, st, q, k, v, ly.q_norm, ly.k_norm, s->rope, l, c.n_head, c.n_kv, pos0,
-                                          s->n_ctx, c.eps, kc, vc);
-        if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->n_ctx, scale, s->kvb, a);
+                                          s->kv_rows, c.eps, kc, vc);
+        if (rc == 0) rc = launch_attn_causal(dev, st, q, kc, vc, l, pos0, c.n_head, c.n_kv, s->kv_rows, scale, s->kvb, a);
         if (rc == 0) rc = gemm(dev, st, a, ly.o, x, l, 1);
         if (rc == 0) rc = launch_rms_norm(dev, st, x, ly.ffn_norm, h, l, d, c.eps);
         if (rc == 0) rc = gemm(dev, st, h, ly.gate, g, l, 0);
@@ -847,6 +943,7 @@ extern "C" int htr_session_profile_step(htr_session *s, unsigned classes, int n_
     if (s->n_past < 1 || s->n_past >= s->n_ctx)
         return htr_fail("htr_session_profile_step: the session is at %d of %d positions", s->n_past, s->n_ctx);
     if (s->m->compute != HTR_COMPUTE_F16) return htr_fail("htr_session_profile_step: the f16 paths' fused step only");
+    HTR_TRY(reserve(s, (size_t)s->n_past + 1));
     HTR_TRY(set_state(s, s->n_past, 0));
     hipStream_t st = dev->stream;
     HTR_TRY(htr_hip(dev, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture"));
@@ -885,6 +982,7 @@ extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
     const htr_text_config &c = s->m->cfg;
     if (token < 0 || token >= c.n_vocab) return htr_fail("token %d is outside the vocabulary", token);
     if (s->n_past + 1 > s->n_ctx) return htr_fail("position %d: the session holds %d", s->n_past, s->n_ctx);
+    HTR_TRY(reserve(s, (size_t)s->n_past + 1));
     uint32_t t = (uint32_t)token;
     HTR_TRY(htr_upload(dev, s->tok, &t, 4));
     HTR_TRY(set_state(s, s->n_past, 0));
@@ -979,14 +1077,6 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         return htr_fail("%zu choices need %zu positions, the session holds %d", max, s->n_past + max - 1, s->n_ctx);
     hipStream_t st = dev->stream;
     HTR_TRY(set_state(s, s->n_past, ch->seed_len));
-    if (ch->graphs_fused != s->fused) {  // captured with the other step form
-        for (hipGraphExec_t *g : {&ch->g_first, &ch->g_one, &ch->g_chunk})
-            if (*g) {
-                hipGraphExecDestroy(*g);
-                *g = nullptr;
-            }
-        ch->graphs_fused = s->fused;
-    }
 
     struct Pending {
         size_t slot, n;
@@ -999,6 +1089,12 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
     bool stop = false;
     while (rc == 0) {
         while (!stop && next < max && !free_slots.empty()) {
+            // the slot's steps need their KV rows before its launches take the cache's layout: choices next …
+            // next + n − 1, every one but the read's first a step at the position after the one before
+            const size_t n_slot = std::min(ch->chunk, max - next);
+            rc = reserve(s, (size_t)s->n_past + next + n_slot - 1);
+            if (rc < 0) break;
+            drop_stale_graphs(ch);
             const size_t slot = free_slots.back();
             free_slots.pop_back();
             size_t n_launched = 0;

@@ -32,7 +32,8 @@ SYMBOLS = [
     "htr_vision_get_config", "htr_vision_load_gguf", "htr_vision_out_shape", "htr_vision_encode", "htr_gguf_open", "htr_gguf_open_source", "htr_gguf_close",
     "htr_gguf_header", "htr_gguf_tensor", "htr_gguf_u32", "htr_gguf_f32", "htr_gguf_str", "htr_gguf_f32_array",
     "htr_gguf_read_small", "htr_text_model_create", "htr_text_model_free", "htr_text_model_load_gguf",
-    "htr_text_model_config", "htr_session_create", "htr_session_free",
+    "htr_text_model_config", "htr_session_create", "htr_session_create_grown", "htr_session_kv_rows",
+    "htr_session_free",
     "htr_session_n_past", "htr_prefill", "htr_step", "htr_session_logits", "htr_session_rewind", "htr_choice_create", "htr_choice_free",
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
@@ -166,6 +167,8 @@ def lib() -> C.CDLL:
             "htr_text_model_load_gguf": (i32, [vp, vp, pp]),
             "htr_text_model_config": (i32, [vp, C.POINTER(TextConfigC)]),
             "htr_session_create": (i32, [vp, sz, pp]),
+            "htr_session_create_grown": (i32, [vp, sz, sz, pp]),
+            "htr_session_kv_rows": (i32, [vp, C.POINTER(C.c_size_t)]),
             "htr_session_free": (i32, [vp]),
             "htr_session_n_past": (i32, [vp, C.POINTER(sz)]),
             "htr_prefill": (i32, [vp, vp, sz, vp]),
@@ -643,17 +646,29 @@ class TextModel:
             lib().htr_text_model_free(self.h)
             self.h = None
 
-    def session(self, n_ctx: int) -> "Session":
-        return Session(self, n_ctx)
+    def session(self, n_ctx: int, kv_grow: int | None = None) -> "Session":
+        """a session for n_ctx positions: its KV cache sized to n_ctx at once, or (kv_grow) grown with the read"""
+        return Session(self, n_ctx, kv_grow)
 
 
 class Session:
-    """text.rs Session: the KV cache for n_ctx positions and the decode step's buffers."""
+    """text.rs Session: the KV cache for n_ctx positions (allocated at once, or grown by kv_grow rows past the need:
+    Session::reserve) and the decode step's buffers."""
 
-    def __init__(self, m: TextModel, n_ctx: int):
+    def __init__(self, m: TextModel, n_ctx: int, kv_grow: int | None = None):
         h = C.c_void_p()
-        _check(lib().htr_session_create(m.h, n_ctx, C.byref(h)))
+        if kv_grow is None:
+            _check(lib().htr_session_create(m.h, n_ctx, C.byref(h)))
+        else:
+            _check(lib().htr_session_create_grown(m.h, n_ctx, kv_grow, C.byref(h)))
         self.m, self.h, self.n_ctx = m, h.value, n_ctx
+
+    @property
+    def reserved_rows(self) -> int:
+        """the KV cache rows allocated now (Session::kv_rows)"""
+        v = C.c_size_t()
+        _check(lib().htr_session_kv_rows(self.h, C.byref(v)))
+        return v.value
 
     def free(self) -> None:
         if self.h:

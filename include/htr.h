@@ -275,8 +275,18 @@ int htr_text_model_config(htr_text_model *m, htr_text_config *out);
  * weight of another type or shape, and values beyond f16's range (65504, after the scale) */
 int htr_vision_load_gguf(htr_device *dev, htr_gguf *g, htr_vision **out);
 
-/* TextModel::session (text.rs:378-434): n_ctx positions (prompt + new tokens); the KV cache is sized once to n_ctx */
+/* TextModel::session (text.rs:378-434): n_ctx positions (prompt + new tokens); the KV cache is allocated here, once,
+ * for all n_ctx rows (the reference's `session` grows it by 512 rows at a time instead — htr_session_create_grown) */
 int htr_session_create(htr_text_model *m, size_t n_ctx, htr_session **out);
+/* TextModel::session_grown (text.rs:389-434; `session` and `session_for` are it with kv_grow 512 and max(expect,
+ * 512)): n_ctx positions, the KV cache allocated by the first prefill or step and grown with the read
+ * (Session::reserve, text.rs:287-327) — whenever a prefill, a step or a GPU choice's run-ahead would write past its
+ * end, to the rows asked + kv_grow (at most n_ctx). A growth waits for the launches in flight, copies the rows held
+ * into the larger cache and frees the old one (both held meanwhile); the results are a presized cache's, bit for bit.
+ * kv_grow = 0 is refused. */
+int htr_session_create_grown(htr_text_model *m, size_t n_ctx, size_t kv_grow, htr_session **out);
+/* the KV cache rows allocated now (Session::kv_rows, text.rs:282-285): n_ctx for htr_session_create */
+int htr_session_kv_rows(htr_session *s, size_t *out);
 int htr_session_free(htr_session *s);
 /* positions recorded so far (Session::n_past) */
 int htr_session_n_past(htr_session *s, size_t *out);
@@ -288,7 +298,8 @@ int htr_step(htr_session *s, int32_t tok, float *h_logits);
 int htr_session_logits(htr_session *s, float *h_logits);
 /* the session's KV cache on the device (text.rs:242-260 Session::k / v, one buffer per layer there): f16 K and V,
  * each [n_layer][n_kv][n_ctx][d_head] (layer_stride halves per layer) — head-major, where the reference keeps
- * [pos][n_kv·d_head]. For tests that read back or plant rows; the pointers live as long as the session. */
+ * [pos][n_kv·d_head]; n_ctx here is the rows allocated (htr_session_kv_rows). For tests that read back or plant rows;
+ * the pointers live until the cache grows or the session is freed. */
 typedef struct {
     uint16_t *d_k, *d_v;
     int n_layer, n_kv, n_ctx, d_head;
