@@ -14,23 +14,28 @@
 //             workgroup per CU, 192 rows where that takes fewer rows × rounds, and splits K for prompt-sized M.
 //             The FFN's W tile is BN/2 gate rows and the same BN/2 up rows in alternating blocks of 32, so a wave's
 //             two column tiles are one gate and one up tile of the same outputs;
-//   K         in stages of 32 through a ring of 4 LDS stages filled by direct-to-LDS loads (global_load_lds_dwordx4):
-//             the stage 3 ahead is loading while one is computed. Inside a stage a row's four 16-byte chunks sit at
-//             chunk ^ (row/4 % 4): 16 consecutive rows of one chunk fall on 16 different 16-byte bank groups
-//             (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes);
-//   pipeline  the fragments of stage kt are read from LDS during stage kt − 1; stage kt runs its first half of MFMAs,
-//             then waits for stage kt + 1 and the workgroup barrier while they drain, issues the loads of stage
-//             kt + 3 and the fragment reads of stage kt + 1, then its second half. Waits are explicit s_waitcnt vmcnt
-//             (the LDS loads' completion) and a bare s_barrier (no fence that would wait for the stages in flight);
+//   K         through a ring of LDS stages filled by direct-to-LDS loads (global_load_lds_dwordx4): the 256-wide
+//             tiles in stages of 64 (a row's 128 bytes of the stage, whole cache lines) in a ring of 2, the stage
+//             after next loading while one is computed; the smaller tiles in stages of 32 in a ring of 4, the stage
+//             3 ahead loading. Inside a stage a row's 16-byte chunks sit XOR-placed (chunk ^ (row/4 % 4) for 4 a
+//             row, chunk ^ (row/2 % 8) for 8): 16 consecutive rows of one chunk fall on 16 different 16-byte bank
+//             groups (gfx950's LDS serves 16 lanes of a 16-byte read a cycle across 256 bytes);
+//   pipeline  each k-step of 16 reads the next one's fragments from LDS under its MFMAs. Stages of 32: stage kt
+//             runs its first half of MFMAs, then waits for stage kt + 1 and the workgroup barrier while they drain,
+//             issues the loads of stage kt + 3 and the fragment reads of stage kt + 1, then its second half. Stages
+//             of 64: before the last k-step every wave has its reads of the stage done and its loads of the next
+//             stage in; after the barrier the loads of stage kt + 2 go out into the freed buffer. Waits are explicit
+//             s_waitcnt vmcnt / lgkmcnt and a bare s_barrier (no fence that would wait for the stages in flight);
 //   order     tiles are dealt to the 8 XCDs in contiguous bands (workgroup b runs on XCD b mod 8); inside a band
 //             groups of 4 tile rows are walked column by column, so the workgroups resident on an XCD share both
 //             their X rows and their W rows in its L2;
 //   edges     rows past M read row M − 1 and are not stored; W rows past a weight's end (a last tile that runs over)
 //             are read clamped and not stored. Stacked weights start on tile boundaries. K/32 may be odd.
-// Measured at M = 12100 on one MI355X: 851 TFLOP/s at N = 8192, K = 1024 (256 × 256 tiles) and 1034 at N = 1024,
-// K = 4096 (192 × 256), against ≈ 2.0 PFLOP/s sustained by MFMAs from registers; the clock under this load is about
-// 1.7 GHz, and the LDS traffic of a stage (its fragment reads and the direct loads' writes) is close to what the LDS
-// serves in the stage's MFMA time.
+// Measured at M = 12100 on one MI355X (a vision layer's four GEMMs, one box): stages of 64 against 32 — Q/K/V 98 →
+// 93 µs, o 46 → 44, down 138–144 → 131–135, gate/up 227–228 → 215–238 (the noisiest); 820–840 TFLOP/s for the
+// layer. Timing-only copies without the direct loads or without the fragment reads run 15–20 % and 10 % faster;
+// without both (MFMAs, barriers and epilogues alone) about 1.3 PFLOP/s. gfx950's LDS serves about 240 bytes a clock
+// to ds_read_b128 (a probe of reads alone), so its bandwidth is not what bounds the loop.
 #include <algorithm>
 
 #include "htr_internal.h"
@@ -42,21 +47,22 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // AM: X rows a stage loads (≥ BM; the rows past BM are the next tile's, loaded so that every wave issues the same
-// direct loads, and not used)
-template <int BM_, int BN_, int WM_, int WN_, int AM_ = BM_> struct Tile {
+// direct loads, and not used); KS: K a stage (32 or 64), NST: stages in the LDS ring
+template <int BM_, int BN_, int WM_, int WN_, int AM_ = BM_, int KS_ = 32, int NST_ = 4> struct Tile {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, AM = AM_;  // tile: X rows × W rows; wave grid
+    static constexpr int KS = KS_, NST = NST_, CPR = KS / 8;        // K and ring stages; 16-byte chunks a row
     static constexpr int NW = WM * WN, GW = 64 * NW;                // waves, threads
     static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles a wave
-    static constexpr int ACH = AM * 4, BCH = BN * 4, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
+    static constexpr int ACH = AM * CPR, BCH = BN * CPR, SCH = ACH + BCH;  // 16-byte chunks: A, B, a stage
     static constexpr int AI = ACH / GW, BI = BCH / GW;              // direct-to-LDS loads a wave a stage
     static_assert(TM >= 1 && TN >= 1 && AI * GW == ACH && BI * GW == BCH && AM >= BM, "tile shape");
+    static_assert((KS == 32 && NST >= 3) || (KS == 64 && NST == 2), "K stages");
 };
-using T256 = Tile<256, 256, 2, 4>;
-using T192 = Tile<192, 256, 2, 4, 256>;
+using T256 = Tile<256, 256, 2, 4, 256, 64, 2>;
+using T192 = Tile<192, 256, 2, 4, 256, 64, 2>;
 using T128 = Tile<128, 128, 2, 2>;
 using T64 = Tile<64, 64, 2, 2>;
 
-constexpr int ST = 4;      // LDS stages of 32 K each
 constexpr int GROUP = 4;   // tile rows walked together
 constexpr int XCDS = 8;
 constexpr int MAX_W = 3;
@@ -151,12 +157,19 @@ __device__ __forceinline__ float silu(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// the 16-byte chunk slot of (row r, chunk c) in a stage region
-__device__ __forceinline__ int chunk_slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
+// the 16-byte chunk slot of (row r, chunk c) in a stage region of rows of CPR chunks: the chunk index XORed with a
+// function of the row, so that the 16 lanes of a fragment read (16 consecutive rows, one chunk) fall on 16 different
+// 16-byte bank groups of the 256 bytes the LDS serves a cycle — rows of 4 chunks: chunk ^ (row/4 % 4); rows of 8
+// (128 bytes, two rows a bank window): chunk ^ (row/2 % 8). The same XOR maps a slot's chunk back to the row's chunk.
+template <int CPR> __device__ __forceinline__ int chunk_swz(int r) {
+    return CPR == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
+}
+template <int CPR> __device__ __forceinline__ int chunk_slot(int r, int c) { return CPR * r + (c ^ chunk_swz<CPR>(r)); }
 
 template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void k_gemm_f16(const GemmK a) {
     constexpr int BM = T::BM, BN = T::BN, WN = T::WN, NW = T::NW, TM = T::TM, TN = T::TN;
     constexpr int ACH = T::ACH, SCH = T::SCH, AI = T::AI, BI = T::BI;
+    constexpr int KS = T::KS, ST = T::NST, CPR = T::CPR, H = KS / 16;  // H: MFMA k-steps a stage
     static_assert(EPI != GEMM_FFN || TN == 2, "the FFN pairs one gate and one up tile a wave");
     __shared__ __attribute__((aligned(16))) int4 s_t[ST * SCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -174,7 +187,7 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
         tn = gr / gm;
     }
     const int row0 = tm * BM, k = a.k, m = a.m;
-    const int nk = (SPLIT ? a.k_per : k) / 32, kbeg = SPLIT ? sp * a.k_per : 0;
+    const int nk = (SPLIT ? a.k_per : k) / KS, kbeg = SPLIT ? sp * a.k_per : 0;
     // the W rows of tile row r (0 … BN−1): F32 / ACC the tile's rows of the stacked weights (one weight a tile, rows
     // past its end clamped); FFN blocks of 32 alternating gate / up rows of the tile's BN/2 outputs
     int wsel = 0;
@@ -192,17 +205,17 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
         return min(wrow0 + r, wrows - 1);
     };
     auto issue = [&](int ks, int buf) {
-        const size_t kk = (size_t)kbeg + (size_t)min(ks, nk - 1) * 32;
+        const size_t kk = (size_t)kbeg + (size_t)min(ks, nk - 1) * KS;
 #pragma unroll
         for (int i = 0; i < AI; i++) {
-            const int s = 64 * (wave + NW * i) + lane, r = s >> 2, c = (s & 3) ^ ((r >> 2) & 3);
+            const int s = 64 * (wave + NW * i) + lane, r = s / CPR, c = (s % CPR) ^ chunk_swz<CPR>(r);
             __builtin_amdgcn_global_load_lds((const void *)(a.x + (size_t)min(row0 + r, m - 1) * k + kk + 8 * c),
                                              (void __attribute__((address_space(3))) *)&s_t[buf * SCH + 64 * (wave + NW * i)],
                                              16, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < BI; i++) {
-            const int s = 64 * (wave + NW * i) + lane, r = s >> 2, c = (s & 3) ^ ((r >> 2) & 3);
+            const int s = 64 * (wave + NW * i) + lane, r = s / CPR, c = (s % CPR) ^ chunk_swz<CPR>(r);
             const _Float16 *base;
             const int wr = w_row(r, base);
             __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)wr * k + kk + 8 * c),
@@ -210,14 +223,16 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
                                              16, 0, 0);
         }
     };
-    // the lane's fragment slots: A tile i, B tile j, k half h (chunk 2h + lane/32 of row … + lane%32)
-    int ao[TM][2], bo[TN][2];
+    // the lane's fragment slots: A tile i, B tile j, k-step h (chunk 2h + lane/32 of row … + lane%32)
+    int ao[TM][H], bo[TN][H];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < H; h++) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) ao[i][h] = chunk_slot(wm * TM * 32 + 32 * i + (lane & 31), 2 * h + (lane >> 5));
+        for (int i = 0; i < TM; i++)
+            ao[i][h] = chunk_slot<CPR>(wm * TM * 32 + 32 * i + (lane & 31), 2 * h + (lane >> 5));
 #pragma unroll
-        for (int j = 0; j < TN; j++) bo[j][h] = ACH + chunk_slot(wn * TN * 32 + 32 * j + (lane & 31), 2 * h + (lane >> 5));
+        for (int j = 0; j < TN; j++)
+            bo[j][h] = ACH + chunk_slot<CPR>(wn * TN * 32 + 32 * j + (lane & 31), 2 * h + (lane >> 5));
     }
     struct Frag {
         half8 a[2][TM], b[2][TN];
@@ -246,6 +261,66 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
             for (int j = 0; j < TN; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
     };
+    if constexpr (KS == 64) {
+        // stages of 64 K (each X and W row's 128 bytes of the stage: whole cache lines) in a ring of two: stage kt
+        // is computed from one buffer while stage kt + 1 loads into the other. Its four k-steps each read the next
+        // k-step's fragments under their MFMAs; before the last, every wave has its reads of stage kt done
+        // (lgkmcnt) and its loads of stage kt + 1 in (vmcnt), and the barrier frees stage kt's buffer for stage
+        // kt + 2, whose loads go out with the next stage's first fragment reads under the last k-step's MFMAs
+        struct Fr {
+            half8 a[TM], b[TN];
+        };
+        auto rd = [&](Fr &f, int stage, int h) {
+            const int4 *st = s_t + (stage % ST) * SCH;
+#pragma unroll
+            for (int i = 0; i < TM; i++) f.a[i] = *reinterpret_cast<const half8 *>(st + ao[i][h]);
+#pragma unroll
+            for (int j = 0; j < TN; j++) f.b[j] = *reinterpret_cast<const half8 *>(st + bo[j][h]);
+        };
+        auto mf = [&](const Fr &f) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+        };
+        constexpr int NMF = TM * TN, NVM = AI + BI, NRD = TM + TN;
+        // the order pinned: each MFMA followed by one of the k-step's other instructions — a direct load while they
+        // last (the last k-step), a fragment read while they last
+        auto pin = [&](bool loads) {
+#pragma unroll
+            for (int q = 0; q < NMF; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                if (loads && q < NVM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one direct load
+                if (q < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // one LDS read
+            }
+        };
+        issue(0, 0);
+        issue(1, 1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(AI + BI) : "memory");  // stage 0 is in
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        Fr f0, f1;
+        rd(f0, 0, 0);
+        for (int kt = 0; kt < nk; kt++) {
+            rd(f1, kt, 1);
+            mf(f0);
+            pin(false);
+            rd(f0, kt, 2);
+            mf(f1);
+            pin(false);
+            rd(f1, kt, 3);
+            mf(f0);
+            pin(false);
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            issue(kt + 2, kt % 2);
+            rd(f0, kt + 1, 0);
+            mf(f1);
+            pin(true);
+        }
+    } else {
 #pragma unroll
     for (int s = 0; s < ST - 1; s++) issue(s, s);
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"((ST - 2) * (AI + BI)) : "memory");  // stage 0 is in
@@ -286,6 +361,7 @@ template <int EPI, class T, bool SPLIT> __global__ __launch_bounds__(T::GW) void
         step(f1, f0, kt + 1);
     }
     if (kt < nk) step(f0, f1, kt);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS load left in flight when the wave ends
 
     // epilogue: lane ℓ, register r → row 8(r/4) + 4(ℓ/32) + r%4, column ℓ%32 of each 32 × 32 tile
@@ -392,7 +468,8 @@ int launch(htr_device *dev, hipStream_t st, int epi, GemmK &a, bool *normed = nu
     if (epi != GEMM_F32 && epi != GEMM_ACC && epi != GEMM_FFN) return htr_fail("gemm_f16: epilogue %d", epi);
     const int want = std::max(1, dev->n_cu / 2);
     int tm, tn;
-    const int n_tiles[3] = {tiles_for<T256>(a, epi, tm, tn), tiles_for<T128>(a, epi, tm, tn),
+    // the 256-wide tiles take K in stages of 64
+    const int n_tiles[3] = {a.k % 64 ? -1 : tiles_for<T256>(a, epi, tm, tn), tiles_for<T128>(a, epi, tm, tn),
                             epi == GEMM_FFN ? -1 : tiles_for<T64>(a, epi, tm, tn)};
     int pick = -1;
     for (int i = 0; i < 3 && pick < 0; i++)
