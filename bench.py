@@ -77,7 +77,7 @@ def prefill_on_f32_path(dev, cfg, te, on, layers, ids) -> float:
     return dt
 
 
-def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
+def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=True):
     from htr import synth
 
     t = time.time()
@@ -131,8 +131,8 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
     mid = prompt_len - 1 + n_new // 2
     fused_phases = fused_step_phases(s, mid, int(prompt[5]), cfg["n_layer"]) if fused else None
     # the same read on the per-kernel step (A/B in one run), and its kernel classes in graphs
-    per_kernel = None
-    if fused:
+    per_kernel, phases = None, None
+    if fused and ab:
         sk = m.session(prompt_len + n_new)
         sk.fused_step = False
         sk.prefill(prompt[:-1])
@@ -144,9 +144,10 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512):
         phases = decode_phases(sk, mid, cfg["n_layer"]) if GRAPHS else None
         chk.free()
         sk.free()
-    else:
+    elif ab:
         phases = decode_phases(s, mid, cfg["n_layer"]) if GRAPHS else None
-    prefill_f32_s = prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s
+    prefill_f32_s = (prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s) \
+        if ab else float("nan")
     out = {
         "step_form": form,
         "tok_s": tok_s,
@@ -474,15 +475,18 @@ def bench_copy(dev, mib=512, reps=5):
     return res
 
 
-def load_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE
-    per dispatch, scaled by what the same counters read for a copy of known size), or None"""
-    f = os.path.join(ROOT, "profiles", "k_dmv_many_w3072x1024_traffic.json")
+def load_traffic(name="k_dmv_many_w3072x1024_traffic.json", key="hbm_bytes_per_launch"):
+    """HBM bytes per launch of the roofline kernel (or per token of the decode kernel) from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by what the same counters read for a copy of known
+    size), or None"""
+    f = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(f):
         return None
     with open(f) as fh:
         t = json.load(fh)
-    return t.get("hbm_bytes_per_launch")
+    if key == "hbm_bytes_per_token":
+        return t["hbm_fetch_bytes_per_token"] + t["hbm_write_bytes_per_token"] if "hbm_fetch_bytes_per_token" in t else None
+    return t.get(key)
 
 
 def _timed(fn, budget_s, min_n=3):
@@ -574,7 +578,9 @@ def roofline_by_config(r: dict) -> dict:
     if "decode" in r:
         d = r["decode"]
         out["config3_decode"] = {"bound": "hbm", "achieved_GBs": d["achieved_GBs"], "frac": d["frac"],
-                                 "unit": f"{d['bytes_per_token']:.0f} B a token at {d['mean_keys']} keys on average"}
+                                 "unit": f"{d['bytes_per_token']:.0f} B a token at {d['mean_keys']} keys on average",
+                                 "traffic_bytes_per_token": load_traffic("k_decode_token_traffic.json",
+                                                                         "hbm_bytes_per_token")}
     if "matvec" in r:
         m = r["matvec"]
         out["config0_matvec_graph_node"] = {"bound": "hbm", "achieved_GBs": m["graph_node_128_copies_GBs"],
@@ -612,6 +618,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="skip the legs that record graphs (decode phases, graph-node timings): for profilers that "
                          "cannot follow stream capture (with HTR_GRAPHS=0 the decode launches its kernels one by one)")
+    ap.add_argument("--no-ab", action="store_true",
+                    help="the decode leg's one-launch read alone: no per-kernel A/B read, no kernel-class timing, no "
+                         "F32-path prefill (counter runs of the decode kernel)")
     args = ap.parse_args()
     global GRAPHS
     GRAPHS = not args.no_graphs
@@ -644,7 +653,7 @@ def main():
     decode_inputs = None
     dev.phase("decode")
     if want("decode"):
-        d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup)
+        d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup, ab=not args.no_ab)
         result["value"] = d["tok_s"]
         result["ms_per_step"] = d["ms_per_read"]
         result["decode"] = d
