@@ -89,3 +89,26 @@ def test_kv_growth_of_zero_rows_refused(dev):
             m.session(64, 0)
     finally:
         m.free()
+
+
+def test_kv_growth_under_the_sampled_read(dev):
+    """the CPU-choice read with a sampled preset (sampling.rs:252-278; T 0.7, top-p 0.9, seed 1234) on a cache that
+    grows every 3 rows: the tokens of a presized cache, and the cache holds at most 3 rows past the read"""
+    m = make_model(dev, htr.COMPUTE_F16, "tiny")
+    try:
+        prompt = tiny_prompt(20)
+        n = 40
+        p = htr.Preset(repetition_penalty=1.1, repetition_window=20, frequency_penalty=0.1, max_new_tokens=n,
+                       temperature=0.7, top_p=0.9)
+        got = []
+        for grow in (None, 3):
+            s = m.session(prompt.size + n, grow)
+            s.prefill(prompt)
+            got.append(s.generate(p, 1234, prompt))
+            assert s.n_past == prompt.size + n
+            if grow is not None:
+                assert s.n_past <= s.reserved_rows <= s.n_past + grow
+            s.free()
+        assert got[0] == got[1] and len(got[0]) == n
+    finally:
+        m.free()
