@@ -237,7 +237,7 @@ int token_step_setup(htr_session *s) {
         return 0;
     }
     if (!token_step_shape(c)) {
-        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128)";
+        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, at most 42 layers and 262144 ids)";
         return 0;
     }
     if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;

@@ -238,3 +238,54 @@ def test_fused_step_reports_a_wait_that_ran_out(dev, model, monkeypatch):
     assert rel_l2(s2.step(int(prompt[-1])), s3.step(int(prompt[-1]))) < 1e-5
     s2.free()
     s3.free()
+
+
+def test_fused_step_at_its_shape_limits(dev):
+    """42 layers (the stamp table's size) and 262,144 vocabulary ids (1024 LM-head rows a workgroup, the window marks'
+    size): the step against the per-kernel step, the GPU choice's tokens with a window that marks the last row of a
+    workgroup's share, and the profile's 1 + 12·42 + 3 stamps; 43 layers are refused with the reason"""
+    from htr import synth
+
+    cfg, te, on, layers = synth_text_model(n_layer=42, n_vocab=262144, seed=4242)
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F16
+    try:
+        m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+    try:
+        prompt = synth.prompt_ids(17, 300, cfg["n_vocab"])
+        prompt[-5:] = [1023, 2047, 262143, 0, 1024]  # ids at the edges of the workgroups' row shares
+        sf, sk = m.session(512), m.session(512)
+        sk.fused_step = False
+        assert sf.fused_step
+        for s in (sf, sk):
+            s.prefill(prompt[:-1])
+        lf, lk = sf.step(int(prompt[-1])), sk.step(int(prompt[-1]))
+        assert rel_l2(lf, lk) < 1e-5
+        toks = []
+        for s in (sf, sk):
+            ch = s.choice(htr.Preset(repetition_penalty=1.3, repetition_window=64, max_new_tokens=48), prompt,
+                          chunk=8, depth=2)
+            toks.append(s.decode_gpu(ch, 48))
+            ch.free()
+        print(f"\n[fused step, 42 layers, 262144 ids] the two forms' tokens agree: {toks[0] == toks[1]}", flush=True)
+        assert toks[0][:8] == toks[1][:8]
+        sf.rewind(200)
+        us = sf.profile_fused_step(int(prompt[200]))
+        assert us.shape == (1 + 12 * 42 + 3,) and np.all(np.diff(us) >= 0.0)
+        sf.free()
+        sk.free()
+    finally:
+        m.free()
+    cfg43, te43, on43, layers43 = synth_text_model(n_layer=43, n_vocab=4096, seed=43)
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F16
+    try:
+        m43 = htr.TextModel(dev, to_htr_cfg(cfg43), te43, on43, layers43)
+    finally:
+        dev.compute = keep
+    s43 = m43.session(64)
+    assert not s43.fused_step and "1024 / 2048 / 3072" in s43.fused_step_unavailable()
+    s43.free()
+    m43.free()
