@@ -49,6 +49,8 @@ struct htr_device {
     void *static_scratch = nullptr;
     // htr_phase has a roctx range open on the calling thread
     bool phase_open = false;
+    // a 256-workgroup launch spreads its workgroups over 8 XCDs round-robin (token_step_xcds; -1: not yet looked at)
+    int xcd_round_robin = -1;
 };
 
 // looks up this device's address of the allocation-free attention's scratch array (the device must be current)
@@ -293,4 +295,7 @@ int token_step_ni(int n_ctx);  // keys a thread of the attention phase, 0 past 8
 bool token_step_shape(const htr_text_config &c);
 // 1 when the launch's 256 workgroups fit the device at once for this cache length, else 0 with the reason
 int token_step_fits(htr_device *dev, int n_ctx, const char **why);
+// 1 when a launch of the step's 256 workgroups puts the workgroups w ≡ x (mod 8) together on one XCD, for each x
+// (the XCD-local hand-overs rest on it); 0 with *why when not; -1 on a HIP error. Looked at once a device.
+int token_step_xcds(htr_device *dev, const char **why);
 int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArgs &a);

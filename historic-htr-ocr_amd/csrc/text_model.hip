@@ -241,6 +241,8 @@ int token_step_setup(htr_session *s) {
         return 0;
     }
     if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;
+    const int xr = token_step_xcds(dev, &s->fused_why);
+    if (xr <= 0) return xr;
     HTR_TRY(htr_dev_alloc(dev, (size_t)c.n_layer * sizeof(TokLayer), HTR_MEM_WORK, (void **)&s->tl));
     HTR_TRY(token_step_table(s));
     const size_t xbytes = token_step_words() * 8;
