@@ -130,8 +130,9 @@ __device__ __forceinline__ int4 pack8(const float (&f)[8]) {
 // A wait's first loads go out this long after the workgroup's own outputs (s_sleep units of 64 clocks: ≈ 0.4 µs):
 // the producers' words take about that long to become visible, and a first poll that comes back with old words
 // costs a whole round trip more. Measured on one MI355X at the 28-layer read (µs a token): no pause 482 … 488,
-// 8 → 465, 12 → 461, 16 → 460 … 469, 24 → 466, 32 → 479; two polls in flight instead (more traffic) 523.
-constexpr int POLL_SLEEP = 12;
+// 8 → 465, 12 → 461, 16 → 460 … 469, 24 → 466, 32 → 479; two polls in flight instead (more traffic) 523. With the
+// attention's hand-overs kept on their XCD (tokens/s): 8 → 2308, 12 → 2350 … 2375, 16 → 2380 … 2389.
+constexpr int POLL_SLEEP = 16;
 // Words from the workgroup's own XCD (B, C) are there sooner: 12 → 2350 tokens/s, 8 → 2371, 4 → 2378, 0 → 2378.
 constexpr int POLL_SLEEP_XCD = 4;
 
