@@ -39,6 +39,8 @@
 //   waits    every wait is bounded by the wall clock: past `spin_ticks` the thread sets *err, stops waiting for the
 //            rest of the launch and the launch runs out (wrong values, no hang). The host refuses the path unless the
 //            256 workgroups fit the device at once and spread over its XCDs as above, and reports *err after the step.
+#include <utility>
+
 #include "choose_key.h"
 #include "htr_internal.h"
 #include "wave.h"
@@ -224,6 +226,18 @@ __device__ __forceinline__ void wave_sum2(float &a, float &b, int lane) {
     a += lane_swap<1>(a, lane), b += lane_swap<1>(b, lane);
 }
 
+// the value of lane n of the lane's row of 16 (DPP row_newbcast)
+template <int n> __device__ __forceinline__ float row_bcast(float v) {
+    static_assert(n >= 0 && n < 16, "lane of a row");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + n, 0xF, 0xF, false));
+}
+// pw[idx] for idx < N: the value idx of the lane's row, held as pr[idx % NR] by lane idx / NR (NR > 1: 16 or more
+// values a row) or as pr[0] by lane idx << (4 − S) (fewer: one a group of 16 >> S lanes)
+template <int N, int NR, int S, int... I>
+__device__ __forceinline__ void row_gather(const float (&pr)[NR], float (&pw)[N], std::integer_sequence<int, I...>) {
+    ((pw[I] = row_bcast<(N >= 16 ? I / NR : I << (4 - S))>(pr[N >= 16 ? I % NR : 0])), ...);
+}
+
 // the fused RMS norm of a lane's 16·NG inputs (the wave holds all K of them): x·1/sqrt(Σx²/K + eps)·w
 template <int NG>
 __device__ __forceinline__ void norm16(float (&xv)[NG][16], const float (&wv)[NG][16], float eps, int k, int lane) {
@@ -338,14 +352,11 @@ __device__ __forceinline__ void head_post(const float *raw, const NormW &nw, con
 template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const TokArgs a) {
     constexpr int C = 16 * NI;
     constexpr int N = 2 * NI;
-    constexpr int KL = C >= 64 ? C / 64 : 1;
     __shared__ __attribute__((aligned(16))) float s_x[DIM];   // the residual, as of its last exchange
     __shared__ __attribute__((aligned(16))) float s_v[NFF];   // an exchanged input (attention output, SwiGLU)
     __shared__ __attribute__((aligned(16))) float s_raw[4][D];  // B: raw q (two heads), k, v rows of the KV head
     __shared__ __attribute__((aligned(16))) float s_post[3][D];  // B: q (× scale, two heads) and k, normed and roped
-    __shared__ float s_sc[2][C];
-    __shared__ float s_pw[4][2][C];
-    __shared__ float s_lw[2];
+    __shared__ float s_ws[4][4];  // B: each wave's max and sum of p, per head
     __shared__ float s_o[4][2][D];
     __shared__ float s_ml[2][WPK];
     __shared__ __attribute__((aligned(16))) float s_mo[WPK][8];
@@ -507,50 +518,47 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                         v[2 * i] = da;
                         v[2 * i + 1] = db;
                     }
+                    // the lane's scores, summed over the 16 lanes j of its row: NR values, idx = NR·j + r (16 or more
+                    // a thread), else one, idx = j >> (4 − S), whole in every lane of its group of 16 >> S; idx → key
+                    // kk + 16·(idx >> 1), head idx & 1
+                    constexpr int S = N >= 16 ? 4 : N == 2 ? 1 : N == 4 ? 2 : 3;
+                    constexpr int NR = N >= 16 ? N / 16 : 1;
+                    float sc[NR];
                     if constexpr (N >= 16) {
                         halve<N, 8, 4>(v, lane);
 #pragma unroll
-                        for (int r = 0; r < N / 16; r++) {
-                            const int idx = (N / 16) * j + r, i = idx >> 1, h = idx & 1;
-                            const int key = kk + 16 * i;
-                            s_sc[h][key] = !LAST || k0 + key < n_keys ? v[r] : -INFINITY;
-                        }
+                        for (int r = 0; r < NR; r++) sc[r] = v[r];
                     } else {
-                        constexpr int S = N == 2 ? 1 : N == 4 ? 2 : 3;
                         halve<N, 8, S>(v, lane);
-                        const float t = group_sum<(8 >> S)>(v[0], lane);
-                        if ((j & ((16 >> S) - 1)) == 0) {
-                            const int idx = j >> (4 - S), i = idx >> 1, h = idx & 1;
-                            const int key = kk + 16 * i;
-                            s_sc[h][key] = !LAST || k0 + key < n_keys ? t : -INFINITY;
-                        }
+                        sc[0] = group_sum<(8 >> S)>(v[0], lane);
                     }
-                    __syncthreads();
-                    // both heads' statistics as two interleaved chains (each alone is a string of dependent
-                    // cross-lane steps that one wave a SIMD cannot hide)
-                    float sv[2][KL], mx[2] = {-INFINITY, -INFINITY};
+                    const bool rep = N >= 16 || (j & ((16 >> S) - 1)) == 0;  // counts its values in the sums
+                    // the wave's own softmax over its keys (rows kk = 4·wave … 4·wave + 3), both heads as two
+                    // interleaved chains; the four waves' statistics meet in the sum of their partials below
+                    float mx[2] = {-INFINITY, -INFINITY};
+                    int hr[NR];
 #pragma unroll
-                    for (int h = 0; h < 2; h++)
-#pragma unroll
-                        for (int i = 0; i < KL; i++) {
-                            const int key = (lane + 64 * i) % C;  // C < 64: lanes past C read a key twice
-                            sv[h][i] = s_sc[h][key];
-                            if (lane + 64 * i >= C) sv[h][i] = -INFINITY;
-                            mx[h] = fmaxf(mx[h], sv[h][i]);
-                        }
+                    for (int r = 0; r < NR; r++) {
+                        const int idx = N >= 16 ? NR * j + r : j >> (4 - S);
+                        hr[r] = idx & 1;
+                        if (LAST && k0 + kk + 16 * (idx >> 1) >= n_keys) sc[r] = -INFINITY;
+                        mx[0] = hr[r] ? mx[0] : fmaxf(mx[0], sc[r]);
+                        mx[1] = hr[r] ? fmaxf(mx[1], sc[r]) : mx[1];
+                    }
                     wave_max2(mx[0], mx[1], lane);
-                    float l_h[2] = {0.0f, 0.0f};
+                    float pr[NR], l_h[2] = {0.0f, 0.0f};
 #pragma unroll
-                    for (int i = 0; i < KL; i++)
-#pragma unroll
-                        for (int h = 0; h < 2; h++) {
-                            const float p = expf(sv[h][i] - mx[h]);  // masked keys: e^(−inf) = 0
-                            if (lane + 64 * i < C) s_pw[wave][h][lane + 64 * i] = p;
-                            l_h[h] += p;
-                        }
+                    for (int r = 0; r < NR; r++) {
+                        // masked keys, and every key of a head whose keys in this wave are all masked (max −inf): 0
+                        pr[r] = sc[r] == -INFINITY ? 0.0f : expf(sc[r] - (hr[r] ? mx[1] : mx[0]));
+                        const float c = rep ? pr[r] : 0.0f;
+                        l_h[0] += hr[r] ? 0.0f : c;
+                        l_h[1] += hr[r] ? c : 0.0f;
+                    }
                     wave_sum2(l_h[0], l_h[1], lane);
-                    if (wave == 0 && lane == 0) s_lw[0] = mx[0], s_lw[1] = mx[1];
-                    __builtin_amdgcn_wave_barrier();
+                    // p of the thread's keys kk + 16·i, both heads, from the lanes of its row that hold them
+                    float pw[N];
+                    row_gather<N, NR, S>(pr, pw, std::make_integer_sequence<int, N>{});
                     float o[16];
 #pragma unroll
                     for (int e = 0; e < 16; e++) o[e] = 0.0f;
@@ -558,7 +566,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                     for (int i = 0; i < NI; i++) {
                         float vf[8];
                         unpack8(LAST && k0 + kk + 16 * i >= pos ? vnew : vr[i], vf);
-                        const float pa = s_pw[wave][0][kk + 16 * i], pb = s_pw[wave][1][kk + 16 * i];
+                        const float pa = pw[2 * i], pb = pw[2 * i + 1];
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             o[e] = fmaf(pa, vf[e], o[e]);
@@ -574,13 +582,28 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                             s_o[wave][h][8 * j + e] = o[r];
                         }
                     }
+                    if (lane == 0) s_ws[wave][0] = mx[0], s_ws[wave][1] = mx[1], s_ws[wave][2] = l_h[0],
+                                   s_ws[wave][3] = l_h[1];
                     __syncthreads();
+                    // the chunk's partial: M = max of the waves' maxima (finite: key k0 is valid), each wave's sums
+                    // weighted by e^(m_w − M) (0 for a wave with no valid key of the head)
                     const int hh = tid >> 7, dd = tid & 127;
-                    const float oc = (s_o[0][hh][dd] + s_o[1][hh][dd]) + (s_o[2][hh][dd] + s_o[3][hh][dd]);
+                    float mw[4], wt[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) mw[q] = s_ws[q][hh];
+                    const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+#pragma unroll
+                    for (int q = 0; q < 4; q++) wt[q] = mw[q] == -INFINITY ? 0.0f : expf(mw[q] - M);
+                    const float oc = (s_o[0][hh][dd] * wt[0] + s_o[1][hh][dd] * wt[1]) +
+                                     (s_o[2][hh][dd] * wt[2] + s_o[3][hh][dd] * wt[3]);
                     uint64_t *pc = xw + OFF_PART + (size_t)(kvh * WPK + cw) * PART_W + hh * (D + 2);
                     put_word_xcd(pc + 2 + dd, oc, tbase + 1);
-                    if (dd == 0) put_word_xcd(pc, s_lw[hh], tbase + 1);
-                    if (dd == 1) put_word_xcd(pc + 1, l_h[hh], tbase + 1);
+                    if (dd == 0) put_word_xcd(pc, M, tbase + 1);
+                    if (dd == 1) {
+                        const float lsum = (s_ws[0][2 + hh] * wt[0] + s_ws[1][2 + hh] * wt[1]) +
+                                           (s_ws[2][2 + hh] * wt[2] + s_ws[3][2 + hh] * wt[3]);
+                        put_word_xcd(pc + 1, lsum, tbase + 1);
+                    }
                 };
                 if (cw == n_chunk - 1)
                     attend(BoolC<true>{});
