@@ -5,7 +5,8 @@
 // (attn_norm fused), qkv_post.wgsl (per-head norms, RoPE NEOX, f16 KV store), attn_decode.wgsl + attn_merge.wgsl
 // (q·scale, f32 softmax), dmv.wgsl (o, down: + residual), dmv_ffn.wgsl (ffn_norm, SwiGLU), embed_q8_0.wgsl. The same
 // arithmetic as the per-kernel step of q8_0.hip / attention.hip (dot16 group sums times the block scale, wave sums,
-// the fused attention's butterfly and softmax); only the split-K merge sums its chunks in another order.
+// the fused attention's butterfly); the attention's softmax runs per wave over its 16 keys (the waves' sums weighted
+// by e^(m_w − M) in the chunk's partial) and the split-K merge sums its chunks in another order.
 //
 // Why one launch: at batch 1 every projection is a few MB spread over 256 CUs, so a kernel of the per-kernel step
 // spends most of its time in the launch itself and in the first load's latency; a layer is 5 such launches. Here
