@@ -952,7 +952,8 @@ int token_step_xcds(htr_device *dev, const char **why) {
 }
 
 int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArgs &a) {
-    switch (token_step_ni(n_ctx)) {
+    const int ni = token_step_ni(n_ctx);
+    switch (ni) {
     case 2: hipLaunchKernelGGL(k_decode_token<2>, dim3(NWG), dim3(TPB), 0, st, a); break;
     case 3: hipLaunchKernelGGL(k_decode_token<3>, dim3(NWG), dim3(TPB), 0, st, a); break;
     case 4: hipLaunchKernelGGL(k_decode_token<4>, dim3(NWG), dim3(TPB), 0, st, a); break;
@@ -962,5 +963,7 @@ int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArg
     case 16: hipLaunchKernelGGL(k_decode_token<16>, dim3(NWG), dim3(TPB), 0, st, a); break;
     default: return htr_fail("decode token: a %d-row cache (at most 8192)", n_ctx);
     }
-    return htr_launched(dev, "k_decode_token");
+    char name[32];
+    snprintf(name, sizeof name, "k_decode_token<%d>", ni);
+    return htr_launched(dev, name);
 }

@@ -142,7 +142,10 @@ def test_fused_step_other_chunk_sizes(dev, model, small_decoder, n_ctx, n_past):
     for s in (sf, sk):
         s.prefill(prompt[:n_past])
     tok = int(prompt[n_past])
-    lf, lk = sf.step(tok), sk.step(tok)
+    lf = sf.step(tok)
+    ni = next(ni for ni in (2, 3, 4, 6, 8, 12, 16) if n_ctx <= 512 * ni)  # the smallest chunks that cover the cache
+    assert dev.last_kernel() == f"k_decode_token<{ni}>"
+    lk = sk.step(tok)
     o = orc.Session(cfg, te, on, layers, n_ctx, f16=True)
     hand_over(sk, o, n_past, N_LAYER)
     lo = o.step(tok)
