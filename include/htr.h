@@ -321,12 +321,14 @@ enum {
 };
 int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int reps, float *ms_per_step);
 
-/* The decode step's form (text.rs:540-552 + layers_fused, text.rs:630-647: the same arithmetic either way, the split-K
- * merge summing its chunks in another order). For the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, ≤ 42 layers,
+/* The decode step's form (text.rs:540-552 + layers_fused, text.rs:630-647: the same arithmetic either way, the
+ * attention's softmax and split-K merge summing in another order). For the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, ≤ 42 layers,
  * ≤ 262144 vocabulary ids) on the f16 paths, with a cache of ≤ 8192 rows, a session steps by ONE launch per token:
  * the embedding, every layer, the LM head and — in htr_decode_gpu — the greedy choice (the semantics of htr_choose), as
  * 256 workgroups, all resident at once, that hand each phase's outputs to the next through tagged words in device
- * memory. That is the default when the device holds the 256 workgroups at once (the environment variable
+ * memory. That is the default when the device holds the 256 workgroups at once and spreads them round-robin over 8
+ * XCDs (a KV head's attention phases run on one XCD and hand over through its L2; checked once a device; the
+ * environment variable
  * HTR_FUSED_STEP=0 makes the per-kernel step the default instead); other models and the F32 path step kernel by
  * kernel. No reference counterpart (the reference records one dispatch per kernel).
  * set_fused_step(1) fails, with the reason, for a session that cannot take the one-launch form; fused_step reports the
