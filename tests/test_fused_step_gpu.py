@@ -124,13 +124,15 @@ def test_fused_step_matches_per_kernel_step_and_oracle(dev, model, small_decoder
     sk.free()
 
 
-@pytest.mark.parametrize("n_ctx,n_past", [(1000, 999), (1000, 500), (1536, 1535), (1536, 1100), (3072, 3071),
+@pytest.mark.parametrize("n_ctx,n_past", [(1000, 999), (1000, 500), (1536, 1535), (1536, 1100), (1536, 1008),
+                                          (1536, 1011), (3072, 3071),
                                           (3072, 2000), (4096, 4095), (4096, 2100), (6144, 6143), (6144, 4000),
                                           (8192, 8191), (8192, 5000)])
 def test_fused_step_other_chunk_sizes(dev, model, small_decoder, n_ctx, n_past):
     """the other instances of the attention phase: chunks of 32 keys (caches ≤ 1024 rows), 48 (≤ 1536; 3 keys a
     thread, its scores padded to 4), 96 (≤ 3072; 6, padded to 8), 128 (≤ 4096), 192 (≤ 6144; 12, padded to 16) and
-    256 (≤ 8192), at the cache's last row and inside it — against the per-kernel step and the oracle as above"""
+    256 (≤ 8192), at the cache's last row and inside it (at 1009 and 1012 keys the last 48-key chunk holds 1 and 4
+    keys: its waves past the first have no key, maximum −inf) — against the per-kernel step and the oracle as above"""
     cfg, te, on, layers = small_decoder
     from htr import synth
 
