@@ -663,7 +663,9 @@ int attn_chunk_for(int n_ctx) {
     // 16 keys per workgroup, doubled while a KV head would need more than 32 chunks (at most 32 partials per head are
     // merged for n_ctx ≤ 8192), up to 256 keys. Measured on one MI355X at 1536 keys: 24 chunks of 64 keys 6.95 µs a
     // launch, 48 of 32 8.2 µs, 96 of 16 12.3 µs, 12 of 128 7.15 µs (the merge and the ticket grow with the chunk
-    // count, the workgroup's own load phase with its keys)
+    // count, the workgroup's own load phase with its keys). At most 16 or 8 chunks a KV head instead (graph nodes,
+    // µs at 512 / 2048 / 8192 keys): 5.26 / 6.19 / 10.19 with 32, 5.25 / 6.48 / 10.15 with 16, 5.22 / 8.24 / 10.19
+    // with 8 — 512 keys sit at the launch's floor whatever the split
     int chunk = 16;
     while ((n_ctx + chunk - 1) / chunk > 32 && chunk < MAX_CHUNK_KEYS) chunk *= 2;
     return chunk;
