@@ -475,6 +475,31 @@ def bench_copy(dev, mib=512, reps=5):
     return res
 
 
+def bench_handover(dev):
+    """the hand-over the one-launch decode step rests on (htr_debug_handover, 256 workgroups of one launch): one tagged
+    word back and forth between two workgroups on one XCD (0 and 8) and on two (0 and 1), stored at workgroup scope
+    (kept in the writer XCD's L2) or agent scope (written through), read with agent-scope loads; and all-to-all
+    exchanges of 1024 / 2048 / 3072 words with the first poll 16 × 64 clocks after a workgroup's own words (1024 words
+    also at 0, 8, 12 and 24)"""
+    res = {}
+    for kind, scope in ((0, "workgroup"), (1, "agent")):
+        for a, b, where in ((0, 8, "one_xcd"), (0, 1, "two_xcds")):
+            # a workgroup-scope word is not seen from another XCD: a short limit ends that wait
+            us, seen = dev.handover(kind, a, b, iters=2000, max_polls=(1 << 20) if kind or where == "one_xcd" else 4096)
+            res[f"pair_{scope}_store_{where}"] = {"round_trip_us": us if seen else None, "seen": seen}
+    for words, pause in ((1024, 16), (2048, 16), (3072, 16), (1024, 0), (1024, 8), (1024, 12), (1024, 24)):
+        us, seen = dev.handover(2, words=words, pause=pause, iters=1000)
+        res[f"all_to_all_{words}_words_pause_{pause}"] = {"exchange_us": us if seen else None, "seen": seen}
+    f = lambda v: "not seen" if v is None else f"{v:.3f}"
+    log("hand-over (µs): one word's round trip, stored at workgroup scope: one XCD "
+        f"{f(res['pair_workgroup_store_one_xcd']['round_trip_us'])}, two XCDs "
+        f"{f(res['pair_workgroup_store_two_xcds']['round_trip_us'])}; at agent scope: one XCD "
+        f"{f(res['pair_agent_store_one_xcd']['round_trip_us'])}, two XCDs {f(res['pair_agent_store_two_xcds']['round_trip_us'])}"
+        "; an all-to-all exchange: " + ", ".join(f"{k[11:]} {f(v['exchange_us'])}" for k, v in res.items()
+                                                if k.startswith("all_to_all")))
+    return res
+
+
 def load_traffic(name="k_dmv_many_w3072x1024_traffic.json", key="hbm_bytes_per_launch"):
     """HBM bytes per launch of the roofline kernel (or per token of the decode kernel) from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by what the same counters read for a copy of known
@@ -612,7 +637,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, vision")
+    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, handover, vision")
     ap.add_argument("--choose-steps", type=int, default=10000,
                     help="single-launch steps of the choose leg (a counter run takes fewer: every launch is sampled)")
     ap.add_argument("--no-graphs", action="store_true",
@@ -681,6 +706,9 @@ def main():
     dev.phase("copy")
     if want("copy"):
         result["copy"] = bench_copy(dev)
+    dev.phase("handover")
+    if want("handover"):
+        result["handover"] = bench_handover(dev)
     dev.phase("vision")
     if want("vision"):
         result["vision_gemm"] = bench_vision_gemm(dev)

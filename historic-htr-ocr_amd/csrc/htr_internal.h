@@ -67,6 +67,7 @@ enum {
     SCR_ATTN_CNT = 3,
     SCR_CAUSAL_BLOCKS = 4,
     SCR_GEMM_PART = 5,  // split-K products [split][M][N]
+    SCR_HANDOVER = 6,   // htr_debug_handover's words
 };
 // the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it, zero-filled)
 int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out);

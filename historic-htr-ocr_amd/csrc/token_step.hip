@@ -29,8 +29,8 @@
 //            device, token_step_xcds). A, B and C of KV head h run on XCD h: its 32 workgroups make the head's q / k /
 //            v rows, attend over its chunks and merge them, so the A → B and B → C words never leave the XCD. They
 //            are stored at workgroup scope and stay in the XCD's L2, where the readers' agent-scope loads hit them:
-//            a one-way hand-over of about 0.2 µs against 0.6 µs through the fabric (a ping-pong of one word between
-//            two workgroups; the step: 2194 → 2378 tokens/s). A word never seen (a workgroup on another XCD) is
+//            a one-way hand-over of about 0.2 µs against 0.6 µs through the fabric (one word back and forth between
+//            two workgroups, htr_debug_handover in handover.hip; the step: 2194 → 2378 tokens/s). A word never seen (a workgroup on another XCD) is
 //            a wait that runs out, never a stale value: the tag proves the word current;
 //   overlap  a phase issues its weight loads (B its K rows; its V rows right after the wait) first, then waits for its
 //            input: the HBM latency of the weights runs under the hand-over's;

@@ -38,7 +38,7 @@ SYMBOLS = [
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
     "htr_graph_free", "htr_decode_attention_static", "htr_session_profile_step", "htr_session_set_fused_step",
-    "htr_session_fused_step", "htr_session_profile_fused_step",
+    "htr_session_fused_step", "htr_session_profile_fused_step", "htr_debug_handover",
 ]
 STEP_EMBED, STEP_QKV, STEP_ATTENTION, STEP_O, STEP_FFN, STEP_DOWN, STEP_HEAD, STEP_ALL = 1, 2, 4, 8, 16, 32, 64, 127
 
@@ -181,6 +181,7 @@ def lib() -> C.CDLL:
             "htr_session_fused_step": (i32, [vp, C.POINTER(i32), C.POINTER(C.c_char_p)]),
             "htr_session_profile_fused_step": (i32, [vp, i32, C.POINTER(C.c_double), i32]),
             "htr_debug_last_kernel": (i32, [vp, C.c_char_p, sz]),
+            "htr_debug_handover": (i32, [vp, i32, i32, i32, i32, i32, i32, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
             "htr_capture_begin": (i32, [vp]),
             "htr_capture_end": (i32, [vp, pp]),
             "htr_graph_launch": (i32, [vp]),
@@ -343,6 +344,16 @@ class Device:
         buf = C.create_string_buffer(96)
         _check(lib().htr_debug_last_kernel(self.h, buf, 96))
         return buf.value.decode()
+
+    def handover(self, kind: int, a: int = 0, b: int = 8, words: int = 1024, pause: int = 16, iters: int = 1000,
+                 max_polls: int = 1 << 20) -> tuple[float, bool]:
+        """tagged words handed between the workgroups of one 256-workgroup launch (htr_debug_handover): kind 0 / 1, a
+        word back and forth between workgroups a and b stored at workgroup / agent scope; kind 2, an all-to-all of
+        `words` words with the first poll `pause` × 64 clocks after a workgroup's own. (µs a round trip or an
+        exchange, whether every wait saw its word)"""
+        us, seen = C.c_double(), C.c_int32()
+        _check(lib().htr_debug_handover(self.h, kind, a, b, words, pause, iters, max_polls, C.byref(us), C.byref(seen)))
+        return us.value, bool(seen.value)
 
     def capture_begin(self) -> None:
         _check(lib().htr_capture_begin(self.h))

@@ -72,6 +72,15 @@ int htr_timer_end(htr_device *dev, float *ms);
 /* the name of the last kernel this device launched, template arguments included (e.g. "k_dmv_full<4,1,qkv>"): for tests
  * that check which kernel instance an entry point dispatched (no reference counterpart) */
 int htr_debug_last_kernel(htr_device *dev, char *name, size_t cap);
+/* The hand-over the one-launch decode step rests on, measured on this device (csrc/handover.hip; no reference
+ * counterpart). A launch of 256 workgroups passes tagged 64-bit words: kind 0, one word back and forth `iters` times
+ * between workgroups a and b, stored at workgroup scope (it stays in the writer XCD's L2); kind 1, the same stored at
+ * agent scope (written through); both read with agent-scope loads; kind 2, every workgroup passes words / 256 words
+ * (256 … 3072, a multiple of 256) to all the others, `iters` times, its first poll `pause` × 64 clocks after its own
+ * words (0, 4, 8, 12, 16, 20, 24 or 32). *us: µs a round trip (kinds 0, 1) or an exchange (kind 2). *seen: 1 when every wait saw its word, 0 when one
+ * ran out after max_polls loads (a workgroup-scope word is not seen from another XCD). Not while capturing. */
+int htr_debug_handover(htr_device *dev, int kind, int a, int b, int words, int pause, int iters, int max_polls,
+                       double *us, int *seen);
 
 /* ---- HIP graphs of the device's stream (no reference counterpart: the reference records a wgpu command buffer per
  *      submission, gpu.rs:1864-1960; here a caller records entry-point calls once and replays them) --------------- */
