@@ -32,8 +32,8 @@
 //            a one-way hand-over of about 0.2 µs against 0.6 µs through the fabric (one word back and forth between
 //            two workgroups, htr_debug_handover in handover.hip; the step: 2194 → 2378 tokens/s). A word never seen (a workgroup on another XCD) is
 //            a wait that runs out, never a stale value: the tag proves the word current;
-//   overlap  a phase issues its weight loads (B its K rows; its V rows right after the wait) first, then waits for its
-//            input: the HBM latency of the weights runs under the hand-over's;
+//   overlap  a phase issues its weight loads first, then waits for its input: the HBM latency of the weights runs
+//            under the hand-over's. B's K rows go out in A right after A's wait, its V rows right after B's;
 //   reuse    one word area per exchange, rewritten every layer. A workgroup writes exchange e of layer l + 1 only after
 //            it has read inputs that every workgroup produced after reading exchange e of layer l (checked per
 //            exchange in the comment of k_decode_token), so no word is overwritten before all its readers are done;
@@ -403,6 +403,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
         const TokLayer &L = a.layers[l];
         const uint32_t tbase = seq * 256u + (uint32_t)(XPL * l);
 
+        int4 kr[NI];  // B's K rows (issued in A)
         // ---- A: q | k | v rows 16w … 16w + 15 (one matrix: the boundaries 2048, 3072 are multiples of 16), attn_norm
         {
             const int mat = cw < 16 ? 0 : cw < 24 ? 1 : 2;
@@ -416,6 +417,12 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             float wv[1][16];
             glob_x<1>(wv, L.attn_norm, lane);
             if (l > 0) take<4>(wt, xw + OFF_H2, DIM, tbase - 1, s_x);  // F of the layer before
+            // B's K rows now, behind A's own wait (before it, A's polls would queue behind them) and ahead of B's:
+            // every chunk loads them, an idle one the row at pos (in bounds, not used). Against issuing them in B:
+            // 2456 → 2466 tokens/s at the 1536-row cache, 2366 → 2388 at 2560 rows (twice on one box)
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                kr[i] = ld16_stream(L.kc + ((size_t)kvh * a.n_ctx + min(cw * C + kk + 16 * i, pos)) * D + 8 * j);
             stamp(s_stamp, prof_on, 1 + 12 * l);
             float xv[1][16];
             lds_x<1>(xv, s_x, lane);
@@ -432,13 +439,11 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
         {
             const bool busy = cw < n_chunk;  // uniform
             const int k0 = cw * C;
-            const _Float16 *kb = L.kc + (size_t)kvh * a.n_ctx * D, *vb = L.vc + (size_t)kvh * a.n_ctx * D;
-            int4 kr[NI], vr[NI];
+            const _Float16 *vb = L.vc + (size_t)kvh * a.n_ctx * D;
+            int4 vr[NI];
             float4 rope4[4];
             NormW hnw;  // the norm weights of this wave's head (waves 0, 1: q; 2: k)
             if (busy) {
-#pragma unroll
-                for (int i = 0; i < NI; i++) kr[i] = ld16_stream(kb + (size_t)min(k0 + kk + 16 * i, pos) * D + 8 * j);
                 const float *rr = a.rope + (size_t)pos * D + 16 * (j & 7);
 #pragma unroll
                 for (int i = 0; i < 4; i++) rope4[i] = ld16f(rr + 4 * i);
