@@ -49,7 +49,11 @@ struct htr_device {
     void *static_scratch = nullptr;
     // htr_phase has a roctx range open on the calling thread
     bool phase_open = false;
-    // a 256-workgroup launch spreads its workgroups over 8 XCDs round-robin (token_step_xcds; -1: not yet looked at)
+    // HTR_POISON=1 at open: fresh and given-back memory is filled with 0xFF (htr_dev_alloc)
+    bool poison = false;
+    // a 256-workgroup launch spreads its workgroups over 8 XCDs round-robin and a workgroup-scope word is seen across
+    // an XCD's workgroups (token_step_xcds; -1: not yet looked at, 1: both hold, 0: the placement does not, 2: the
+    // visibility does not)
     int xcd_round_robin = -1;
 };
 
@@ -69,7 +73,8 @@ enum {
     SCR_GEMM_PART = 5,  // split-K products [split][M][N]
     SCR_HANDOVER = 6,   // htr_debug_handover's words
 };
-// the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it, zero-filled)
+// the device's scratch buffer `slot` with at least `bytes` bytes (a larger one replaces it: the tickets' and best
+// keys' slots zero-filled, the others as htr_dev_alloc fills)
 int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out);
 
 // the device is dead: latch the first reason and fire the hook once; returns -1
@@ -81,8 +86,10 @@ int htr_hip(htr_device *dev, hipError_t e, const char *what);
 // after a kernel launch: hipGetLastError → htr_hip
 int htr_launched(htr_device *dev, const char *kernel);
 
-// device memory counted in the ledger (zero-filled)
+// device memory counted in the ledger: zero-filled, or 0xFF under HTR_POISON=1 (for memory written before it is read)
 int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out);
+// the same, zero-filled in every mode (counters, tickets, self-resetting words that must start at zero)
+int htr_dev_alloc_zero(htr_device *dev, size_t bytes, int kind, void **out);
 int htr_dev_free(htr_device *dev, void *p);
 
 #define HTR_TRY(expr)                                                                                                  \

@@ -87,6 +87,9 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
     dev->ordinal = ordinal;
     const char *graphs = getenv("HTR_GRAPHS");
     dev->use_graphs = !(graphs && strcmp(graphs, "0") == 0);
+    // gpu.rs:739-768, 821-823, 1307-1310 (OCR_WGPU_POISON=1): a diagnostic fill of fresh and given-back memory
+    const char *poison = getenv("HTR_POISON");
+    dev->poison = poison && strcmp(poison, "1") == 0;
     // gpu.rs:1107-1115: OCR_WGPU_COMPUTE forces a compute path (coop and f16 are one path here: f16 operands into the
     // matrix cores, f32 sums); unset, the best one — f16 on matrix units, as Compute::choose picks on such a device
     if (const char *want = getenv("OCR_WGPU_COMPUTE")) {
@@ -284,7 +287,14 @@ static uint64_t *ledger(htr_device *dev, int kind) {
     }
 }
 
-int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out) {
+// HTR_POISON=1 (the reference's OCR_WGPU_POISON=1, gpu.rs:739-768, 821-823): memory is 0xFF bytes — NaN as f32 and
+// f16 — when it is handed out (htr_dev_alloc_zero's excepted) and again when it is given back, so a kernel that reads
+// what nothing wrote reads NaN, and one that reads memory after it was freed (a launch outliving its buffer) too
+static int fill_new(htr_device *dev, void *p, size_t b, bool zero) {
+    return htr_hip(dev, hipMemsetAsync(p, zero || !dev->poison ? 0 : 0xFF, b, dev->stream), "hipMemsetAsync");
+}
+
+static int alloc_filled(htr_device *dev, size_t bytes, int kind, bool zero, void **out) {
     HTR_TRY(htr_check_alive(dev));
     HTR_TRY(htr_check_not_capturing(dev, "device allocation"));
     if (kind < HTR_MEM_WEIGHTS || kind > HTR_MEM_READBACK) return htr_fail("memory kind %d: 0…3", kind);
@@ -296,11 +306,17 @@ int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out) {
         snprintf(what, sizeof what, "hipMalloc(%zu bytes)", b);
         return htr_hip(dev, e, what);
     }
-    HTR_TRY(htr_hip(dev, hipMemsetAsync(p, 0, b, dev->stream), "hipMemsetAsync"));
+    HTR_TRY(fill_new(dev, p, b, zero));
     dev->allocs[p] = {b, kind};
     *ledger(dev, kind) += b;
     *out = p;
     return 0;
+}
+
+int htr_dev_alloc(htr_device *dev, size_t bytes, int kind, void **out) { return alloc_filled(dev, bytes, kind, false, out); }
+
+int htr_dev_alloc_zero(htr_device *dev, size_t bytes, int kind, void **out) {
+    return alloc_filled(dev, bytes, kind, true, out);
 }
 
 int htr_dev_free(htr_device *dev, void *p) {
@@ -309,7 +325,10 @@ int htr_dev_free(htr_device *dev, void *p) {
     if (it == dev->allocs.end()) return htr_fail("htr_free: %p is not an allocation of device %d", p, dev->ordinal);
     HTR_TRY(htr_check_not_capturing(dev, "htr_free"));
     // the stream's work that may still read it finishes first (a Buf outlives every submission that binds it)
-    if (dev->dead_msg.empty()) hipStreamSynchronize(dev->stream);
+    if (dev->dead_msg.empty()) {
+        if (dev->poison) hipMemsetAsync(p, 0xFF, it->second.first, dev->stream);
+        hipStreamSynchronize(dev->stream);
+    }
     *ledger(dev, it->second.second) -= it->second.first;
     dev->allocs.erase(it);
     hipFree(p);
@@ -321,7 +340,9 @@ int htr_scratch(htr_device *dev, int slot, size_t bytes, void **out) {
         if (dev->scratch[slot]) HTR_TRY(htr_dev_free(dev, dev->scratch[slot]));
         dev->scratch[slot] = nullptr;
         dev->scratch_bytes[slot] = 0;
-        HTR_TRY(htr_dev_alloc(dev, bytes, HTR_MEM_WORK, &dev->scratch[slot]));
+        // the self-resetting words (best keys, tickets) start at zero; the rest is written before it is read
+        const bool zero = slot == SCR_CHOOSE_PART || slot == SCR_CHOOSE_CNT || slot == SCR_ATTN_CNT;
+        HTR_TRY(alloc_filled(dev, bytes, HTR_MEM_WORK, zero, &dev->scratch[slot]));
         dev->scratch_bytes[slot] = bytes;
     }
     *out = dev->scratch[slot];

@@ -83,7 +83,12 @@ struct htr_session {
     uint32_t *tseq = nullptr;
     bool fused = false;
     const char *fused_why = nullptr;
-    long long spin_ticks = 0;
+    long long spin_ticks = 0, spin_default = 0;
+    // a one-launch step's wait ran past its limit and the session went back to the per-kernel step (the step or the
+    // read was redone on it); htr_session_set_fused_step(1) takes the one-launch step up again
+    bool fell_back = false;
+    // bumped when what the captured graphs hold by value changes (the wait limit): a choice's graphs are re-captured
+    unsigned cap_gen = 0;
 };
 
 struct htr_choice {
@@ -95,11 +100,12 @@ struct htr_choice {
     uint32_t *hist = nullptr, *counts = nullptr, *counters = nullptr;
     uint64_t *best = nullptr;
     float *fpen = nullptr;
-    uint32_t *h_ids = nullptr;  // pinned [depth][chunk]
+    uint32_t *h_ids = nullptr;  // pinned [depth][chunk], then [depth] one-launch error words
     std::vector<hipEvent_t> events;
     hipGraphExec_t g_first = nullptr, g_one = nullptr, g_chunk = nullptr;
     bool graphs_fused = false;  // the step form the graphs were captured with
     unsigned graphs_gen = 0;    // the session's cache layout (kv_gen) they were captured with
+    unsigned graphs_cap = 0;    // and its cap_gen
 };
 
 namespace {
@@ -237,7 +243,8 @@ int token_step_setup(htr_session *s) {
         return 0;
     }
     if (!token_step_shape(c)) {
-        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, at most 42 layers and 262144 ids)";
+        s->fused_why = "the model is not the 1024 / 2048 / 3072 decoder (16 / 8 heads of 128, at most 42 layers, 256 "
+                       "to 262144 ids)";
         return 0;
     }
     if (!token_step_fits(dev, s->n_ctx, &s->fused_why)) return 0;
@@ -246,8 +253,9 @@ int token_step_setup(htr_session *s) {
     HTR_TRY(htr_dev_alloc(dev, (size_t)c.n_layer * sizeof(TokLayer), HTR_MEM_WORK, (void **)&s->tl));
     HTR_TRY(token_step_table(s));
     const size_t xbytes = token_step_words() * 8;
+    // zero, or 0xFF bytes under HTR_POISON=1: neither carries a token's tag (tags start at seq 1, and 0xFF…FF is no
+    // exchange of any layer)
     HTR_TRY(htr_dev_alloc(dev, xbytes, HTR_MEM_WORK, (void **)&s->xw));
-    HTR_TRY(htr_hip(dev, hipMemsetAsync(s->xw, 0, xbytes, dev->stream), "hipMemsetAsync"));
     HTR_TRY(htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->tseq));
     const uint32_t init[2] = {1, 0};
     HTR_TRY(htr_upload(dev, s->tseq, init, sizeof init));
@@ -255,7 +263,7 @@ int token_step_setup(htr_session *s) {
     int khz = 0;
     if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev->ordinal) != hipSuccess || khz <= 0)
         khz = 100000;
-    s->spin_ticks = (long long)khz * 200;
+    s->spin_default = s->spin_ticks = (long long)khz * 200;
     // HTR_FUSED_SPIN_US: another limit, in µs (tests of the error path set a tiny one: every wait then runs out)
     if (const char *e = getenv("HTR_FUSED_SPIN_US")) {
         const long long us = atoll(e);
@@ -265,19 +273,39 @@ int token_step_setup(htr_session *s) {
     return 0;
 }
 
-// after a one-launch step ran (the stream synchronised): its err word, cleared for the next call
-int token_step_check(htr_session *s) {
+const char *const FELL_BACK_WHY = "a wait of the one-launch step ran past its limit (its 256 workgroups did not all run "
+                                  "at once): the session went back to the per-kernel step";
+
+// after one-launch steps ran (the stream synchronised): *failed = their err word was set. Then a workgroup that ran
+// out of time may have started after workgroup 0 advanced seq and tagged its words with the next token's seq: seq
+// skips that one as well, and err is cleared for the next launch
+int token_step_err(htr_session *s, bool *failed) {
+    *failed = false;
     if (!s->tl) return 0;
-    uint32_t err = 0;
-    HTR_TRY(htr_download(s->dev, &err, s->tseq + 1, 4));
-    if (!err) return 0;
-    // a workgroup that ran out of time may have started after workgroup 0 advanced seq and tagged its words with the
-    // next token's seq: skip that one as well, and clear err
     uint32_t w[2];
     HTR_TRY(htr_download(s->dev, w, s->tseq, sizeof w));
+    if (!w[1]) return 0;
+    *failed = true;
     w[0] += 1;
     w[1] = 0;
-    HTR_TRY(htr_upload(s->dev, s->tseq, w, sizeof w));
+    return htr_upload(s->dev, s->tseq, w, sizeof w);
+}
+
+// the session steps kernel by kernel from now on (its graphs of the one-launch step are dropped)
+void fall_back(htr_session *s) {
+    s->fused = false;
+    s->fell_back = true;
+    if (s->step_graph) {
+        hipGraphExecDestroy(s->step_graph);
+        s->step_graph = nullptr;
+    }
+}
+
+// a measurement's one-launch step: its err word as an error
+int token_step_check(htr_session *s) {
+    bool failed = false;
+    HTR_TRY(token_step_err(s, &failed));
+    if (!failed) return 0;
     return htr_fail("decode step: a workgroup of the one-launch step waited past its limit (the 256 workgroups did not "
                     "all run at once); the step's logits and cache rows are invalid");
 }
@@ -445,7 +473,7 @@ int reserve(htr_session *s, size_t rows) {
 // a choice's graphs hold the step form and the cache layout of their capture: dropped when either changed
 void drop_stale_graphs(htr_choice *ch) {
     const htr_session *s = ch->s;
-    if (ch->graphs_fused == s->fused && ch->graphs_gen == s->kv_gen) return;
+    if (ch->graphs_fused == s->fused && ch->graphs_gen == s->kv_gen && ch->graphs_cap == s->cap_gen) return;
     for (hipGraphExec_t *g : {&ch->g_first, &ch->g_one, &ch->g_chunk})
         if (*g) {
             hipGraphExecDestroy(*g);
@@ -453,6 +481,7 @@ void drop_stale_graphs(htr_choice *ch) {
         }
     ch->graphs_fused = s->fused;
     ch->graphs_gen = s->kv_gen;
+    ch->graphs_cap = s->cap_gen;
 }
 
 }  // namespace
@@ -702,7 +731,7 @@ int session_new(htr_text_model *m, size_t n_ctx, size_t kv_grow, bool presize, h
     if (rc == 0) rc = htr_dev_alloc(dev, 64, HTR_MEM_WORK, (void **)&s->state);
     if (rc == 0)
         rc = htr_dev_alloc(dev, attn_part_bytes(c.n_head, s->asc.max_chunk), HTR_MEM_WORK, (void **)&s->asc.part);
-    if (rc == 0) rc = htr_dev_alloc(dev, attn_counter_bytes(c.n_kv), HTR_MEM_WORK, (void **)&s->asc.counters);
+    if (rc == 0) rc = htr_dev_alloc_zero(dev, attn_counter_bytes(c.n_kv), HTR_MEM_WORK, (void **)&s->asc.counters);
     if (rc == 0) rc = token_step_setup(s);
     if (rc == 0 && presize) rc = reserve(s, n_ctx);
     if (rc == 0 && s->fused) {
@@ -777,13 +806,29 @@ extern "C" int htr_session_set_fused_step(htr_session *s, int on) {
         s->step_graph = nullptr;
     }
     s->fused = on != 0;
+    if (on) s->fell_back = false;
     return 0;
 }
 
 extern "C" int htr_session_fused_step(htr_session *s, int *on, const char **why_not) {
     if (!s || !on) return htr_fail("htr_session_fused_step: null argument");
     *on = s->fused ? 1 : 0;
-    if (why_not) *why_not = s->tl ? nullptr : s->fused_why;
+    if (why_not) *why_not = !s->tl ? s->fused_why : (!s->fused && s->fell_back) ? FELL_BACK_WHY : nullptr;
+    return 0;
+}
+
+extern "C" int htr_session_set_wait_limit(htr_session *s, double us) {
+    if (!s) return htr_fail("htr_session_set_wait_limit: null session");
+    if (!s->tl) return htr_fail("the one-launch decode step is not available: %s", s->fused_why);
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, s->dev->ordinal) != hipSuccess || khz <= 0)
+        khz = 100000;
+    s->spin_ticks = us > 0.0 ? std::max(1LL, (long long)(us * khz / 1000.0)) : s->spin_default;
+    s->cap_gen += 1;  // the launches recorded from now on carry the new limit
+    if (s->step_graph) {
+        hipGraphExecDestroy(s->step_graph);
+        s->step_graph = nullptr;
+    }
     return 0;
 }
 
@@ -990,7 +1035,18 @@ extern "C" int htr_step(htr_session *s, int32_t token, float *h_logits) {
     HTR_TRY(set_state(s, s->n_past, 0));
     HTR_TRY(run_steps(s, nullptr, 1, true, &s->step_graph));
     HTR_TRY(htr_sync(dev));
-    if (s->fused) HTR_TRY(token_step_check(s));
+    if (s->fused) {
+        // a one-launch step whose wait ran out: the session steps kernel by kernel from now on, and this step is
+        // redone that way (the state and the token are the host's; the KV row at the position is written again)
+        bool failed = false;
+        HTR_TRY(token_step_err(s, &failed));
+        if (failed) {
+            fall_back(s);
+            HTR_TRY(set_state(s, s->n_past, 0));
+            HTR_TRY(run_steps(s, nullptr, 1, true, &s->step_graph));
+            HTR_TRY(htr_sync(dev));
+        }
+    }
     s->n_past += 1;
     if (h_logits) HTR_TRY(htr_download(dev, h_logits, s->logits, (size_t)c.n_vocab * 4));
     return 0;
@@ -1047,11 +1103,11 @@ extern "C" int htr_choice_create(htr_session *s, const htr_preset *p, const int3
     const size_t words = ch->fp > 0.0f ? (size_t)n_vocab : 1;
     int rc = htr_dev_alloc(dev, hist.size() * 4, HTR_MEM_WORK, (void **)&ch->hist);
     if (rc == 0) rc = htr_upload(dev, ch->hist, hist.data(), hist.size() * 4);
-    if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->counts);
+    if (rc == 0) rc = htr_dev_alloc_zero(dev, words * 4, HTR_MEM_WORK, (void **)&ch->counts);
     if (rc == 0) rc = htr_dev_alloc(dev, words * 4, HTR_MEM_WORK, (void **)&ch->fpen);
-    if (rc == 0) rc = htr_dev_alloc(dev, choose_best_bytes(1), HTR_MEM_WORK, (void **)&ch->best);
-    if (rc == 0) rc = htr_dev_alloc(dev, choose_ticket_bytes(1), HTR_MEM_WORK, (void **)&ch->counters);
-    if (rc == 0) rc = htr_hip(dev, hipHostMalloc((void **)&ch->h_ids, depth * chunk * 4, hipHostMallocDefault), "hipHostMalloc");
+    if (rc == 0) rc = htr_dev_alloc_zero(dev, choose_best_bytes(1), HTR_MEM_WORK, (void **)&ch->best);
+    if (rc == 0) rc = htr_dev_alloc_zero(dev, choose_ticket_bytes(1), HTR_MEM_WORK, (void **)&ch->counters);
+    if (rc == 0) rc = htr_hip(dev, hipHostMalloc((void **)&ch->h_ids, (depth * chunk + depth) * 4, hipHostMallocDefault), "hipHostMalloc");
     for (size_t i = 0; i < depth && rc == 0; i++) {
         hipEvent_t e;
         rc = htr_hip(dev, hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
@@ -1066,7 +1122,34 @@ extern "C" int htr_choice_create(htr_session *s, const htr_preset *p, const int3
     return 0;
 }
 
-// text.rs:587-625
+// a read's choices from `from` on were launched but are given up (a one-launch step's wait ran out in their chunk or
+// before): the frequency counts they added are taken back (each choice i wrote its token at hist[seed_len + i] and
+// added one to its count) — choices from … next − 1
+int take_back_counts(htr_choice *ch, size_t from, size_t next) {
+    if (ch->fp == 0.0f || from >= next) return 0;
+    htr_device *dev = ch->s->dev;
+    std::vector<uint32_t> ids(next - from), counts((size_t)ch->n_vocab);
+    std::vector<float> fpen((size_t)ch->n_vocab);
+    HTR_TRY(htr_download(dev, ids.data(), ch->hist + ch->seed_len + from, ids.size() * 4));
+    HTR_TRY(htr_download(dev, counts.data(), ch->counts, counts.size() * 4));
+    HTR_TRY(htr_download(dev, fpen.data(), ch->fpen, fpen.size() * 4));
+    for (uint32_t t : ids) {
+        if (t >= (uint32_t)ch->n_vocab || counts[t] == 0) return htr_fail("decode: a given-up choice's count is gone");
+        counts[t] -= 1;
+        fpen[t] = ch->fp * (float)counts[t];  // the value the step that counted last wrote: fp · count
+    }
+    HTR_TRY(htr_upload(dev, ch->counts, counts.data(), counts.size() * 4));
+    return htr_upload(dev, ch->fpen, fpen.data(), fpen.size() * 4);
+}
+
+// text.rs:587-625. Each launch of `chunk` choices copies its ids back with the one-launch step's error word in the same
+// stream order, and the ids reach on_token only after both have landed (the reference reads each submission's ids
+// through read_mapped_u32, which fails on a dead device before on_token sees them, text.rs:616-623, gpu.rs:1391-1396).
+// A set error word means a wait of some one-launch step of that chunk ran out (the 256 workgroups were not all resident
+// at once): none of the chunk's ids is passed on, the launches after it are drained unseen, and the read goes on from
+// the chunk's first step on the per-kernel step, which the session keeps — the counts, the position and the token
+// rewound to what the chunk started from (its first choice, if it is the read's first, came from the prefill's logits
+// by the choice kernel and is kept).
 extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_token_cb on_token, void *user) {
     if (!s || !ch || ch->s != s) return htr_fail("htr_decode_gpu: null argument or a choice of another session");
     htr_device *dev = s->dev;
@@ -1079,14 +1162,16 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         return htr_fail("%zu choices need %zu positions, the session holds %d", max, s->n_past + max - 1, s->n_ctx);
     hipStream_t st = dev->stream;
     HTR_TRY(set_state(s, s->n_past, ch->seed_len));
+    uint32_t *h_err = ch->h_ids + ch->depth * ch->chunk;
 
     struct Pending {
-        size_t slot, n;
+        size_t slot, first, n;
     };
     std::deque<Pending> queue;
     std::vector<size_t> free_slots;
     for (size_t i = ch->depth; i-- > 0;) free_slots.push_back(i);
-    size_t next = 0;  // choices launched
+    size_t next = 0;          // choices launched
+    int32_t last_tok = -1;    // the last choice passed to on_token
     int rc = 0;
     bool stop = false;
     while (rc == 0) {
@@ -1120,8 +1205,12 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
                          hipMemcpyAsync(ch->h_ids + slot * ch->chunk, ch->hist + ch->seed_len + next, n_launched * 4,
                                         hipMemcpyDeviceToHost, st),
                          "token readback");
+            h_err[slot] = 0;
+            if (rc == 0 && s->tl)
+                rc = htr_hip(dev, hipMemcpyAsync(h_err + slot, s->tseq + 1, 4, hipMemcpyDeviceToHost, st),
+                             "error word readback");
             if (rc == 0) rc = htr_hip(dev, hipEventRecord(ch->events[slot], st), "hipEventRecord");
-            queue.push_back({slot, n_launched});
+            queue.push_back({slot, next, n_launched});
             next += n_launched;
         }
         if (rc < 0 || queue.empty()) break;
@@ -1129,8 +1218,37 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         queue.pop_front();
         rc = htr_hip(dev, hipEventSynchronize(ch->events[pd.slot]), "hipEventSynchronize");
         if (rc < 0) break;
+        if (h_err[pd.slot]) {
+            // drain what was launched after the chunk, clear the error word, step kernel by kernel from here
+            rc = htr_sync(dev);
+            bool failed = false;
+            if (rc == 0) rc = token_step_err(s, &failed);
+            if (rc < 0) break;
+            fall_back(s);
+            const size_t redo = std::max<size_t>(pd.first, 1);  // the first choice made after a step
+            if (pd.first == 0) {  // the read's first choice: the choice kernel's, on the prefill's logits
+                uint32_t t0 = 0;
+                rc = htr_download(dev, &t0, ch->hist + ch->seed_len, 4);
+                if (rc < 0) break;
+                last_tok = (int32_t)t0;
+                if (on_token && !on_token(last_tok, user)) stop = true;
+            }
+            rc = take_back_counts(ch, redo, next);
+            if (rc < 0) break;
+            queue.clear();
+            free_slots.clear();
+            for (size_t i = ch->depth; i-- > 0;) free_slots.push_back(i);
+            next = redo;
+            if (stop || next >= max) break;
+            // the step of choice `redo` embeds choice redo − 1 at position n_past + redo − 1
+            const uint32_t t = (uint32_t)last_tok;
+            rc = htr_upload(dev, s->tok, &t, 4);
+            if (rc == 0) rc = set_state(s, s->n_past + (int)redo - 1, ch->seed_len + (int)redo);
+            continue;
+        }
         for (size_t i = 0; i < pd.n && !stop; i++) {
-            if (on_token && !on_token((int32_t)ch->h_ids[pd.slot * ch->chunk + i], user)) stop = true;
+            last_tok = (int32_t)ch->h_ids[pd.slot * ch->chunk + i];
+            if (on_token && !on_token(last_tok, user)) stop = true;
         }
         free_slots.push_back(pd.slot);
         if (stop) {
@@ -1139,7 +1257,12 @@ extern "C" int htr_decode_gpu(htr_session *s, htr_choice *ch, size_t max, htr_to
         }
     }
     if (rc == 0) rc = htr_sync(dev);
-    if (rc == 0 && s->fused) rc = token_step_check(s);
+    if (rc == 0) {
+        // launches past a stop ran unseen: a wait of theirs that ran out leaves the session on the per-kernel step
+        bool failed = false;
+        rc = token_step_err(s, &failed);
+        if (rc == 0 && failed) fall_back(s);
+    }
     if (rc < 0) return rc;
     // the steps launched: every choice but the first of the read advanced the position by one
     s->n_past += (int)(next - 1);

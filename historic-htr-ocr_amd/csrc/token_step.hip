@@ -903,9 +903,11 @@ int token_step_ni(int n_ctx) {
     return 0;
 }
 
+// the LM-head tail gives every workgroup at least one row (its first batch's loads are clamped into its share), so
+// the vocabulary holds at least one row a workgroup
 bool token_step_shape(const htr_text_config &c) {
     return c.dim == DIM && c.n_head * c.d_head == QD && c.n_kv * c.d_head == KVD && c.n_ff == NFF && c.d_head == D &&
-           c.n_head == 2 * c.n_kv && c.n_layer <= MAX_LAYERS && c.n_vocab <= NWG * MAX_HEAD_ROWS;
+           c.n_head == 2 * c.n_kv && c.n_layer <= MAX_LAYERS && c.n_vocab >= NWG && c.n_vocab <= NWG * MAX_HEAD_ROWS;
 }
 
 int token_step_fits(htr_device *dev, int n_ctx, const char **why) {
@@ -956,10 +958,23 @@ int token_step_xcds(htr_device *dev, const char **why) {
         unsigned seen = 0;
         for (int w = 0; w < NWG; w++) ok = ok && x[w] == x[w & 7];
         for (int w = 0; w < 8; w++) seen |= 1u << (x[w] & 7);
-        dev->xcd_round_robin = ok && seen == 0xffu;
+        dev->xcd_round_robin = ok && seen == 0xffu ? 1 : 0;
+        // the premise of the two XCD-local hand-overs: a word stored at workgroup scope is seen by the agent-scope
+        // loads of another workgroup on the same XCD (it stays in that XCD's L2). A cache behaviour of this part, not
+        // a guarantee of the memory model: probed once a device, on every XCD, with bounded waits (a word never seen
+        // ends its wait after 2^16 polls and the probe reports it)
+        for (int x = 0; x < 8 && dev->xcd_round_robin == 1; x++) {
+            double us = 0.0;
+            int vis = 0;
+            HTR_TRY(htr_debug_handover(dev, 0, x, x + 8, 1024, 16, 32, 1 << 16, &us, &vis));
+            if (!vis) dev->xcd_round_robin = 2;
+        }
     }
-    if (!dev->xcd_round_robin) *why = "its workgroups do not spread round-robin over 8 XCDs";
-    return dev->xcd_round_robin;
+    if (dev->xcd_round_robin == 0) *why = "its workgroups do not spread round-robin over 8 XCDs";
+    if (dev->xcd_round_robin == 2)
+        *why = "a word stored at workgroup scope was not seen by another workgroup of its XCD (the XCD-local "
+               "hand-overs' premise)";
+    return dev->xcd_round_robin == 1;
 }
 
 int launch_decode_token(htr_device *dev, hipStream_t st, int n_ctx, const TokArgs &a) {

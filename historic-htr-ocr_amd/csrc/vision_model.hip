@@ -393,7 +393,7 @@ extern "C" int htr_vision_load_gguf(htr_device *dev, htr_gguf *g, htr_vision **o
         if (gguf_has(g, absent)) return htr_fail("%s is in the GGUF but not part of this engine's graph", absent);
     GgufVisionFeed feed(g);
     HTR_TRY(feed.sg.init(dev));
-    HTR_TRY(htr_dev_alloc(dev, 4, HTR_MEM_WORK, (void **)&feed.over));
+    HTR_TRY(htr_dev_alloc_zero(dev, 4, HTR_MEM_WORK, (void **)&feed.over));
     auto *v = new htr_vision;
     int rc = build_vision(dev, c, feed, v);
     unsigned n_over = 0;

@@ -38,7 +38,7 @@ SYMBOLS = [
     "htr_decode_gpu", "htr_choose_host", "htr_generate", "htr_synth_q8_0", "htr_synth_normal",
     "htr_session_kv_cache", "htr_debug_last_kernel", "htr_capture_begin", "htr_capture_end", "htr_graph_launch",
     "htr_graph_free", "htr_decode_attention_static", "htr_session_profile_step", "htr_session_set_fused_step",
-    "htr_session_fused_step", "htr_session_profile_fused_step", "htr_debug_handover",
+    "htr_session_fused_step", "htr_session_profile_fused_step", "htr_debug_handover", "htr_session_set_wait_limit",
 ]
 STEP_EMBED, STEP_QKV, STEP_ATTENTION, STEP_O, STEP_FFN, STEP_DOWN, STEP_HEAD, STEP_ALL = 1, 2, 4, 8, 16, 32, 64, 127
 
@@ -180,6 +180,7 @@ def lib() -> C.CDLL:
             "htr_session_set_fused_step": (i32, [vp, i32]),
             "htr_session_fused_step": (i32, [vp, C.POINTER(i32), C.POINTER(C.c_char_p)]),
             "htr_session_profile_fused_step": (i32, [vp, i32, C.POINTER(C.c_double), i32]),
+            "htr_session_set_wait_limit": (i32, [vp, C.c_double]),
             "htr_debug_last_kernel": (i32, [vp, C.c_char_p, sz]),
             "htr_debug_handover": (i32, [vp, i32, i32, i32, i32, i32, i32, i32, C.POINTER(C.c_double), C.POINTER(i32)]),
             "htr_capture_begin": (i32, [vp]),
@@ -733,6 +734,11 @@ class Session:
         on, why = C.c_int(), C.c_char_p()
         _check(lib().htr_session_fused_step(self.h, C.byref(on), C.byref(why)))
         return why.value.decode() if why.value else None
+
+    def set_wait_limit(self, us: float | None) -> None:
+        """the one-launch step's bound on each of its waits, in µs (None: the default 0.2 s): the launches recorded
+        from now on carry it (tests of the error path make every wait run out from the host)"""
+        _check(lib().htr_session_set_wait_limit(self.h, float(us) if us else 0.0))
 
     def profile_fused_step(self, tok: int) -> np.ndarray:
         """one one-launch step of `tok` at n_past (not advanced): workgroup 0's stamps in µs after the embed,

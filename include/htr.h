@@ -39,6 +39,11 @@ typedef struct htr_choice htr_choice;
 const char *htr_last_error(void);
 
 /* ---- device (gpu.rs:1101-1345 Gpu::with_compute / drop, gpu.rs:1386-1396 alive, gpu.rs:884-897 FatalHook) ----- */
+/* The environment at open: HTR_GRAPHS=0 launches the decode's kernels one by one instead of replaying graphs;
+ * OCR_WGPU_COMPUTE picks the compute path (below); HTR_POISON=1 is the reference's OCR_WGPU_POISON=1 diagnostic
+ * (gpu.rs:739-768, 821-823, 1307-1310): memory the device hands out is filled with 0xFF bytes (NaN as f32 and f16)
+ * instead of zeros — except counters and tickets that must start at zero — and filled again when it is given back, so
+ * a kernel reading what nothing wrote (or what was freed) reads NaN. */
 int htr_device_open(int ordinal, htr_device **out);
 int htr_device_close(htr_device *dev);
 /* 0 while the device is healthy; < 0 with the sticky reason once it is dead (gpu.rs:1386-1396 Gpu::alive) */
@@ -100,7 +105,7 @@ typedef struct {
     uint64_t weights, kv_cache, work, readback;
 } htr_gpu_bytes;
 int htr_mem_live(htr_device *dev, htr_gpu_bytes *out);
-/* device memory of `bytes` bytes counted under `kind`; freed by htr_free. Zero-filled. */
+/* device memory of `bytes` bytes counted under `kind`; freed by htr_free. Zero-filled (0xFF bytes under HTR_POISON=1). */
 int htr_alloc(htr_device *dev, size_t bytes, int kind, void **d_out);
 int htr_free(htr_device *dev, void *d_ptr);
 /* host ↔ device copies on the device's stream; htr_download waits for it */
@@ -341,7 +346,11 @@ int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int 
  * HTR_FUSED_STEP=0 makes the per-kernel step the default instead); other models and the F32 path step kernel by
  * kernel. No reference counterpart (the reference records one dispatch per kernel).
  * set_fused_step(1) fails, with the reason, for a session that cannot take the one-launch form; fused_step reports the
- * session's form and, when the one-launch form is not available, why (a static string, or NULL).
+ * session's form and, when the one-launch form is not available or the session went back from it, why (a static
+ * string, or NULL). Every wait of the one-launch step is bounded (0.2 s of wall clock): a step whose wait ran out —
+ * its 256 workgroups were not all resident at once, as when another process or stream holds CUs — is redone on the
+ * per-kernel step, and the session keeps the per-kernel step from then on (htr_step redoes the step; htr_decode_gpu
+ * redoes the chunk, see there); set_fused_step(1) takes the one-launch step up again.
  * profile_fused_step runs one one-launch step of `tok` at the session's position (not advanced; its KV row written
  * there; no choice) and returns workgroup 0's 1 + 12·n_layer + 3 wall-clock stamps in µs after the embed: per layer
  * the input of each phase taken and its output written, for qkv, attention, merge, o, gate/up, down; then the LM
@@ -349,6 +358,10 @@ int htr_session_profile_step(htr_session *s, unsigned classes, int n_steps, int 
 int htr_session_set_fused_step(htr_session *s, int on);
 int htr_session_fused_step(htr_session *s, int *on, const char **why_not);
 int htr_session_profile_fused_step(htr_session *s, int32_t tok, double *us, int n);
+/* the one-launch step's bound on each wait, in µs (≤ 0: the default 0.2 s), carried by the launches recorded from now
+ * on. No reference counterpart: tests of the error path make every wait run out from the host (the kernels still end
+ * through their bounded waits). The environment variable HTR_FUSED_SPIN_US sets it when the session is made. */
+int htr_session_set_wait_limit(htr_session *s, double us);
 
 /* ---- the GPU token choice and the run-ahead decode (text.rs:165-232 Choice, text.rs:587-625 decode_gpu) -------- */
 /* the preset fields the choice reads (ocr-decode presets.rs:17-29) */
@@ -366,7 +379,11 @@ int htr_choice_free(htr_choice *c);
 typedef int (*htr_token_cb)(int32_t tok, void *user);
 /* TextModel::decode_gpu (text.rs:587-625): up to max choices, the first from the session's logits, each later one
  * after a decode step that embeds the previous choice on the device. Steps are replayed as HIP graphs, `chunk` per
- * launch, `depth` launches in flight; 4 bytes per token come back. on_token returning 0 ends the read. */
+ * launch, `depth` launches in flight; 4 bytes per token come back. on_token returning 0 ends the read. A chunk's ids
+ * reach on_token only once the chunk is known good (the reference's read_mapped_u32 fails before on_token sees a
+ * submission, text.rs:616-623): a chunk in which a one-launch step's wait ran out passes none of its ids on, the
+ * launches behind it are drained unseen, and the read goes on from the chunk's first step on the per-kernel step
+ * (frequency counts, position and token rewound), which the session then keeps. */
 int htr_decode_gpu(htr_session *s, htr_choice *c, size_t max, htr_token_cb on_token, void *user);
 
 /* ---- the CPU-choice decode (ocr-decode sampling.rs:23-89, 252-278) ------------------------------------------------ */

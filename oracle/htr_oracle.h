@@ -183,6 +183,13 @@ typedef struct {
 int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
                      const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
                      const uint8_t *rgb, int w, int h, int n_layers, float *out);
+/* the encoder resumed from a residual: x_in [px·py][dim] (the residual before layer `first`, of a px × py patch grid)
+ * through layers first … first + count − 1 → out [px·py][dim], or (project) further through the projector → out
+ * [px·py/4][proj_dim]. Pinned by composition: resumed from or_vision_encode's residual after `first` layers it is
+ * or_vision_encode after first + count (tests/test_vision_oracle.py). Returns 0, −1 on bad sizes. */
+int or_vision_resume(const or_vision_cfg *c, const or_vision_layer *layers, const float *input_norm,
+                     const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2, int px, int py, const float *x_in,
+                     int first, int count, int project, float *out);
 /* the same with f16 weight planes (an mmproj's bf16 weights as vision.rs:124-142 converts them at load:
  * f16(w · scale), the down projection × 64) */
 typedef struct {

@@ -227,28 +227,19 @@ static void vision_w(const uint8_t *src, int w16, size_t n, float scale, uint16_
     else or_q8_0_to_f16(src, n, scale, dst);
 }
 
-static int vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
-                         const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
-                         const uint8_t *rgb, int w, int h, int n_layers, float *out, int w16src) {
-    const int grid = c->patch * c->merge;
-    if (w % grid || h % grid || w <= 0 || h <= 0 || c->d_head != 64 || c->merge != 2) return -1;
-    if (n_layers > c->n_layer) return -1;
-    const int px = w / c->patch, py = h / c->patch, n = px * py, d = c->dim, f = c->n_ff, pp = 3 * c->patch * c->patch;
-    const int nl = n_layers < 0 ? c->n_layer : n_layers;
-    float lut[768];
-    or_pixel_lut(c->mean, c->std, lut);
-    float *P = malloc((size_t)n * pp * 4), *x = malloc((size_t)n * d * 4), *tmp = malloc((size_t)n * d * 4);
+/* layers[first … first + count) of the encoder on the residual x [n][d] of a px × py patch grid, in place
+ * (vision.rs:338-399) */
+static void vision_layers(const or_vision_cfg *c, const or_vision_layer *layers, int first, int count, int px, int py,
+                          float *x, int w16src) {
+    const int n = px * py, d = c->dim, f = c->n_ff;
     float *qb = malloc((size_t)n * d * 4), *kb = malloc((size_t)n * d * 4), *vb = malloc((size_t)n * d * 4);
     uint16_t *h16 = malloc((size_t)n * d * 2), *a16 = malloc((size_t)n * d * 2), *g16 = malloc((size_t)n * f * 2);
     uint16_t *w16 = malloc((size_t)f * d * 2), *w16b = malloc((size_t)f * d * 2);
     const int max_pos = px > py ? px : py;
     float *cs = malloc((size_t)2 * max_pos * (c->d_head / 4) * 2 * 4);
     or_rope2d_table(c->rope_theta, c->d_head, max_pos, cs);
-    or_patchify(rgb, w, px, n, c->patch, lut, P);
-    or_matmul_f32(P, patch_embd, tmp, n, d, pp, 0);
-    or_rms_norm(tmp, pre_ln, x, n, d, c->eps);
     const float scale = 1.0f / sqrtf((float)c->d_head);
-    for (int li = 0; li < nl; li++) {
+    for (int li = first; li < first + count; li++) {
         const or_vision_layer *L = &layers[li];
         or_rms_norm_h(x, L->ln1, h16, n, d, c->eps);
         vision_w(L->q, w16src, (size_t)d * d, 1.0f, w16);
@@ -269,37 +260,6 @@ static int vision_encode(const or_vision_cfg *c, const float *patch_embd, const 
         vision_w(L->down, w16src, (size_t)d * f, 64.0f, w16);
         or_matmul_f16(g16, w16, x, n, d, f, 1);
     }
-    int rc = 0;
-    if (n_layers >= 0) {
-        memcpy(out, x, (size_t)n * d * 4);
-    } else {
-        /* project (vision.rs:405-423): input_norm → unfold 2×2 → merger → mm.1 → gelu → mm.2, f32 activations and
-         * f16-valued weights */
-        const int n_out = n / 4, pd = c->proj_dim;
-        float *z = malloc((size_t)n * d * 4), *mg = malloc((size_t)n_out * d * 4), *m1 = malloc((size_t)n_out * pd * 4);
-        float *wf = malloc((size_t)d * 4 * d * 4);
-        uint16_t *wh = malloc((size_t)d * 4 * d * 2);
-        or_rms_norm(x, input_norm, tmp, n, d, c->eps);
-        or_unfold2x2(tmp, z, px, py, d);
-        vision_w(merger, w16src, (size_t)d * 4 * d, 1.0f, wh);
-        for (size_t i = 0; i < (size_t)d * 4 * d; i++) wf[i] = or_f32_from_f16(wh[i]);
-        or_matmul_f32(z, wf, mg, n_out, d, 4 * d, 0);
-        vision_w(mm1, w16src, (size_t)pd * d, 1.0f, wh);
-        for (size_t i = 0; i < (size_t)pd * d; i++) wf[i] = or_f32_from_f16(wh[i]);
-        or_matmul_f32(mg, wf, m1, n_out, pd, d, 0);
-        or_gelu(m1, (size_t)n_out * pd);
-        vision_w(mm2, w16src, (size_t)pd * pd, 1.0f, wh);
-        for (size_t i = 0; i < (size_t)pd * pd; i++) wf[i] = or_f32_from_f16(wh[i]);
-        or_matmul_f32(m1, wf, out, n_out, pd, pd, 0);
-        free(z);
-        free(mg);
-        free(m1);
-        free(wf);
-        free(wh);
-    }
-    free(P);
-    free(x);
-    free(tmp);
     free(qb);
     free(kb);
     free(vb);
@@ -309,7 +269,73 @@ static int vision_encode(const or_vision_cfg *c, const float *patch_embd, const 
     free(w16);
     free(w16b);
     free(cs);
-    return rc;
+}
+
+/* project (vision.rs:405-423): input_norm → unfold 2×2 → merger → mm.1 → gelu → mm.2, f32 activations and f16-valued
+ * weights; x [n][d] → out [n/4][proj_dim] */
+static void vision_project(const or_vision_cfg *c, const float *x, const float *input_norm, const uint8_t *merger,
+                           const uint8_t *mm1, const uint8_t *mm2, int px, int py, float *out, int w16src) {
+    const int n = px * py, d = c->dim, n_out = n / 4, pd = c->proj_dim;
+    float *tmp = malloc((size_t)n * d * 4);
+    float *z = malloc((size_t)n * d * 4), *mg = malloc((size_t)n_out * d * 4), *m1 = malloc((size_t)n_out * pd * 4);
+    float *wf = malloc((size_t)d * 4 * d * 4);
+    uint16_t *wh = malloc((size_t)d * 4 * d * 2);
+    or_rms_norm(x, input_norm, tmp, n, d, c->eps);
+    or_unfold2x2(tmp, z, px, py, d);
+    vision_w(merger, w16src, (size_t)d * 4 * d, 1.0f, wh);
+    for (size_t i = 0; i < (size_t)d * 4 * d; i++) wf[i] = or_f32_from_f16(wh[i]);
+    or_matmul_f32(z, wf, mg, n_out, d, 4 * d, 0);
+    vision_w(mm1, w16src, (size_t)pd * d, 1.0f, wh);
+    for (size_t i = 0; i < (size_t)pd * d; i++) wf[i] = or_f32_from_f16(wh[i]);
+    or_matmul_f32(mg, wf, m1, n_out, pd, d, 0);
+    or_gelu(m1, (size_t)n_out * pd);
+    vision_w(mm2, w16src, (size_t)pd * pd, 1.0f, wh);
+    for (size_t i = 0; i < (size_t)pd * pd; i++) wf[i] = or_f32_from_f16(wh[i]);
+    or_matmul_f32(m1, wf, out, n_out, pd, pd, 0);
+    free(tmp);
+    free(z);
+    free(mg);
+    free(m1);
+    free(wf);
+    free(wh);
+}
+
+static int vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,
+                         const float *input_norm, const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2,
+                         const uint8_t *rgb, int w, int h, int n_layers, float *out, int w16src) {
+    const int grid = c->patch * c->merge;
+    if (w % grid || h % grid || w <= 0 || h <= 0 || c->d_head != 64 || c->merge != 2) return -1;
+    if (n_layers > c->n_layer) return -1;
+    const int px = w / c->patch, py = h / c->patch, n = px * py, d = c->dim, pp = 3 * c->patch * c->patch;
+    const int nl = n_layers < 0 ? c->n_layer : n_layers;
+    float lut[768];
+    or_pixel_lut(c->mean, c->std, lut);
+    float *P = malloc((size_t)n * pp * 4), *x = malloc((size_t)n * d * 4), *tmp = malloc((size_t)n * d * 4);
+    or_patchify(rgb, w, px, n, c->patch, lut, P);
+    or_matmul_f32(P, patch_embd, tmp, n, d, pp, 0);
+    or_rms_norm(tmp, pre_ln, x, n, d, c->eps);
+    vision_layers(c, layers, 0, nl, px, py, x, w16src);
+    if (n_layers >= 0) memcpy(out, x, (size_t)n * d * 4);
+    else vision_project(c, x, input_norm, merger, mm1, mm2, px, py, out, w16src);
+    free(P);
+    free(x);
+    free(tmp);
+    return 0;
+}
+
+int or_vision_resume(const or_vision_cfg *c, const or_vision_layer *layers, const float *input_norm,
+                     const uint8_t *merger, const uint8_t *mm1, const uint8_t *mm2, int px, int py, const float *x_in,
+                     int first, int count, int project, float *out) {
+    if (px % c->merge || py % c->merge || px <= 0 || py <= 0 || c->d_head != 64 || c->merge != 2) return -1;
+    if (first < 0 || count < 0 || first + count > c->n_layer) return -1;
+    const size_t nd = (size_t)px * py * c->dim;
+    float *x = malloc(nd * 4);
+    memcpy(x, x_in, nd * 4);
+    vision_layers(c, layers, first, count, px, py, x, 0);
+    if (project) vision_project(c, x, input_norm, merger, mm1, mm2, px, py, out, 0);
+    else memcpy(out, x, nd * 4);
+    free(x);
+    return 0;
 }
 
 int or_vision_encode(const or_vision_cfg *c, const float *patch_embd, const float *pre_ln, const or_vision_layer *layers,

@@ -73,6 +73,7 @@ def lib() -> C.CDLL:
             "or_gelu": (None, [vp, sz]),
             "or_vision_encode": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
             "or_vision_encode_w16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+            "or_vision_resume": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, vp, i32, i32, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -464,6 +465,30 @@ class VisionCfg(C.Structure):
 
 class VisionLayerC(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")]
+
+
+def _vision_cfg_layers(cfg: dict, t: dict):
+    c = VisionCfg(cfg["n_layer"], cfg["dim"], cfg["n_head"], 64, cfg["n_ff"], cfg["patch"], 2, cfg["proj_dim"],
+                  cfg["eps"], cfg["rope_theta"], (C.c_float * 3)(*cfg["mean"]), (C.c_float * 3)(*cfg["std"]))
+    arr = (VisionLayerC * cfg["n_layer"])()
+    for i, ly in enumerate(t["layers"]):
+        arr[i] = VisionLayerC(**{k: _p(ly[k]) for k in ("ln1", "ln2", "q", "k", "v", "o", "gate", "up", "down")})
+    return c, arr
+
+
+def vision_resume(cfg: dict, t: dict, x: np.ndarray, px: int, py: int, first: int, count: int,
+                  project: bool = False) -> np.ndarray:
+    """the encoder resumed from the residual x [px·py][dim] before layer `first`: layers first … first + count − 1,
+    then (project) the projector (q8_0 host tensors, as vision_encode)"""
+    c, arr = _vision_cfg_layers(cfg, t)
+    x = np.ascontiguousarray(x, np.float32)
+    n = px * py
+    out = np.empty((n // 4, cfg["proj_dim"]) if project else (n, cfg["dim"]), np.float32)
+    rc = lib().or_vision_resume(C.byref(c), arr, _p(t["input_norm"]), _p(t["merger"]), _p(t["mm1"]), _p(t["mm2"]),
+                                px, py, _p(x), first, count, int(project), _p(out))
+    if rc != 0:
+        raise ValueError("oracle vision_resume: unsupported size")
+    return out
 
 
 def vision_encode(cfg: dict, t: dict, rgb: np.ndarray, n_layers: int = -1, w16: bool = False) -> np.ndarray:

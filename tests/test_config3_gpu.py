@@ -10,8 +10,10 @@ What each part is held to:
     sensitivity to f16 rounding: a 2e-7 nudge of one norm moves the oracle's f16 prefill by 1.9e-3 on this shape) and
     ≤ 1e-4 on the F32 path (exact q8_0 values, f32 sums in two orders);
   - the decode (what the bench times) from the same cache: the GPU's rows 0 … 1022 are handed to the oracle, which
-    then steps with its own arithmetic. The step for the prompt's last token and the last step of the read (1024 and
-    1535 keys: the fused attention's 64-key chunks, 16 and 24 of them) match the oracle's logits at rel-L2 ≤ 2e-4; every
+    then steps with its own arithmetic. On the f16 path the read runs on the one-launch step (k_decode_token<3>: 48-key
+    attention chunks at the 1536-row cache, 22 and 32 of them busy a KV head at 1024 and 1535 keys), which the test
+    asserts; on the F32 path the per-kernel step. The step for the prompt's last token and the last step of the read
+    (1024 and 1535 keys) match the oracle's logits at rel-L2 ≤ 2e-4; every
     one of the 512 tokens is the oracle's choice given the GPU's earlier tokens (teacher-forced), except documented
     near-ties (the oracle's logits of the two tokens within 1e-6 relative), which are printed.
 """
@@ -95,6 +97,10 @@ def test_config3_read_matches_oracle(dev, decoder, path):
                   depth=2)
     toks = s.decode_gpu(ch, NEW)
     assert len(toks) == NEW and s.n_past == PROMPT + NEW - 1
+    # the form that made the choices: the one-launch step on the f16 path (and it stayed on it), kernels on F32
+    assert s.fused_step == f16
+    if f16:
+        assert dev.last_kernel() == "k_decode_token<3>"
     ties = []
     pen = teacher_forced(o, lo1, prompt, toks, ties)
     # the read's last logits (position 1534, 1535 keys), penalised in place by the last choice on both sides
@@ -149,5 +155,45 @@ def test_fused_attention_ignores_stale_rows_past_the_position(dev):
             fa, fb = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
             assert np.all(np.isfinite(fa)) and np.all(np.abs(fa - fb) <= 2e-3 * (1 + np.abs(fb)))
         assert np.array_equal(kg[1], kbad[1]) and np.array_equal(vg[1], vbad[1])
+    s.free()
+    m.free()
+
+
+def test_fused_step_ignores_stale_rows_past_the_position(dev):
+    """the same on the one-launch step (the decoder's shape, 3 layers, a 1536-row cache: 48-key chunks): a session
+    rewound to 1000 with K = NaN and V = +inf planted from the position to the end of its chunk (rows 1000 … 1007) —
+    the step's logits are finite and the oracle's, its new row stored, the planted rows after it untouched"""
+    from htr import synth
+
+    cfg, te, on, layers = synth_text_model(n_layer=3, n_vocab=4096, seed=2024)
+    m = model_on(dev, htr.COMPUTE_F16, cfg, te, on, layers)
+    s = m.session(CTX)
+    assert s.fused_step
+    prompt = synth.prompt_ids(17, 1100, cfg["n_vocab"])
+    s.prefill(prompt)
+    pos = 1000
+    s.rewind(pos)
+    kvd = cfg["n_kv"] * 128
+    n_bad = 1008 - pos  # the rest of the 48-key chunk 960 … 1007 that holds position 1000
+    kbad = np.full((n_bad, kvd), 0x7E00, np.uint16)
+    vbad = np.full((n_bad, kvd), 0x7C00, np.uint16)
+    for li in range(cfg["n_layer"]):
+        s.set_kv_rows(li, pos, kbad, vbad)
+    o = orc.Session(cfg, te, on, layers, CTX, f16=True)
+    hand_over(s, o, pos, cfg["n_layer"])
+    tok = int(prompt[pos])
+    lg, lo = s.step(tok), o.step(tok)
+    assert dev.last_kernel() == "k_decode_token<3>" and s.fused_step
+    assert np.all(np.isfinite(lg))
+    e = rel_l2(lg, lo)
+    print(f"\n[stale rows, one-launch step] step at {pos} over planted inf / NaN rows: rel-L2 vs the oracle {e:.2e}")
+    assert e < 2e-4
+    for li in range(cfg["n_layer"]):
+        kg, vg = s.kv_rows(li, pos, n_bad)
+        ko, vo = o.get_kv(li, pos, 1)
+        for a, b in ((kg[0], ko[0]), (vg[0], vo[0])):
+            fa, fb = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
+            assert np.all(np.isfinite(fa)) and np.all(np.abs(fa - fb) <= 2e-3 * (1 + np.abs(fb)))
+        assert np.array_equal(kg[1:], kbad[1:]) and np.array_equal(vg[1:], vbad[1:])
     s.free()
     m.free()

@@ -224,27 +224,120 @@ def test_fused_step_profile_stamps(dev, model):
     s.free()
 
 
-def test_fused_step_reports_a_wait_that_ran_out(dev, model, monkeypatch):
-    """a 1 µs limit (HTR_FUSED_SPIN_US, read when the session is made): the waits run out, the launch still ends, and
-    the step reports it; with the normal limit the next session steps as before"""
+def test_fused_step_recovers_from_a_wait_that_ran_out(dev, model, monkeypatch):
+    """a 1 µs limit (HTR_FUSED_SPIN_US, read when the session is made): every wait of the one-launch step runs out, the
+    launch still ends, and the step is redone on the per-kernel step, which the session keeps (with the reason) — its
+    logits are then the per-kernel session's bit for bit. The measurement entry (profile_fused_step) reports the error
+    instead. With the normal limit and set_fused_step(1) the session steps in one launch again."""
     from htr import synth
 
     prompt = synth.prompt_ids(3, 40, N_VOCAB)
     monkeypatch.setenv("HTR_FUSED_SPIN_US", "1")
     s = model.session(CTX)
     monkeypatch.delenv("HTR_FUSED_SPIN_US")
+    sk = model.session(CTX)
+    sk.fused_step = False
     assert s.fused_step
-    s.prefill(prompt[:-1])
+    for x in (s, sk):
+        x.prefill(prompt[:-2])
     with pytest.raises(htr.HtrError, match="waited past its limit"):
-        s.step(int(prompt[-1]))
+        s.profile_fused_step(int(prompt[-2]))
+    assert s.fused_step  # a measurement does not switch the form
+    a, b = s.step(int(prompt[-2])), sk.step(int(prompt[-2]))
+    assert not s.fused_step and "ran past its limit" in s.fused_step_unavailable()
+    assert np.array_equal(a, b) and s.n_past == sk.n_past == len(prompt) - 1
+    s.set_wait_limit(None)
+    s.fused_step = True
+    assert s.fused_step and s.fused_step_unavailable() is None
+    s2 = model.session(CTX)
+    s2.prefill(prompt[:-1])
+    assert np.array_equal(s.step(int(prompt[-1])), s2.step(int(prompt[-1])))  # the one-launch step, as before
+    assert s.fused_step
+    for x in (s, sk, s2):
+        x.free()
+
+
+@pytest.mark.parametrize("where", ["first_chunk", "mid_read"])
+def test_fused_decode_gpu_recovers_from_a_wait_that_ran_out(dev, model, small_decoder, where, monkeypatch):
+    """decode_gpu (chunk 16, depth 2, rp 1.3 over 16 with fp 0.4) when waits of the one-launch step run out: in the
+    first chunk (a 1 µs limit from the session's start; the read's first choice is the choice kernel's, on the
+    prefill's logits) or in the third (the limit set to 1 µs from on_token at the read's 6th token: the chunks recorded
+    after it carry it). No id of a failed chunk reaches on_token; the read goes on from the chunk's first step on the
+    per-kernel step, with the frequency counts, position and token rewound. So: 96 ids, each passed once; in the first
+    case the whole read is the per-kernel session's read; in both, every id is the oracle's choice given the earlier
+    ones (teacher-forced from the GPU's prefill rows; near-ties logged), the session on the per-kernel step after."""
+    cfg, te, on, layers = small_decoder
+    from htr import synth
+
+    prompt = synth.prompt_ids(92, 600, N_VOCAB)
+    rp, window, fp, new = 1.3, 16, 0.4, 96
+    preset = htr.Preset(repetition_penalty=rp, repetition_window=window, frequency_penalty=fp, max_new_tokens=new)
+    if where == "first_chunk":
+        monkeypatch.setenv("HTR_FUSED_SPIN_US", "1")
+    s = model.session(CTX)
+    monkeypatch.delenv("HTR_FUSED_SPIN_US", raising=False)
+    assert s.fused_step
+    s.prefill(prompt)
+    ch = s.choice(preset, prompt, chunk=16, depth=2)
+    seen = []
+
+    def on_token(t):
+        seen.append(t)
+        if where == "mid_read" and len(seen) == 6:
+            s.set_wait_limit(1.0)
+        return True
+
+    toks = s.decode_gpu(ch, new, on_token)
+    assert toks == seen and len(toks) == new and s.n_past == len(prompt) + new - 1
+    assert not s.fused_step and "ran past its limit" in s.fused_step_unavailable()
+    ch.free()
+    # the per-kernel read from the same prefill
+    sk = model.session(CTX)
+    sk.fused_step = False
+    sk.prefill(prompt)
+    chk = sk.choice(preset, prompt, chunk=16, depth=2)
+    ref = sk.decode_gpu(chk, new)
+    chk.free()
+    if where == "first_chunk":
+        assert toks == ref
+    # teacher-forced: every id the oracle's choice given the read's earlier ones
+    o = orc.Session(cfg, te, on, layers, CTX, f16=True)
+    hand_over(s, o, len(prompt), N_LAYER)
+    o.rewind(len(prompt) - 1)
+    lo = o.step(int(prompt[-1]))
+    hist, counts, ties = [int(t) for t in prompt], {}, []
+    for i, t in enumerate(toks):
+        pen = lo.copy()
+        want = orc.choose(pen, rp, window, fp, hist, counts)
+        if want != t:
+            assert near_tie(pen, want, t), f"{where}: token {i}: oracle {want}, GPU {t}"
+            ties.append(i)
+        hist.append(int(t))
+        counts[int(t)] = counts.get(int(t), 0) + 1
+        if i + 1 < len(toks):
+            lo = o.step(int(t))
+    print(f"\n[recovery, {where}] {new} ids teacher-forced (near-ties {ties}); the per-kernel read's: "
+          f"{toks == ref}", flush=True)
     s.free()
-    s2, s3 = model.session(CTX), model.session(CTX)
-    s3.fused_step = False
-    for x in (s2, s3):
-        x.prefill(prompt[:-1])
-    assert rel_l2(s2.step(int(prompt[-1])), s3.step(int(prompt[-1]))) < 1e-5
-    s2.free()
-    s3.free()
+    sk.free()
+
+
+def test_fused_step_refused_for_a_small_vocabulary(dev):
+    """the LM-head tail gives each of the 256 workgroups at least one row: a decoder of the right shape with 100 ids
+    steps kernel by kernel, and says why"""
+    cfg, te, on, layers = synth_text_model(n_layer=1, n_vocab=100, seed=77)
+    keep = dev.compute
+    dev.compute = htr.COMPUTE_F16
+    try:
+        m = htr.TextModel(dev, to_htr_cfg(cfg), te, on, layers)
+    finally:
+        dev.compute = keep
+    s = m.session(64)
+    assert not s.fused_step and "256 to 262144 ids" in s.fused_step_unavailable()
+    s.prefill(np.arange(10, dtype=np.int32))
+    assert np.all(np.isfinite(s.step(11)))
+    s.free()
+    m.free()
 
 
 def test_fused_step_at_its_shape_limits(dev):
@@ -272,12 +365,31 @@ def test_fused_step_at_its_shape_limits(dev):
         assert rel_l2(lf, lk) < 1e-5
         toks = []
         for s in (sf, sk):
+            s.rewind(len(prompt) - 1)
+            first = s.step(int(prompt[-1]))
             ch = s.choice(htr.Preset(repetition_penalty=1.3, repetition_window=64, max_new_tokens=48), prompt,
                           chunk=8, depth=2)
             toks.append(s.decode_gpu(ch, 48))
             ch.free()
-        print(f"\n[fused step, 42 layers, 262144 ids] the two forms' tokens agree: {toks[0] == toks[1]}", flush=True)
-        assert toks[0][:8] == toks[1][:8]
+            # every token the oracle's choice given the read's earlier ones (teacher-forced from the GPU's rows)
+            o = orc.Session(cfg, te, on, layers, 512, f16=True)
+            hand_over(s, o, len(prompt) - 1, cfg["n_layer"])
+            lo = o.step(int(prompt[-1]))
+            assert rel_l2(first, lo) < 2e-4
+            hist, ties = [int(t) for t in prompt], []
+            for i, t in enumerate(toks[-1]):
+                pen = lo.copy()
+                want = orc.choose(pen, 1.3, 64, 0.0, hist)
+                if want != t:
+                    assert near_tie(pen, want, t), f"{'fused' if s is sf else 'per-kernel'} token {i}: {want} vs {t}"
+                    ties.append(i)
+                hist.append(int(t))
+                if i + 1 < len(toks[-1]):
+                    lo = o.step(int(t))
+            del o
+            print(f"\n[fused step, 42 layers, 262144 ids] {'one-launch' if s is sf else 'per-kernel'} read: 48 tokens "
+                  f"teacher-forced, near-ties {ties}", flush=True)
+        print(f"[fused step, 42 layers, 262144 ids] the two forms' tokens agree: {toks[0] == toks[1]}", flush=True)
         sf.rewind(200)
         us = sf.profile_fused_step(int(prompt[200]))
         assert us.shape == (1 + 12 * 42 + 3,) and np.all(np.diff(us) >= 0.0)

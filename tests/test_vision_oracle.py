@@ -257,3 +257,23 @@ def test_vision_encode_on_f16_planes_is_the_q8_0_encode():
         a = orc.vision_encode(cfg, t, rgb, nl)
         b = orc.vision_encode(cfg, t16, rgb, nl, w16=True)
         assert np.array_equal(a, b), nl
+
+
+def test_vision_resume_composes_with_encode():
+    """or_vision_resume (the encoder from a given residual, the per-layer check of the GPU's page encode) is the same
+    layer loop and projector: resumed from vision_encode's residual after L layers, it is vision_encode after L + k
+    layers, and after every layer and the projector, bit for bit"""
+    cfg = tiny_vision_cfg()
+    t = tiny_vision_tensors(cfg)
+    rgb = tiny_page(cfg, 56, 84)
+    px, py = 56 // cfg["patch"], 84 // cfg["patch"]
+    n_layer = cfg["n_layer"]
+    x0 = orc.vision_encode(cfg, t, rgb, 0)
+    for first in range(n_layer):
+        x = orc.vision_encode(cfg, t, rgb, first)
+        for count in range(n_layer - first + 1):
+            got = orc.vision_resume(cfg, t, x, px, py, first, count)
+            assert np.array_equal(got, orc.vision_encode(cfg, t, rgb, first + count)), (first, count)
+    assert np.array_equal(orc.vision_resume(cfg, t, x0, px, py, 0, n_layer, project=True), orc.vision_encode(cfg, t, rgb))
+    # and it is not the identity: a layer moves the residual
+    assert rel_l2(orc.vision_resume(cfg, t, x0, px, py, 0, 1), x0) > 1e-3
