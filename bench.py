@@ -7,20 +7,27 @@ HIP graphs. Each step rewinds the session to 1023 positions, runs one decode ste
 decodes 512 tokens (so every step is the same read).
 
 Also measured in the same run (one JSON line):
-  roofline      the q8_0 matvec kernel's streaming rate at the 3072 × 1024 projection (W [3072 × 1024], x f32[1024],
-                y f32[3072]) over a rotation of 128 distinct W copies (428 MB > the 256 MB Infinity Cache), 128 matvecs
-                per launch; algorithmic bytes 3,358,720 per matvec; HIP events on the library's stream
+  roofline      the decode's own kernel, k_decode_token (one token in one launch): its algorithmic bytes per token at
+                the read's mean context (1279.5 keys: 781,569,024 B) over its average launch time there (a graph of 16
+                launches at 1280 keys, replayed; HIP events on the library's stream), against 8 TB/s; traffic from the
+                committed FETCH_SIZE / WRITE_SIZE summary of the same kernel over the bench's read
   roofline_by_config
                 every workload's fraction of its roofline: the decode (bytes per token × tokens/s), one matvec per
-                graph node over the rotation, the choice per step (graphed) and 512 rows batched, the attention at
-                512 / 2048 / 8192 keys (graphed over ≥ 512 MiB of caches), the vision GEMMs (MFMA)
+                graph node over the rotation and the q8_0 matvec kernel's streaming rate (k_dmv_many: 128 matvecs of
+                W [3072 × 1024] per launch over 128 distinct copies, 430 MB > the 256 MB Infinity Cache), the choice
+                per step (graphed) and 512 rows batched, the attention at 512 / 2048 / 8192 keys (graphed over
+                ≥ 512 MiB of caches), the vision GEMMs (MFMA)
   decode.phases the decode step's kernel classes timed alone in graphs (htr_session_profile_step) at the read's mean
                 context
   matvec        the same kernel one matvec per launch / per graph node over the rotation (and the 64-copy figure)
   choose        windowed penalty + argmax over 151936 logits: 10k seeded steps over 512 rows of the choice workload
-                (planted maxima, 25 % repeated window ids), launched one by one and replayed as graphs; all rows batched
+                (planted maxima, 25 % repeated window ids), launched one by one and replayed as graphs, the rows
+                restored between passes (each step sees its seeded logits); all rows batched; every pass's 512 tokens
+                the same
   attention     GQA decode attention (16 q / 8 kv heads × 128) at 512 / 2048 / 8192 keys over ≥ 512 MiB of rotating caches
-  cpu_baseline  the oracle (oracle/, a C restatement of the reference path, OpenMP) decoding on the host cores
+  cpu_baseline  the oracle (oracle/, a C restatement of the reference path, OpenMP) decoding the read's own keys 1024 …
+                1535 on the host cores from the GPU's prefill rows, and the choice on the choose leg's 512 rows, whose
+                tokens it checks
 """
 from __future__ import annotations
 
@@ -148,8 +155,12 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
         phases = decode_phases(s, mid, cfg["n_layer"]) if GRAPHS else None
     prefill_f32_s = (prefill_on_f32_path(dev, cfg, te, on, layers, prompt[:-1]) if path == "f16" else prefill_s) \
         if ab else float("nan")
+    # the one-launch step's average launch at the read's mean context: a graph of 16 launches at position 1279
+    # (1280 keys), replayed, HIP events on the library's stream (htr_session_profile_step)
+    kernel_us = fused_phases["step_in_graph_us"] if fused_phases else float("nan")
     out = {
         "step_form": form,
+        "kernel_us_at_mean_keys": kernel_us,
         "tok_s": tok_s,
         "bytes_per_token": bpt,
         "mean_keys": mean_keys,
@@ -167,6 +178,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
         "prefill_f32_path_ms": prefill_f32_s * 1e3,
         "reads_identical": same,
         "first_tokens": reads[0][:8],
+        "first_tokens_all": reads[0],
     }
     return out, (cfg, te, on, layers, prompt), (m, s, ch)
 
@@ -291,57 +303,107 @@ def bench_matvec(dev, copies=128, reps=10):
 def bench_choose(dev, n_steps=10000, n_buf=512, n_vocab=151936, window=64):
     """the choice workload (htr.synth.choice_inputs: N(0, 3) logits with 8 planted equal maxima, 3 on window ids; 64
     uniform window ids with 25 % repeats) in 512 rows, 311 MB of logits: 10k single steps over the rows launched one by
-    one, the same replayed as graphs of 512 steps, and all rows in one launch"""
+    one (passes of 512 steps), the same replayed as graphs of 512 steps, and all rows in one launch. The choice
+    penalises its row in place, so the rows are restored from a pristine copy between passes (untimed): every step sees
+    its row's seeded logits, an independent step. Each row's token has its own slot; every pass must give the same 512
+    tokens (the CPU leg checks them against the oracle's choice on the same rows). → (result, (host logits, host
+    windows, tokens))"""
     from htr import synth
 
     log(f"choose: {n_steps} steps over {n_buf} rows of the choice workload")
     logits = dev.alloc(n_buf * n_vocab * 4)
+    pristine = dev.alloc(n_buf * n_vocab * 4)
+    host_l = np.empty((n_buf, n_vocab), np.float32)
     hist_h = np.zeros((n_buf, window + 1), np.uint32)
     block = 32
     for i in range(0, n_buf, block):
         lg, h = synth.choice_inputs(7000 + i, block, n_vocab, window)
-        htr.lib().htr_upload(dev.h, logits.ptr + i * n_vocab * 4, lg.ctypes.data, lg.nbytes)
+        host_l[i:i + block] = lg
         hist_h[i:i + block, :window] = h
+    pristine.upload(host_l)
     hist = dev.upload(hist_h)
-    tok = dev.alloc(4)
+    tok = dev.alloc(n_buf * 4)
     L = htr.lib()
     stride = (window + 1) * 4
 
     def one(i):
-        rc = L.htr_choose(dev.h, logits.ptr + (i % n_buf) * n_vocab * 4, n_vocab, hist.ptr + (i % n_buf) * stride,
-                          window, window, 1.1, 0.0, None, None, tok.ptr)
+        r = i % n_buf
+        rc = L.htr_choose(dev.h, logits.ptr + r * n_vocab * 4, n_vocab, hist.ptr + r * stride, window, window, 1.1,
+                          0.0, None, None, tok.ptr + 4 * r)
         if rc < 0:
             raise htr.HtrError(htr.last_error())
 
+    def restore():
+        logits.copy_from(pristine)
+        dev.sync()
+
+    restore()
     for i in range(16):
         one(i)
-    dev.sync()
-    dev.timer_begin()
-    for i in range(n_steps):
-        one(i)
-    ms = dev.timer_end()
-    res = {"steps": n_steps, "us_per_step": ms / n_steps * 1e3,
-           "GBs": CHOOSE_STEP_BYTES / (ms / n_steps * 1e-3) / 1e9}
-    us = graphed(dev, [lambda i=i: one(i) for i in range(n_buf)], max(1, n_steps // n_buf))
+    restore()
+    passes, ms, done = [], 0.0, 0
+    while done < n_steps:
+        n = min(n_buf, n_steps - done)
+        dev.timer_begin()
+        for i in range(n):
+            one(i)
+        ms += dev.timer_end()
+        passes.append(tok.download(np.uint32, n).copy())
+        restore()
+        done += n
+    n_rows = passes[0].size  # the rows of the first pass (all 512 unless fewer steps were asked)
+    same = all(np.array_equal(p, passes[0][:p.size]) for p in passes)
+    res = {"steps": n_steps, "us_per_step": ms / n_steps * 1e3, "GBs": CHOOSE_STEP_BYTES / (ms / n_steps * 1e-3) / 1e9,
+           "passes_of_512": len(passes), "passes_identical": same,
+           "rows_restored_between_passes": True}
+    # graphs of 512 steps, replayed once per pass with the rows restored between replays
+    if GRAPHS:
+        dev.capture_begin()
+        try:
+            for i in range(n_buf):
+                one(i)
+        finally:
+            g = dev.capture_end()
+        g.launch()
+        restore()
+        reps = max(1, n_steps // n_buf)
+        ms_g = 0.0
+        for _ in range(reps):
+            dev.timer_begin()
+            g.launch()
+            ms_g += dev.timer_end()
+            same = same and np.array_equal(tok.download(np.uint32, n_rows), passes[0])
+            restore()
+        g.free()
+        us = ms_g * 1e3 / (reps * n_buf)
+        res["graph_passes_identical"] = same
+    else:
+        us = float("nan")
     res["graph_node_us_per_step"] = us
     res["graph_node_GBs"] = CHOOSE_STEP_BYTES / (us * 1e-6) / 1e9
     res["graph_node_frac"] = res["graph_node_GBs"] / HBM_PEAK_GBS
-    # the 512 rows in one launch (independent rows, each with its own window)
+    # the 512 rows in one launch (independent rows, each with its own window), restored between launches
     toks = dev.alloc(n_buf * 4)
     htr.choose_many(dev, logits, n_vocab, n_buf, hist, window + 1, window, window, 1.1, toks)
-    dev.timer_begin()
+    batched_same = np.array_equal(toks.download(np.uint32, n_rows), passes[0])
+    restore()
+    ms = 0.0
     for _ in range(5):
+        dev.timer_begin()
         htr.choose_many(dev, logits, n_vocab, n_buf, hist, window + 1, window, window, 1.1, toks)
-    ms = dev.timer_end() / 5
+        ms += dev.timer_end()
+        restore()
+    ms /= 5
     res["batched_rows_per_launch"] = n_buf
+    res["batched_tokens_equal_single_steps"] = batched_same
     res["batched_us_per_row"] = ms / n_buf * 1e3
     res["batched_GBs"] = n_buf * CHOOSE_STEP_BYTES / (ms * 1e-3) / 1e9
     res["batched_frac"] = res["batched_GBs"] / HBM_PEAK_GBS
-    for b in (logits, hist, tok, toks):
+    for b in (logits, pristine, hist, tok, toks):
         b.free()
     log(f"choose: {res['us_per_step']:.2f} us/step launched, {us:.2f} us as graph nodes, batched "
-        f"{res['batched_GBs']:.0f} GB/s")
-    return res
+        f"{res['batched_GBs']:.0f} GB/s; every pass the same 512 tokens: {same}")
+    return res, (host_l[:n_rows], hist_h[:n_rows, :window].astype(np.int64), passes[0].astype(np.int64))
 
 
 def bench_attention(dev, n_head=16, n_kv=8, rotate_mib=512):
@@ -523,25 +585,27 @@ def _timed(fn, budget_s, min_n=3):
     return n, time.perf_counter() - t0
 
 
-def cpu_configs(orc, threads, budget_s=2.0):
+def cpu_configs(orc, threads, choice_rows=None, budget_s=2.0):
     """the oracle on the host cores for the other single-kernel workloads: the q8_0 matvec W [3072 x 1024], the
-    penalised greedy choice over 151,936 logits (window 64, rp 1.1), the decode attention (16 / 8 heads x 128) at 512 /
-    2048 / 8192 keys"""
+    penalised greedy choice over 151,936 logits (window 64, rp 1.1) — on the choose leg's own 512 rows, whose tokens it
+    checks — and the decode attention (16 / 8 heads x 128) at 512 / 2048 / 8192 keys"""
     r = np.random.default_rng(0)
     w = orc.q8_0_quantize(r.normal(0, 1, 3072 * 1024).astype(np.float32))[0]
     x = r.normal(0, 1, 1024).astype(np.float32)
     n, dt = _timed(lambda: orc.matvec_q8_0(w, 3072, 1024, x), budget_s)
     res = {"matvec_w3072x1024": {"us": dt / n * 1e6, "GBs": MATVEC_UNIT_BYTES / (dt / n) / 1e9, "calls": n}}
-    rows = [r.normal(0, 3, 151936).astype(np.float32) for _ in range(4)]
-    hist = [int(t) for t in r.integers(0, 151936, 64)]
-    spent, n = 0.0, 0
-    while n < 3 or spent < budget_s:
-        lo = rows[n % 4].copy()  # choose penalises in place: a fresh row each step, copied outside the timing
-        t0 = time.perf_counter()
-        orc.choose(lo, 1.1, 64, 0.0, hist)
-        spent += time.perf_counter() - t0
-        n += 1
-    res["choose_151936"] = {"us": spent / n * 1e6, "calls": n}
+    if choice_rows is not None:
+        host_l, hist, gpu_toks = choice_rows
+        spent, agree = 0.0, 0
+        for i in range(host_l.shape[0]):
+            lo = host_l[i].copy()  # choose penalises in place: a fresh row each step, copied outside the timing
+            t0 = time.perf_counter()
+            t = orc.choose(lo, 1.1, 64, 0.0, [int(v) for v in hist[i]])
+            spent += time.perf_counter() - t0
+            agree += int(t == gpu_toks[i])
+        res["choose_151936"] = {"us": spent / host_l.shape[0] * 1e6, "calls": host_l.shape[0],
+                                "rows_checked": host_l.shape[0], "gpu_tokens_equal": agree == host_l.shape[0],
+                                "gpu_tokens_equal_count": agree}
     q = r.normal(0, 1, 16 * 128).astype(np.float32)
     sc = float(np.float32(1 / np.sqrt(128)))
     for L in (512, 2048, 8192):
@@ -552,9 +616,11 @@ def cpu_configs(orc, threads, budget_s=2.0):
     return res
 
 
-def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
-    """the oracle (C restatement of the reference decode path, OpenMP) decoding on the host cores; the other
-    single-kernel workloads timed the same way under per_config"""
+def cpu_baseline(model_inputs, prefill_rows, choice_rows=None, budget_s=25.0, n_new=512):
+    """the oracle (C restatement of the reference decode path, OpenMP) decoding the workload on the host cores: the
+    GPU's prefill rows 0 … 1022 of every layer handed to it, one step for the prompt's last token, then greedy tokens
+    (rp 1.1 / 64) over keys 1024 … 1535 — the measured read's own keys — until the read's 512 or the time budget; the
+    other single-kernel workloads timed the same way under per_config"""
     # the oracle (test infrastructure): imported here, for the CPU baseline leg only
     import importlib.util
 
@@ -564,25 +630,35 @@ def cpu_baseline(model_inputs, budget_s=10.0, prompt_n=32, max_new=1500):
 
     cfg, te, on, layers, prompt = model_inputs
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    o = orc.Session(cfg, te, on, layers, prompt_n + max_new + 1, f16=True)  # the measured path's fused step
-    lo = o.prefill(prompt[:prompt_n])
-    hist = [int(t) for t in prompt[:prompt_n]]
+    n0 = len(prompt) - 1
+    o = orc.Session(cfg, te, on, layers, len(prompt) + n_new, f16=True)  # the measured path's fused step
+    for li, (k, v) in enumerate(prefill_rows):
+        o.set_kv(li, 0, k, v)
+    o.rewind(n0)
+    lo = o.step(int(prompt[-1]))
+    hist = [int(t) for t in prompt]
+    toks = []
     t0 = time.perf_counter()
     n = 0
-    while n < max_new and (n < 3 or time.perf_counter() - t0 < budget_s):
+    while n < n_new and (n < 3 or time.perf_counter() - t0 < budget_s):
         t = orc.choose(lo, 1.1, 64, 0.0, hist)
         hist.append(t)
-        lo = o.step(t)
+        toks.append(t)
         n += 1
+        if n < n_new:
+            lo = o.step(t)
     dt = time.perf_counter() - t0
-    log(f"cpu baseline: {n} tokens in {dt:.1f} s on {threads} threads")
-    per = cpu_configs(orc, threads)
-    log(f"cpu baseline: matvec {per['matvec_w3072x1024']['GBs']:.1f} GB/s, choose {per['choose_151936']['us']:.0f} us, "
-        f"attention 8192 keys {per['attention_8192']['us']:.0f} us")
+    log(f"cpu baseline: {n} tokens in {dt:.1f} s on {threads} threads (keys {n0 + 1} … {n0 + n})")
+    per = cpu_configs(orc, threads, choice_rows)
+    ch = per.get("choose_151936", {})
+    log(f"cpu baseline: matvec {per['matvec_w3072x1024']['GBs']:.1f} GB/s, choose {ch.get('us', float('nan')):.0f} us "
+        f"(the GPU's 512 tokens of the choose leg equal: {ch.get('gpu_tokens_equal')}), attention 8192 keys "
+        f"{per['attention_8192']['us']:.0f} us")
     return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port", "per_config": per,
-            "sample": f"oracle (C restatement, OpenMP; the f16 paths' fused step) greedy decode of {n} tokens (rp 1.1 / 64) of the same 28-layer q8_0 "
-                      f"model after a {prompt_n}-token prompt: attention context {prompt_n}-{prompt_n + n} keys, shorter "
-                      f"than the workload's 1024-1536 (the 633 MB of weights per token dominate either way)"}
+            "tokens": toks,
+            "sample": f"oracle (C restatement, OpenMP; the f16 paths' fused step) greedy decode of {n} tokens (rp 1.1 / "
+                      f"64) of the same 28-layer q8_0 model from the GPU's prefill rows of the same 1024-token prompt: "
+                      f"keys {n0 + 1}-{n0 + n}, the measured read's own"}
 
 
 def no_nan(v):
@@ -612,8 +688,12 @@ def roofline_by_config(r: dict) -> dict:
                                             "frac": m["graph_node_128_copies_frac"],
                                             "unit": "one W [3072 x 1024] matvec a graph node, 128 copies rotated"}
         out["config0_matvec_batched"] = {"bound": "hbm", "achieved_GBs": m["batched_launch_GBs"],
-                                         "frac": m["batched_frac"],
-                                         "unit": "128 matvecs in one launch (the kernel's streaming rate)"}
+                                         "frac": m["batched_frac"], "kernel": "k_dmv_many",
+                                         "avg_launch_us": m["batched_launch_us"],
+                                         "algorithmic_bytes_per_launch": m["batched_bytes_per_launch"],
+                                         "traffic": load_traffic(),
+                                         "unit": "128 matvecs in one launch over 128 distinct W copies (430 MB, past "
+                                                 "the 256 MB Infinity Cache): the kernel's streaming rate"}
     if "choose" in r:
         c = r["choose"]
         out["config1_choice_graph_node"] = {"bound": "hbm", "achieved_GBs": c["graph_node_GBs"],
@@ -675,31 +755,37 @@ def main():
                                "repetition penalty 1.1 over a 64-token window; one step = one 512-token read",
                    "device": name},
     }
-    decode_inputs = None
+    decode_inputs, prefill_rows, choice_rows = None, None, None
     dev.phase("decode")
     if want("decode"):
         d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup, ab=not args.no_ab)
         result["value"] = d["tok_s"]
         result["ms_per_step"] = d["ms_per_read"]
         result["decode"] = d
+        kus = d["kernel_us_at_mean_keys"]
+        if kus == kus:
+            ach = d["bytes_per_token"] / (kus * 1e-6) / 1e9
+            result["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": ach / HBM_PEAK_GBS,
+                                  "traffic": load_traffic("k_decode_token_traffic.json", "hbm_bytes_per_token"),
+                                  "kernel": "k_decode_token<3>: one decode token of the 28-layer q8_0 decoder in one "
+                                            "launch (embed, 28 layers, LM head, greedy choice)",
+                                  "algorithmic_bytes_per_launch": d["bytes_per_token"],
+                                  "avg_launch_us": kus,
+                                  "launch_timing": "a graph of 16 launches at position 1279 (1280 keys, the read's "
+                                                   "mean), replayed 20 times, HIP events on the library's stream"}
+        if not args.skip_cpu:
+            m_, s_, _ = keep
+            prefill_rows = [s_.kv_rows(li, 0, len(decode_inputs[4]) - 1) for li in range(decode_inputs[0]["n_layer"])]
         for obj in keep[::-1]:
             obj.free()
     dev.phase("matvec")
     if want("matvec"):
         mv = bench_matvec(dev)
         result["matvec"] = mv
-        ach = mv["batched_launch_GBs"]
-        result["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": ach / HBM_PEAK_GBS, "traffic": load_traffic(),
-                              "kernel": "k_dmv_many: q8_0 matvec W[3072x1024] f32 x[1024] -> y[3072], 128 distinct W "
-                                        "copies per launch (430 MB, past the 256 MB Infinity Cache); algorithmic "
-                                        "bytes 3,358,720 per matvec. The matvec kernel's streaming rate: the decode "
-                                        "runs its matvecs one a graph node, see roofline_by_config",
-                              "algorithmic_bytes_per_launch": mv["batched_bytes_per_launch"],
-                              "avg_launch_us": mv["batched_launch_us"]}
     dev.phase("choose")
     if want("choose"):
-        result["choose"] = bench_choose(dev, n_steps=args.choose_steps)
+        result["choose"], choice_rows = bench_choose(dev, n_steps=args.choose_steps)
     dev.phase("attention")
     if want("attention"):
         result["attention"] = bench_attention(dev)
@@ -716,7 +802,12 @@ def main():
     dev.phase("-")
     result["roofline_by_config"] = roofline_by_config(result)
     if decode_inputs is not None and not args.skip_cpu:
-        result["cpu_baseline"] = cpu_baseline(decode_inputs)
+        cb = cpu_baseline(decode_inputs, prefill_rows, choice_rows)
+        toks = cb.pop("tokens")
+        cb["same_tokens_as_gpu_read"] = toks == result["decode"]["first_tokens_all"][:len(toks)]
+        result["cpu_baseline"] = cb
+    if "decode" in result:
+        result["decode"].pop("first_tokens_all")
     dev.close()
     print(json.dumps(no_nan(result)), flush=True)
 

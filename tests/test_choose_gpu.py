@@ -143,3 +143,44 @@ def synth_choice(seed, rows, n_vocab, window):
     from htr import synth
 
     return synth.choice_inputs(seed, rows, n_vocab, window)
+
+
+def test_config1_bench_rows_bit_exact(dev):
+    """the bench's own choice workload: its 512 rows (htr.synth.choice_inputs, seeds 7000 + 32·b), every row as a
+    single launch (k_choose on one row, as the bench's 10k steps run it) and all 512 in one launch — every token and
+    every penalised row the oracle's bit for bit; a second pass on rows restored from the pristine copy gives the same
+    tokens (the bench restores its rows between passes so each step sees its seeded logits)"""
+    from htr import synth
+
+    n_buf, n_vocab, window, rp = 512, 151936, 64, 1.1
+    logits = np.empty((n_buf, n_vocab), np.float32)
+    hist = np.zeros((n_buf, window + 1), np.uint32)
+    for i in range(0, n_buf, 32):
+        lg, h = synth.choice_inputs(7000 + i, 32, n_vocab, window)
+        logits[i:i + 32] = lg
+        hist[i:i + 32, :window] = h
+    want, pens = [], []
+    for r in range(n_buf):
+        ref = logits[r].copy()
+        want.append(orc.choose(ref, rp, window, 0.0, [int(t) for t in hist[r, :window]]))
+        pens.append(ref)
+    lb, hb, tok = dev.upload(logits), dev.upload(hist), dev.alloc(n_buf * 4)
+    L = htr.lib()
+    for p in range(2):
+        lb.upload(logits)
+        for r in range(n_buf):
+            rc = L.htr_choose(dev.h, lb.ptr + r * n_vocab * 4, n_vocab, hb.ptr + r * (window + 1) * 4, window, window,
+                              rp, 0.0, None, None, tok.ptr + 4 * r)
+            assert rc == 0, htr.last_error()
+        got = tok.download(np.uint32, n_buf)
+        assert [int(t) for t in got] == want, p
+    pen = lb.download(np.float32).reshape(n_buf, n_vocab)
+    for r in range(0, n_buf, 37):
+        assert np.array_equal(pen[r].view(np.uint32), pens[r].view(np.uint32)), r
+    lb.upload(logits)
+    htr.choose_many(dev, lb, n_vocab, n_buf, hb, window + 1, window, window, rp, tok)
+    assert [int(t) for t in tok.download(np.uint32, n_buf)] == want
+    print(f"\n[config 1] the bench's 512 rows: single launches (twice) and one batched launch equal the oracle's "
+          f"choice; {len(set(want))} distinct tokens", flush=True)
+    for b in (lb, hb, tok):
+        b.free()

@@ -155,7 +155,10 @@ def test_fused_choice_exact_ties(dev, tied_model, rp, window, fp):
     prompt = synth.prompt_ids(808, 300, N_VOCAB)
     prompt[-6:] = [16, 101, 4001, 7, 2047, 9]
     toks, cov = read_and_check(dev, tied_model, prompt, rp, window, fp, 48, f"tied rows rp {rp} w {window} fp {fp}")
-    assert cov["tied_max"] >= 4 and cov["ties_across_shares"] >= 1
+    if rp >= 1.0:  # rp < 1 raises a chosen member over its twin: the tie breaks once one of them is in the window
+        assert cov["tied_max"] >= 4 and cov["ties_across_shares"] >= 1
+    else:
+        assert cov["tied_max"] >= 1
     if rp != 1.0:
         assert cov["reversed"] >= 1
 
@@ -212,8 +215,10 @@ def test_fused_choice_designed_logits(dev, seed, rp, window, fp):
     finally:
         m.free()
     assert cov["tied_max"] >= 4 and cov["zero_max"] >= 1 and cov["nan"] == 48
-    if seed == 11:
-        assert cov["neg_inf"] >= 1 and cov["reversed"] >= 1
+    if seed == 11:  # the read visits element 5 (−inf at R_NEG_INF); rp > 1 reverses tied leaders
+        assert cov["neg_inf"] >= 1 and (rp < 1.0 or cov["reversed"] >= 1)
+    else:  # a read whose every choice is among ties at +0
+        assert cov["zero_max"] >= 40
 
 
 def test_fused_choice_nan_at_index_0(dev):

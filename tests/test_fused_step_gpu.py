@@ -249,10 +249,14 @@ def test_fused_step_recovers_from_a_wait_that_ran_out(dev, model, monkeypatch):
     s.set_wait_limit(None)
     s.fused_step = True
     assert s.fused_step and s.fused_step_unavailable() is None
+    # a session whose row 38 the per-kernel step wrote as well: the next one-launch steps agree bit for bit
     s2 = model.session(CTX)
-    s2.prefill(prompt[:-1])
+    s2.prefill(prompt[:-2])
+    s2.fused_step = False
+    s2.step(int(prompt[-2]))
+    s2.fused_step = True
     assert np.array_equal(s.step(int(prompt[-1])), s2.step(int(prompt[-1])))  # the one-launch step, as before
-    assert s.fused_step
+    assert s.fused_step and dev.last_kernel().startswith("k_decode_token<")
     for x in (s, sk, s2):
         x.free()
 
