@@ -84,7 +84,7 @@ def prefill_on_f32_path(dev, cfg, te, on, layers, ids) -> float:
     return dt
 
 
-def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=True):
+def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=True, n_ctx=None):
     from htr import synth
 
     t = time.time()
@@ -93,7 +93,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
     m = htr.TextModel(dev, htr.TextConfig(**cfg), te, on, layers)
     log("decoder weights uploaded")
     prompt = synth.prompt_ids(4242, prompt_len, cfg["n_vocab"])
-    s = m.session(prompt_len + n_new)
+    s = m.session(n_ctx or prompt_len + n_new)
     dev.sync()
     t0 = time.perf_counter()
     s.prefill(prompt[:-1])
@@ -140,7 +140,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
     # the same read on the per-kernel step (A/B in one run), and its kernel classes in graphs
     per_kernel, phases = None, None
     if fused and ab:
-        sk = m.session(prompt_len + n_new)
+        sk = m.session(n_ctx or prompt_len + n_new)
         sk.fused_step = False
         sk.prefill(prompt[:-1])
         chk = sk.choice(preset, prompt, chunk=16, depth=2)
@@ -158,9 +158,11 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
     # the one-launch step's average launch at the read's mean context: a graph of 16 launches at position 1279
     # (1280 keys), replayed, HIP events on the library's stream (htr_session_profile_step)
     kernel_us = fused_phases["step_in_graph_us"] if fused_phases else float("nan")
+    instance = dev.last_kernel()
     out = {
         "step_form": form,
         "kernel_us_at_mean_keys": kernel_us,
+        "kernel_instance": instance,
         "tok_s": tok_s,
         "bytes_per_token": bpt,
         "mean_keys": mean_keys,
@@ -717,6 +719,9 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--prompt", type=int, default=1024,
+                    help="the decode leg's prompt length (the workload: 1024; longer ones measure longer contexts)")
+    ap.add_argument("--ctx", type=int, default=0, help="the decode leg's session rows (default: prompt + 512)")
     ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, handover, vision")
     ap.add_argument("--choose-steps", type=int, default=10000,
                     help="single-launch steps of the choose leg (a counter run takes fewer: every launch is sampled)")
@@ -758,7 +763,8 @@ def main():
     decode_inputs, prefill_rows, choice_rows = None, None, None
     dev.phase("decode")
     if want("decode"):
-        d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup, ab=not args.no_ab)
+        d, decode_inputs, keep = bench_decode(dev, args.steps, args.warmup, prompt_len=args.prompt, ab=not args.no_ab,
+                                              n_ctx=args.ctx or None)
         result["value"] = d["tok_s"]
         result["ms_per_step"] = d["ms_per_read"]
         result["decode"] = d
@@ -768,12 +774,13 @@ def main():
             result["roofline"] = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                   "frac": ach / HBM_PEAK_GBS,
                                   "traffic": load_traffic("k_decode_token_traffic.json", "hbm_bytes_per_token"),
-                                  "kernel": "k_decode_token<3>: one decode token of the 28-layer q8_0 decoder in one "
-                                            "launch (embed, 28 layers, LM head, greedy choice)",
+                                  "kernel": f"{d['kernel_instance']}: one decode token of the 28-layer q8_0 decoder in "
+                                            "one launch (embed, 28 layers, LM head, greedy choice)",
                                   "algorithmic_bytes_per_launch": d["bytes_per_token"],
                                   "avg_launch_us": kus,
-                                  "launch_timing": "a graph of 16 launches at position 1279 (1280 keys, the read's "
-                                                   "mean), replayed 20 times, HIP events on the library's stream"}
+                                  "launch_timing": f"a graph of 16 launches at {int(d['mean_keys'] + 0.5)} keys (the "
+                                                   "read's mean), replayed 20 times, HIP events on the library's "
+                                                   "stream"}
         if not args.skip_cpu:
             m_, s_, _ = keep
             prefill_rows = [s_.kv_rows(li, 0, len(decode_inputs[4]) - 1) for li in range(decode_inputs[0]["n_layer"])]
