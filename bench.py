@@ -137,6 +137,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
     tok_s = steps * n_new / dt
     mid = prompt_len - 1 + n_new // 2
     fused_phases = fused_step_phases(s, mid, int(prompt[5]), cfg["n_layer"]) if fused else None
+    instance = dev.last_kernel()  # the one-launch step's instance (the A/B legs below launch other kernels)
     # the same read on the per-kernel step (A/B in one run), and its kernel classes in graphs
     per_kernel, phases = None, None
     if fused and ab:
@@ -158,7 +159,6 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len=1024, n_new=512, ab=Tr
     # the one-launch step's average launch at the read's mean context: a graph of 16 launches at position 1279
     # (1280 keys), replayed, HIP events on the library's stream (htr_session_profile_step)
     kernel_us = fused_phases["step_in_graph_us"] if fused_phases else float("nan")
-    instance = dev.last_kernel()
     out = {
         "step_form": form,
         "kernel_us_at_mean_keys": kernel_us,
