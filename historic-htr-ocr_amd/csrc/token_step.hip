@@ -199,6 +199,13 @@ __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uin
     __syncthreads();
 }
 
+// the layer table through the constant address space: the host writes it before the launch and nothing in the kernel
+// does, so its loads are scalar. As vector loads (the table is in device memory) a phase's first pointer load sat in
+// the wave's vector-memory order behind the previous phase's output stores, and its weights went out only once those
+// stores had been acknowledged
+typedef const __attribute__((address_space(4))) TokLayer const_layer;
+__device__ __forceinline__ const_layer &layer_at(const TokArgs &a, int l) { return ((const_layer *)a.layers)[l]; }
+
 // workgroup 0's wall-clock stamps, kept in LDS (a store to memory here would wait for the phase's own stores) and
 // written out at the end of the launch
 constexpr int MAX_LAYERS = 42;
@@ -400,7 +407,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
     const int j = tid & 15, kk = tid >> 4;
 
     for (int l = 0; l < a.n_layer; l++) {
-        const TokLayer &L = a.layers[l];
+        const_layer &L = layer_at(a, l);
         const uint32_t tbase = seq * 256u + (uint32_t)(XPL * l);
 
         int4 kr[NI];  // B's K rows (issued in A)
