@@ -130,14 +130,25 @@ __device__ __forceinline__ int4 pack8(const float (&f)[8]) {
     return make_int4((int)u[0], (int)u[1], (int)u[2], (int)u[3]);
 }
 
-// A wait's first loads go out this long after the workgroup's own outputs (s_sleep units of 64 clocks: ≈ 0.4 µs):
+// A wait's first loads go out this long after the workgroup's own outputs (s_sleep units of 64 clocks, ≈ 30 ns):
 // the producers' words take about that long to become visible, and a first poll that comes back with old words
 // costs a whole round trip more. Measured on one MI355X at the 28-layer read (µs a token): no pause 482 … 488,
 // 8 → 465, 12 → 461, 16 → 460 … 469, 24 → 466, 32 → 479; two polls in flight instead (more traffic) 523. With the
-// attention's hand-overs kept on their XCD (tokens/s): 8 → 2308, 12 → 2350 … 2375, 16 → 2380 … 2389.
-constexpr int POLL_SLEEP = 16;
-// Words from the workgroup's own XCD (B, C) are there sooner: 12 → 2350 tokens/s, 8 → 2371, 4 → 2378, 0 → 2378.
-constexpr int POLL_SLEEP_XCD = 4;
+// attention's hand-overs kept on their XCD (tokens/s): 8 → 2308, 12 → 2350 … 2375, 16 → 2380 … 2389. With the layer
+// table read by scalar loads, one pause for the four cross-XCD waits (tokens/s, twice each on one box): 12 → 2354,
+// 14 → 2439, 16 → 2531, 18 → 2571, 20 → 2577, 22 → 2573, 24 → 2562, 28 → 2552, 32 → 2520; the phases' own optima
+// differ (qkv's wait is shortest at 16 … 18, o's at 16 … 20, gate/up's at 24 … 28, down's at 20 … 24), and with one
+// a phase — qkv 18, o 18, gate/up 26, down 22, the attention's raw rows 10, the merge 4 — 2618 against 2577 for 20
+// everywhere (A/B on two boxes). The LM head's wait at 16 or 22: the same.
+constexpr int POLL_SLEEP = 16;      // the LM head's input and the choice's keys
+constexpr int POLL_SLEEP_QKV = 18;  // A: the residual of the layer before (1024 words)
+constexpr int POLL_SLEEP_O = 18;    // D: the attention output (2048 words)
+constexpr int POLL_SLEEP_GU = 26;   // E: the residual after o (1024 words)
+constexpr int POLL_SLEEP_DOWN = 22; // F: the SwiGLU output (3072 words)
+// Words from the workgroup's own XCD are there sooner: the attention's raw rows (B) 10, the chunks' partials (C) 4
+// (with the cross-XCD pause at 16: 12 → 2350 tokens/s, 8 → 2371, 4 → 2378, 0 → 2378 for both)
+constexpr int POLL_SLEEP_RAW = 10;
+constexpr int POLL_SLEEP_PART = 4;
 
 template <bool B> struct BoolC {
     static constexpr bool value = B;
@@ -168,11 +179,11 @@ struct Waiter {
 // The NP words idx = tid + 256·k (k < NP, idx < n) of src, each once it carries `tag`, → dst[idx] (LDS); then a
 // workgroup barrier. The first loads of every word go out together; a word that is not there yet is loaded again
 // until it is, or until the wall clock passes the limit.
-template <int NP>
+template <int NP, int SLEEP = POLL_SLEEP>
 __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uint32_t tag, float *dst) {
     const int tid = threadIdx.x;
     uint64_t v[NP];
-    __builtin_amdgcn_s_sleep(POLL_SLEEP);
+    __builtin_amdgcn_s_sleep(SLEEP);
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int idx = tid + TPB * k;
@@ -423,7 +434,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             for (int r = 0; r < 4; r++) row_issue<1>(rw[r], q, d, lr0 + 4 * wave + r, lane);
             float wv[1][16];
             glob_x<1>(wv, L.attn_norm, lane);
-            if (l > 0) take<4>(wt, xw + OFF_H2, DIM, tbase - 1, s_x);  // F of the layer before
+            if (l > 0) take<4, POLL_SLEEP_QKV>(wt, xw + OFF_H2, DIM, tbase - 1, s_x);  // F of the layer before
             // B's K rows now, behind A's own wait (before it, A's polls would queue behind them) and ahead of B's:
             // every chunk loads them, an idle one the row at pos (in bounds, not used). Against issuing them in B:
             // 2456 → 2466 tokens/s at the 1536-row cache, 2366 → 2388 at 2560 rows (twice on one box)
@@ -459,7 +470,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 const uint64_t *src0 = xw + OFF_QKV;
                 uint64_t vv[2];
                 int at[2];
-                __builtin_amdgcn_s_sleep(POLL_SLEEP_XCD);
+                __builtin_amdgcn_s_sleep(POLL_SLEEP_RAW);
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
                     const int idx = tid + TPB * k, part = idx >> 7, dd = idx & 127;
@@ -651,7 +662,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const bool has_o = cc < n_chunk;
             const int cm = tid >> 1;  // threads < 2·n_chunk: m (even) / l (odd) of chunk tid / 2
             const bool has_m = tid < 2 * n_chunk;
-            __builtin_amdgcn_s_sleep(POLL_SLEEP_XCD);
+            __builtin_amdgcn_s_sleep(POLL_SLEEP_PART);
             uint64_t vo = has_o ? ld_word(pk + (size_t)cc * PART_W + 2 + d0 + e) : (uint64_t)(tbase + 1) << 32;
             uint64_t vm = has_m ? ld_word(pk + (size_t)cm * PART_W + (tid & 1)) : (uint64_t)(tbase + 1) << 32;
             long long t0 = 0;
@@ -698,7 +709,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const int row = 4 * w + wave;
             RowW<2> rw;
             row_issue<2>(rw, L.q[3], L.d[3], row, lane);
-            take<8>(wt, xw + OFF_ATT, QD, tbase + 2, s_v);
+            take<8, POLL_SLEEP_O>(wt, xw + OFF_ATT, QD, tbase + 2, s_v);
             stamp(s_stamp, prof_on, 7 + 12 * l);
             float xv[2][16];
             lds_x<2>(xv, s_v, lane);
@@ -718,7 +729,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             }
             float wv[1][16];
             glob_x<1>(wv, L.ffn_norm, lane);
-            take<4>(wt, xw + OFF_H1, DIM, tbase + 3, s_x);
+            take<4, POLL_SLEEP_GU>(wt, xw + OFF_H1, DIM, tbase + 3, s_x);
             stamp(s_stamp, prof_on, 9 + 12 * l);
             float xv[1][16];
             lds_x<1>(xv, s_x, lane);
@@ -741,7 +752,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const int row = 4 * w + wave;
             RowW<3> rw;
             row_issue<3>(rw, L.q[6], L.d[6], row, lane);
-            take<12>(wt, xw + OFF_FF, NFF, tbase + 4, s_v);
+            take<12, POLL_SLEEP_DOWN>(wt, xw + OFF_FF, NFF, tbase + 4, s_v);
             stamp(s_stamp, prof_on, 11 + 12 * l);
             float xv[3][16];
             lds_x<3>(xv, s_v, lane);
