@@ -194,12 +194,13 @@ __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uin
         bool all = true;
 #pragma unroll
         for (int k = 0; k < NP; k++) all = all && (uint32_t)(v[k] >> 32) == tag;
-        if (all || wt.broken || wt.expired(t0)) break;
+        if (all || wt.broken) break;
 #pragma unroll
         for (int k = 0; k < NP; k++) {
             const int idx = tid + TPB * k;
             if ((uint32_t)(v[k] >> 32) != tag) v[k] = ld_word(src + idx);
         }
+        if (wt.expired(t0)) break;  // the clock is read while the loads travel
     }
     __syncthreads();  // the previous readers of dst are done
 #pragma unroll
@@ -480,10 +481,11 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 long long t0 = 0;
                 for (;;) {
                     const bool all = (uint32_t)(vv[0] >> 32) == tbase && (uint32_t)(vv[1] >> 32) == tbase;
-                    if (all || wt.broken || wt.expired(t0)) break;
+                    if (all || wt.broken) break;
 #pragma unroll
                     for (int k = 0; k < 2; k++)
                         if ((uint32_t)(vv[k] >> 32) != tbase) vv[k] = ld_word(src0 + at[k]);
+                    if (wt.expired(t0)) break;
                 }
                 // the V rows now: issued before the wait, the raw rows' loads would queue behind them (the K rows,
                 // needed first, are in by here): 2434 → 2455 tokens/s, the attention's wait 1.25 → 1.17 µs a layer
@@ -668,9 +670,10 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             long long t0 = 0;
             for (;;) {
                 const bool all = (uint32_t)(vo >> 32) == tbase + 1 && (uint32_t)(vm >> 32) == tbase + 1;
-                if (all || wt.broken || wt.expired(t0)) break;
+                if (all || wt.broken) break;
                 if ((uint32_t)(vo >> 32) != tbase + 1) vo = ld_word(pk + (size_t)cc * PART_W + 2 + d0 + e);
                 if ((uint32_t)(vm >> 32) != tbase + 1) vm = ld_word(pk + (size_t)cm * PART_W + (tid & 1));
+                if (wt.expired(t0)) break;
             }
             if (has_o) s_mo[cc][e] = __uint_as_float((uint32_t)vo);
             if (has_m) s_ml[tid & 1][cm] = __uint_as_float((uint32_t)vm);
