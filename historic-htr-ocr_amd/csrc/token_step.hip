@@ -178,7 +178,9 @@ struct Waiter {
 
 // The NP words idx = tid + 256·k (k < NP, idx < n) of src, each once it carries `tag`, → dst[idx] (LDS); then a
 // workgroup barrier. The first loads of every word go out together; a word that is not there yet is loaded again
-// until it is, or until the wall clock passes the limit.
+// until it is, or until the wall clock passes the limit. No barrier ahead of the stores into dst: every dst is read
+// last at least two barriers before (each exchange has its own LDS array, the residual one a copy for A and D and
+// one for E and F)
 template <int NP, int SLEEP = POLL_SLEEP>
 __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uint32_t tag, float *dst) {
     const int tid = threadIdx.x;
@@ -202,7 +204,6 @@ __device__ __forceinline__ void take(Waiter &wt, const uint64_t *src, int n, uin
         }
         if (wt.expired(t0)) break;  // the clock is read while the loads travel
     }
-    __syncthreads();  // the previous readers of dst are done
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int idx = tid + TPB * k;
@@ -372,8 +373,9 @@ __device__ __forceinline__ void head_post(const float *raw, const NormW &nw, con
 template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const TokArgs a) {
     constexpr int C = 16 * NI;
     constexpr int N = NI <= 1 ? 2 : NI <= 2 ? 4 : NI <= 4 ? 8 : NI <= 8 ? 16 : 32;  // 2·NI scores, padded
-    __shared__ __attribute__((aligned(16))) float s_x[DIM];   // the residual, as of its last exchange
-    __shared__ __attribute__((aligned(16))) float s_v[NFF];   // an exchanged input (attention output, SwiGLU)
+    // the exchanged inputs: the residual entering the layer (A, D) and after o (E, F), the attention output (D), the
+    // SwiGLU output (F)
+    __shared__ __attribute__((aligned(16))) float s_x[DIM], s_h[DIM], s_att[QD], s_ff[NFF];
     __shared__ __attribute__((aligned(16))) float s_raw[4][D];  // B: raw q (two heads), k, v rows of the KV head
     __shared__ __attribute__((aligned(16))) float s_post[3][D];  // B: q (× scale, two heads) and k, normed and roped
     __shared__ float s_ws[4][4];  // B: each wave's max and sum of p, per head
@@ -491,7 +493,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
                 // needed first, are in by here): 2434 → 2455 tokens/s, the attention's wait 1.25 → 1.17 µs a layer
 #pragma unroll
                 for (int i = 0; i < NI; i++) vr[i] = ld16_stream(vb + (size_t)min(k0 + kk + 16 * i, pos) * D + 8 * j);
-                __syncthreads();
+                // (s_raw was read last in the layer before's B: no barrier needed ahead of these stores)
 #pragma unroll
                 for (int k = 0; k < 2; k++) (&s_raw[0][0])[tid + TPB * k] = __uint_as_float((uint32_t)vv[k]);
                 __syncthreads();
@@ -712,10 +714,10 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const int row = 4 * w + wave;
             RowW<2> rw;
             row_issue<2>(rw, L.q[3], L.d[3], row, lane);
-            take<8, POLL_SLEEP_O>(wt, xw + OFF_ATT, QD, tbase + 2, s_v);
+            take<8, POLL_SLEEP_O>(wt, xw + OFF_ATT, QD, tbase + 2, s_att);
             stamp(s_stamp, prof_on, 7 + 12 * l);
             float xv[2][16];
-            lds_x<2>(xv, s_v, lane);
+            lds_x<2>(xv, s_att, lane);
             const float v = wave_sum(row_dot<2>(rw, xv), lane);
             if (lane == 0) put_word(xw + OFF_H1 + row, s_x[row] + v, tbase + 3);
         }
@@ -732,10 +734,10 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             }
             float wv[1][16];
             glob_x<1>(wv, L.ffn_norm, lane);
-            take<4, POLL_SLEEP_GU>(wt, xw + OFF_H1, DIM, tbase + 3, s_x);
+            take<4, POLL_SLEEP_GU>(wt, xw + OFF_H1, DIM, tbase + 3, s_h);
             stamp(s_stamp, prof_on, 9 + 12 * l);
             float xv[1][16];
-            lds_x<1>(xv, s_x, lane);
+            lds_x<1>(xv, s_h, lane);
             norm16<1>(xv, wv, a.eps, DIM, lane);
             float ag[4], au[4];
 #pragma unroll
@@ -755,12 +757,12 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             const int row = 4 * w + wave;
             RowW<3> rw;
             row_issue<3>(rw, L.q[6], L.d[6], row, lane);
-            take<12, POLL_SLEEP_DOWN>(wt, xw + OFF_FF, NFF, tbase + 4, s_v);
+            take<12, POLL_SLEEP_DOWN>(wt, xw + OFF_FF, NFF, tbase + 4, s_ff);
             stamp(s_stamp, prof_on, 11 + 12 * l);
             float xv[3][16];
-            lds_x<3>(xv, s_v, lane);
+            lds_x<3>(xv, s_ff, lane);
             const float v = wave_sum(row_dot<3>(rw, xv), lane);
-            const float xn = s_x[row] + v;
+            const float xn = s_h[row] + v;
             if (lane == 0) {
                 put_word(xw + OFF_H2 + row, xn, tbase + 5);  // the next layer's, or the LM head's, input
                 if (l + 1 == a.n_layer) a.x_out[row] = xn;  // the residual (an out-of-range id's embedding)
@@ -797,7 +799,7 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
         const uint32_t w_id = tid < n_win ? a.hist[len - n_win + tid] : 0xffffffffu;
         for (int u = tid; u < MAX_HEAD_ROWS / 16; u += TPB) reinterpret_cast<uint4 *>(s_pen)[u] = make_uint4(0, 0, 0, 0);
         if (tid == 0) s_nan0 = 0;
-        take<4>(wt, xlast + OFF_H2, DIM, ttag, s_x);  // its barriers also order the clearing before the marks
+        take<4>(wt, xlast + OFF_H2, DIM, ttag, s_x);  // its barrier also orders the clearing before the marks
         stamp(s_stamp, prof_on, 1 + 12 * a.n_layer);
         if (w_id >= (uint32_t)r0 && w_id < (uint32_t)r1) s_pen[w_id - r0] = 1;
         for (int j = tid + TPB; j < n_win; j += TPB) {
@@ -858,13 +860,14 @@ template <int NI> __global__ __launch_bounds__(TPB) void k_decode_token(const To
             // workgroup 0 takes the 256 keys, keeps the largest (the first maximum of the whole vocabulary), writes
             // the token, appends it to the history and advances position and length
             if (w == 0) {
-                take<2>(wt, xw + OFF_BEST, 2 * NWG, ctag, s_v);
+                take<2>(wt, xw + OFF_BEST, 2 * NWG, ctag, s_att);
                 if (wave == 0) {
                     uint64_t k = 0;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const int g = lane + 64 * q;
-                        const uint64_t kq = ((uint64_t)__float_as_uint(s_v[2 * g]) << 32) | __float_as_uint(s_v[2 * g + 1]);
+                        const uint64_t kq =
+                            ((uint64_t)__float_as_uint(s_att[2 * g]) << 32) | __float_as_uint(s_att[2 * g + 1]);
                         k = kq > k ? kq : k;
                     }
 #pragma unroll
