@@ -32,8 +32,11 @@
 //            a one-way hand-over of about 0.2 µs against 0.6 µs through the fabric (one word back and forth between
 //            two workgroups, htr_debug_handover in handover.hip; the step: 2194 → 2378 tokens/s). A word never seen (a workgroup on another XCD) is
 //            a wait that runs out, never a stale value: the tag proves the word current;
-//   overlap  a phase issues its weight loads first, then waits for its input: the HBM latency of the weights runs
-//            under the hand-over's. B's K rows go out in A right after A's wait, its V rows right after B's;
+//   overlap  a phase issues its loads first (a norm's weights, cache hits, ahead of the rows), then, after a pause
+//            tuned for each hand-over, polls for its input: the HBM latency of the weights runs under the
+//            hand-over's. B's K rows go out in A right after A's wait, its V rows right after B's. A wave's loads
+//            complete in order, so nothing else is loaded ahead of the polls: the layer table, read once a phase
+//            for its pointers, is read by scalar loads;
 //   reuse    one word area per exchange, rewritten every layer. A workgroup writes exchange e of layer l + 1 only after
 //            it has read inputs that every workgroup produced after reading exchange e of layer l (checked per
 //            exchange in the comment of k_decode_token), so no word is overwritten before all its readers are done;
