@@ -539,6 +539,29 @@ def bench_copy(dev, mib=512, reps=5):
     return res
 
 
+def bench_read(dev, nbytes=429916160, reps=20):
+    """a read of known size and nothing else (htr_debug_read): the read rate a streaming kernel can reach on this
+    device, over the batched matvec's own byte count (128 W copies, past the 256 MB Infinity Cache); 16 / 32 / 64 KB a
+    workgroup, plain and non-temporal 16-byte loads"""
+    buf, sink = dev.alloc(nbytes), dev.alloc(4)
+    res = {"bytes": nbytes}
+    for nt in (True, False):
+        for kb in (16, 32, 64):
+            buf.read_through(sink, nt, kb)
+            dev.timer_begin()
+            for _ in range(reps):
+                buf.read_through(sink, nt, kb)
+            us = dev.timer_end() / reps * 1e3
+            res[f"{'nontemporal' if nt else 'plain'}_{kb}KB_a_workgroup_GBs"] = nbytes / (us * 1e-6) / 1e9
+    buf.free()
+    sink.free()
+    res["best_GBs"] = max(v for k, v in res.items() if k.endswith("_GBs"))
+    res["best_frac_of_peak"] = res["best_GBs"] / HBM_PEAK_GBS
+    log("read " + ", ".join(f"{k[:-4]} {v:.0f}" for k, v in res.items() if k.endswith("workgroup_GBs"))
+        + f" GB/s; best {res['best_GBs']:.0f} GB/s ({res['best_frac_of_peak']:.3f} of 8 TB/s)")
+    return res
+
+
 def bench_handover(dev):
     """the hand-over the one-launch decode step rests on (htr_debug_handover, 256 workgroups of one launch): one tagged
     word back and forth between two workgroups on one XCD (0 and 8) and on two (0 and 1), stored at workgroup scope
@@ -696,6 +719,8 @@ def roofline_by_config(r: dict) -> dict:
                                          "traffic": load_traffic(),
                                          "unit": "128 matvecs in one launch over 128 distinct W copies (430 MB, past "
                                                  "the 256 MB Infinity Cache): the kernel's streaming rate"}
+        if "read" in r:
+            out["config0_matvec_batched"]["frac_of_read_ceiling"] = m["batched_launch_GBs"] / r["read"]["best_GBs"]
     if "choose" in r:
         c = r["choose"]
         out["config1_choice_graph_node"] = {"bound": "hbm", "achieved_GBs": c["graph_node_GBs"],
@@ -722,7 +747,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=1024,
                     help="the decode leg's prompt length (the workload: 1024; longer ones measure longer contexts)")
     ap.add_argument("--ctx", type=int, default=0, help="the decode leg's session rows (default: prompt + 512)")
-    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy, handover, vision")
+    ap.add_argument("--only", default="", help="comma list of: decode, matvec, choose, attention, copy (and the read leg), handover, vision")
     ap.add_argument("--choose-steps", type=int, default=10000,
                     help="single-launch steps of the choose leg (a counter run takes fewer: every launch is sampled)")
     ap.add_argument("--no-graphs", action="store_true",
@@ -799,6 +824,7 @@ def main():
     dev.phase("copy")
     if want("copy"):
         result["copy"] = bench_copy(dev)
+        result["read"] = bench_read(dev)
     dev.phase("handover")
     if want("handover"):
         result["handover"] = bench_handover(dev)

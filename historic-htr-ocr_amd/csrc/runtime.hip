@@ -412,6 +412,52 @@ extern "C" int htr_copy(htr_device *dev, void *d_dst, const void *d_src, size_t 
     return htr_launched(dev, "k_copy16");
 }
 
+// ---- a read of known size: the read rate a streaming kernel can reach on this device --------------------------------
+
+// every workgroup reads PER consecutive 4 KB blocks (256 threads × 16 bytes), all its loads issued before the first
+// use, and folds them into one word that is stored only if it equals a value no fold of a zero buffer gives (the
+// loads stay; the store is one word at sink, whatever the buffer holds)
+template <bool NT, int PER> __global__ __launch_bounds__(256) void k_read16(const int4 *src, size_t n16, uint32_t *sink) {
+    const auto *s = (const __attribute__((address_space(1))) gint4 *)(uintptr_t)src;
+    const size_t base = (size_t)blockIdx.x * PER * 256 + threadIdx.x;
+    gint4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const size_t at = base + (size_t)i * 256;
+        v[i] = at < n16 ? (NT ? __builtin_nontemporal_load(s + at) : s[at]) : gint4{0, 0, 0, 0};
+    }
+    int f = 0;
+#pragma unroll
+    for (int i = 0; i < PER; i++) f ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (f == 0x7fffffff) sink[0] = (uint32_t)f;
+}
+
+extern "C" int htr_debug_read(htr_device *dev, const void *d_src, size_t bytes, int nontemporal, int kb_per_workgroup,
+                              uint32_t *d_sink) {
+    HTR_TRY(htr_check_alive(dev));
+    if (!d_src || !d_sink) return htr_fail("htr_debug_read: null pointer");
+    if (((uintptr_t)d_src & 15) || bytes % 16 || !bytes)
+        return htr_fail("htr_debug_read: %zu bytes at %p (a positive multiple of 16, 16-byte aligned)", bytes, d_src);
+    const int per = kb_per_workgroup / 4;
+    if (per != 4 && per != 8 && per != 16) return htr_fail("htr_debug_read: %d KB a workgroup (16, 32 or 64)", kb_per_workgroup);
+    const size_t n16 = bytes / 16, grid = (n16 + (size_t)per * 256 - 1) / ((size_t)per * 256);
+    if (grid > (size_t)INT32_MAX) return htr_fail("htr_debug_read: %zu bytes", bytes);
+    const auto *p = (const int4 *)d_src;
+#define HTR_READ(NT, PER)                                                                                              \
+    hipLaunchKernelGGL((k_read16<NT, PER>), dim3((unsigned)grid), dim3(256), 0, dev->stream, p, n16, d_sink)
+    if (nontemporal) {
+        if (per == 4) HTR_READ(true, 4);
+        else if (per == 8) HTR_READ(true, 8);
+        else HTR_READ(true, 16);
+    } else {
+        if (per == 4) HTR_READ(false, 4);
+        else if (per == 8) HTR_READ(false, 8);
+        else HTR_READ(false, 16);
+    }
+#undef HTR_READ
+    return htr_launched(dev, "k_read16");
+}
+
 // ---- weights --------------------------------------------------------------------------------------------------------
 
 static inline uint16_t f16_bits_rne(float v);  // below

@@ -25,7 +25,7 @@ COMPUTE_F32, COMPUTE_F16 = 0, 1
 SYMBOLS = [
     "htr_last_error", "htr_device_open", "htr_device_close", "htr_alive", "htr_set_fatal_hook", "htr_debug_mark_lost",
     "htr_sync", "htr_device_set_compute", "htr_device_compute", "htr_device_info", "htr_timer_begin", "htr_timer_end", "htr_mem_live", "htr_alloc", "htr_free",
-    "htr_upload", "htr_download", "htr_copy", "htr_phase",
+    "htr_upload", "htr_download", "htr_copy", "htr_debug_read", "htr_phase",
     "htr_weight_q8_0", "htr_weight_q8_0_f16", "htr_weight_free", "htr_weight_shape", "htr_matvec_q8_0",
     "htr_matvec_q8_0_many", "htr_matvec_qkv", "htr_matvec_ffn", "htr_qkv_post", "htr_decode_attention", "htr_causal_attention", "htr_choose",
     "htr_choose_many", "htr_matmul_q8_0", "htr_gemm_f16", "htr_gemm_ffn_f16", "htr_vision_create", "htr_vision_free",
@@ -126,6 +126,7 @@ def lib() -> C.CDLL:
             "htr_upload": (i32, [vp, vp, vp, sz]),
             "htr_download": (i32, [vp, vp, vp, sz]),
             "htr_copy": (i32, [vp, vp, vp, sz]),
+            "htr_debug_read": (i32, [vp, vp, sz, i32, i32, vp]),
             "htr_phase": (i32, [vp, C.c_char_p]),
             "htr_weight_q8_0": (i32, [vp, vp, sz, sz, pp]),
             "htr_weight_q8_0_f16": (i32, [vp, vp, sz, sz, f32, pp]),
@@ -263,6 +264,13 @@ class Buffer:
         """device → device copy (gpu.rs Batch::copy)"""
         n = min(self.nbytes, src.nbytes) if nbytes is None else nbytes
         _check(lib().htr_copy(self.dev.h, self.ptr, src.ptr, n))
+        return self
+
+    def read_through(self, sink: "Buffer", nontemporal: bool = True, kb_per_workgroup: int = 16) -> "Buffer":
+        """the whole buffer read on the device and nothing else (htr_debug_read: the read rate of a streaming kernel;
+        at most one u32 of `sink` is written)"""
+        _check(lib().htr_debug_read(self.dev.h, self.ptr, self.nbytes - self.nbytes % 16, 1 if nontemporal else 0,
+                                    kb_per_workgroup, sink.ptr))
         return self
 
     def free(self) -> None:

@@ -114,6 +114,13 @@ int htr_download(htr_device *dev, void *h_dst, const void *d_src, size_t bytes);
 /* d_dst[0 … bytes) = d_src[0 … bytes) on the device's stream, both 16-byte aligned, not overlapping (gpu.rs:2102-2110
  * Batch::copy). Also the plain copy of known size that calibrates the HBM byte counters. */
 int htr_copy(htr_device *dev, void *d_dst, const void *d_src, size_t bytes);
+/* a read of d_src[0 … bytes) on the device's stream and nothing else (no reference counterpart: a measurement of this
+ * device): every workgroup reads kb_per_workgroup KB (16, 32 or 64) through 16-byte loads, non-temporal when
+ * `nontemporal`, all issued before the first use, and folds them into a word stored at d_sink only when it equals a
+ * fixed value (so at most one u32 there is written). Timed with htr_timer_*, the read rate a streaming kernel such as
+ * the q8_0 matvec can reach here. bytes a positive multiple of 16, d_src 16-byte aligned. */
+int htr_debug_read(htr_device *dev, const void *d_src, size_t bytes, int nontemporal, int kb_per_workgroup,
+                   uint32_t *d_sink);
 /* the phase of the following work (gpu.rs:1349-1358 Gpu::phase: "vision", "prefill", "decode", "-" = none): a roctx
  * range on the calling thread that rocprofv3 --marker-trace records; the device's previous phase range ends */
 int htr_phase(htr_device *dev, const char *name);

@@ -19,13 +19,15 @@ in the one-launch step's tail, so the same cases are driven through it here, wit
     overlapping row negative), penalty reversal, rows whose logit is always NaN (an infinite scale on zero quants) or
     −inf (an f32 overflow), the frequency penalty, rp below 1;
   - NaN at index 0: the reference's choose returns 0 (its first maximum starts there), so does the tail.
+
+The same zero-layer construction pins the embedding gather on its own: the LM head's input is then the gathered row.
 """
 import numpy as np
 import pytest
 
 import htr
 import oracle as orc
-from helpers import synth_text_model, to_htr_cfg
+from helpers import rel_l2, synth_text_model, to_htr_cfg
 
 pytestmark = pytest.mark.gpu
 
@@ -233,3 +235,62 @@ def test_fused_choice_nan_at_index_0(dev):
     finally:
         m.free()
     assert toks == [0] * 20
+
+
+# ---- the embedding gather (embed_q8_0.wgsl:19-38, text.rs:547), through a model whose layers add nothing ------------
+
+
+def test_embedding_gather_reaches_the_lm_head_as_the_tokens_row(dev):
+    """every layer weight zero, so the residual at the LM head is the gathered row itself: logits = E·(rmsnorm(E[t])
+    ⊙ output_norm) with E the dequantised token_embd. The rows' 32 blocks carry scales of their own (a gather that
+    dropped or misplaced a block's scale changes the normed direction; a whole-row scale would cancel in the norm), and
+    the tokens sit at the workgroup-share edges (0, 15 / 16, 2047 / 2048, n_vocab − 1). Checked on the one-launch step,
+    the per-kernel step (k_embed) and the prefill's last row, against fp64"""
+    g = np.random.default_rng(4242)
+    q = g.integers(-127, 128, (N_VOCAB, DIM)).astype(np.int8)
+    d = (np.abs(g.normal(0.0, 1.0, (N_VOCAB, DIM // 32))) * 0.002 + 1e-4).astype(np.float16)
+    blocks = np.zeros((N_VOCAB, DIM // 32, 34), np.uint8)
+    blocks[:, :, :2] = d.reshape(N_VOCAB, DIM // 32, 1).view(np.uint8)
+    blocks[:, :, 2:] = q.reshape(N_VOCAB, DIM // 32, 32).view(np.uint8)
+    on = (1.0 + g.normal(0.0, 0.02, DIM)).astype(np.float32)
+    zero = lambda rows, cols: np.zeros(rows * cols // 32 * 34, np.uint8)  # noqa: E731
+    ones = lambda n: np.ones(n, np.float32)  # noqa: E731
+    layers = [{"attn_norm": ones(DIM), "q": zero(2048, DIM), "k": zero(1024, DIM), "v": zero(1024, DIM),
+               "o": zero(DIM, 2048), "q_norm": ones(128), "k_norm": ones(128), "ffn_norm": ones(DIM),
+               "gate": zero(3072, DIM), "up": zero(3072, DIM), "down": zero(DIM, 3072)} for _ in range(N_LAYER)]
+    cfg = dict(n_layer=N_LAYER, dim=DIM, n_head=16, n_kv=8, d_head=128, n_ff=3072, n_vocab=N_VOCAB,
+               n_ctx_train=40960, eps=1e-6, rope_base=1e6)
+    e64 = q.astype(np.float64) * np.repeat(d.astype(np.float64), 32, axis=1)
+
+    def want(t: int) -> np.ndarray:
+        x = e64[t]
+        return e64 @ (x / np.sqrt(np.mean(x * x) + 1e-6) * on.astype(np.float64))
+
+    toks = [0, 15, 16, 2047, 2048, N_VOCAB - 1, 777, 3001]
+    m = make_model(dev, cfg, blocks.reshape(-1), on, layers)
+    try:
+        worst = {}
+        for fused in (True, False):
+            s = m.session(CTX)
+            s.fused_step = fused
+            assert s.fused_step == fused
+            s.prefill(np.array([5, 6], np.int32))
+            for t in toks:
+                got = s.step(t)
+                if fused:
+                    assert dev.last_kernel().startswith("k_decode_token<")
+                err = rel_l2(got, want(t))
+                worst[fused] = max(worst.get(fused, 0.0), err)
+                assert err <= 1e-5, f"{'one-launch' if fused else 'per-kernel'} step, token {t}: rel-L2 {err:.2e}"
+            s.free()
+        s = m.session(CTX)
+        for t in (0, N_VOCAB - 1, 2048):
+            s.rewind(0)
+            err = rel_l2(s.prefill(np.array([9, 10, t], np.int32)), want(t))
+            worst["prefill"] = max(worst.get("prefill", 0.0), err)
+            assert err <= 1e-3, f"prefill, last token {t}: rel-L2 {err:.2e}"
+        s.free()
+    finally:
+        m.free()
+    print(f"\n[embedding gather] rel-L2 vs fp64: one-launch {worst[True]:.1e}, per-kernel {worst[False]:.1e}, "
+          f"prefill {worst['prefill']:.1e}", flush=True)
