@@ -25,6 +25,11 @@ Also measured in the same run (one JSON line):
                 restored between passes (each step sees its seeded logits); all rows batched; every pass's 512 tokens
                 the same
   attention     GQA decode attention (16 q / 8 kv heads × 128) at 512 / 2048 / 8192 keys over ≥ 512 MiB of rotating caches
+  copy, read    a 512 MiB device copy (the byte counters' reference point) and a read of the matvec's 430 MB and
+                nothing else (the read rate a streaming kernel can reach: htr_debug_read)
+  handover      the one-launch step's hand-over on its own (htr_debug_handover)
+  vision_gemm, vision_encode
+                a vision layer's GEMMs at 12100 rows against the dense f16 MFMA peak; a 1540 × 1540 page end to end
   cpu_baseline  the oracle (oracle/, a C restatement of the reference path, OpenMP) decoding the read's own keys 1024 …
                 1535 on the host cores from the GPU's prefill rows, and the choice on the choose leg's 512 rows, whose
                 tokens it checks
@@ -687,8 +692,8 @@ def cpu_baseline(model_inputs, prefill_rows, choice_rows=None, budget_s=25.0, n_
 
 
 def no_nan(v):
-    """NaN (a leg skipped with --no-graphs) → null, so that the line is strict JSON"""
-    if isinstance(v, float) and v != v:
+    """NaN (a leg skipped with --no-graphs) and ±inf → null, so that the line is strict JSON"""
+    if isinstance(v, float) and (v != v or v in (float("inf"), float("-inf"))):
         return None
     if isinstance(v, dict):
         return {k: no_nan(x) for k, x in v.items()}
