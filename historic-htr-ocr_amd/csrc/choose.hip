@@ -19,7 +19,8 @@
 // reset themselves.
 //
 // Cross-workgroup traffic is device-scope atomics only: on this multi-XCD GPU a release fence in every workgroup
-// would write back the L2 each time, which costs more than the whole scan.
+// would write back the L2 each time, which costs more than the whole scan. Many rows in one launch (no frequency
+// penalty) take k_choose_rows instead: a workgroup a row, so nothing crosses between workgroups at all.
 #include <cmath>
 
 #include "choose_key.h"
@@ -165,6 +166,99 @@ template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArg
     __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Many rows (no frequency penalty): one workgroup a row, nothing handed between workgroups. The window's ids set one bit
+// each in an LDS bitmap of the row (a repeated id sets the same bit: each distinct id is penalised once); the row
+// streams through in 16-byte loads, RU of them in flight a thread, each group of 4 logits tested against its 4 bits
+// (one LDS word holds the bits of 32 logits), penalised and written back where marked, and folded into the thread's
+// best by `better`; the workgroup's best is the token. The NaN-at-index-0 rule as in k_choose. Rows of another
+// alignment or a vocabulary not a multiple of 4 take one logit a step.
+constexpr int RW_T = 512, RU = 8;
+typedef float gfloat4 __attribute__((ext_vector_type(4)));
+
+template <bool VEC> __global__ __launch_bounds__(RW_T) void k_choose_rows(const ChooseArgs a) {
+    extern __shared__ uint32_t s_bits[];  // ⌈n_vocab / 32⌉ words
+    __shared__ float s_v[RW_T / 64];
+    __shared__ uint32_t s_i[RW_T / 64];
+    __shared__ int s_nan0;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nv = a.n_vocab, words = (nv + 31) >> 5;
+    float *logits = a.logits + (size_t)row * nv;
+    uint32_t *hist = a.hist + (size_t)row * a.hist_stride;
+    const int len = a.len;
+    const int start = len - min(len, a.window);
+    const int n_win = a.rp != 1.0f ? len - start : 0;
+    if (n_win > 0) {
+        for (int w = tid; w < words; w += RW_T) s_bits[w] = 0u;
+        __syncthreads();
+        for (int j = tid; j < n_win; j += RW_T) {
+            const uint32_t t = hist[start + j];
+            if (t < (uint32_t)nv) atomicOr(&s_bits[t >> 5], 1u << (t & 31));
+        }
+        __syncthreads();
+    }
+    float bv = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    bool nan0 = false;
+    auto take = [&](float x, uint32_t k, bool pen) {
+        if (pen) {
+            x = x < 0.0f ? x * a.rp : x / a.rp;
+            logits[k] = x;
+        }
+        if (k == 0) nan0 = x != x;  // the NaN-at-index-0 rule reads the penalised value
+        if (better(x, k, bv, bi)) {
+            bv = x;
+            bi = k;
+        }
+    };
+    if constexpr (VEC) {
+        const auto *l4 = (const __attribute__((address_space(1))) gfloat4 *)(uintptr_t)logits;
+        const int n4 = nv >> 2;
+        for (int u0 = tid; u0 < n4; u0 += RU * RW_T) {
+            gfloat4 v[RU];
+#pragma unroll
+            for (int k = 0; k < RU; k++) {
+                const int u = u0 + k * RW_T;
+                v[k] = u < n4 ? __builtin_nontemporal_load(l4 + u) : gfloat4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int k = 0; k < RU; k++) {
+                const int u = u0 + k * RW_T;
+                if (u < n4) {
+                    const uint32_t b = n_win > 0 ? (s_bits[u >> 3] >> (4 * (u & 7))) & 15u : 0u;
+                    const uint32_t k0 = 4u * (uint32_t)u;
+                    take(v[k].x, k0, b & 1u);
+                    take(v[k].y, k0 + 1, b & 2u);
+                    take(v[k].z, k0 + 2, b & 4u);
+                    take(v[k].w, k0 + 3, b & 8u);
+                }
+            }
+        }
+    } else {
+        for (int k = tid; k < nv; k += RW_T)
+            take(logits[k], (uint32_t)k, n_win > 0 && ((s_bits[k >> 5] >> (k & 31)) & 1u));
+    }
+    wave_best(bv, bi, lane);
+    if (tid == 0) s_nan0 = nan0;  // thread 0 holds index 0
+    if (lane == 0) {
+        s_v[wave] = bv;
+        s_i[wave] = bi;
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    float v = s_v[0];
+    uint32_t i = s_i[0];
+#pragma unroll
+    for (int w = 1; w < RW_T / 64; w++)
+        if (better(s_v[w], s_i[w], v, i)) {
+            v = s_v[w];
+            i = s_i[w];
+        }
+    // a NaN at index 0 → token 0; every logit NaN (no best) → 0
+    const uint32_t tk = s_nan0 || i >= (uint32_t)nv ? 0u : i;
+    a.tok[row] = tk;
+    hist[len] = tk;
+}
+
 }  // namespace
 
 int choose_groups(int n_vocab, int span) { return (n_vocab + span - 1) / span; }
@@ -175,9 +269,22 @@ size_t choose_ticket_bytes(int rows) { return (size_t)rows * LINE * 4; }
 int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a) {
     if (a.n_vocab <= 0 || a.rows <= 0) return htr_fail("choose: %d logits, %d rows", a.n_vocab, a.rows);
     // one row: 2048 logits a workgroup (75 over 151,936), a step 10.8 µs launched alone against 11.6 µs with 4096 and
-    // 12.8 µs with 8192; many rows: 4096 (5.2 TB/s over 512 rows against 4.0 with 2048)
-    if (a.rows == 1) hipLaunchKernelGGL(k_choose<2048>, dim3(choose_groups(a.n_vocab, 2048), 1), dim3(CW), 0, st, a);
-    else hipLaunchKernelGGL(k_choose<4096>, dim3(choose_groups(a.n_vocab, 4096), a.rows), dim3(CW), 0, st, a);
+    // 12.8 µs with 8192
+    if (a.rows == 1) {
+        hipLaunchKernelGGL(k_choose<2048>, dim3(choose_groups(a.n_vocab, 2048), 1), dim3(CW), 0, st, a);
+        return htr_launched(dev, "k_choose");
+    }
+    // many rows without the frequency penalty or the device-resident counters: a workgroup a row, the window's bitmap
+    // in LDS (up to 64 KB)
+    const size_t bitmap = (size_t)(a.n_vocab + 31) / 32 * 4;
+    if (a.fp == 0.0f && !a.len_dev && !a.advance && bitmap <= 65536) {
+        const bool vec = a.n_vocab % 4 == 0 && ((uintptr_t)a.logits & 15) == 0;
+        if (vec) hipLaunchKernelGGL(k_choose_rows<true>, dim3(a.rows), dim3(RW_T), bitmap, st, a);
+        else hipLaunchKernelGGL(k_choose_rows<false>, dim3(a.rows), dim3(RW_T), bitmap, st, a);
+        return htr_launched(dev, "k_choose_rows");
+    }
+    // otherwise 4096 logits a workgroup of each row (4.3 TB/s over the bench's 512 rows; k_choose_rows 5.2–5.5)
+    hipLaunchKernelGGL(k_choose<4096>, dim3(choose_groups(a.n_vocab, 4096), a.rows), dim3(CW), 0, st, a);
     return htr_launched(dev, "k_choose");
 }
 

@@ -184,3 +184,74 @@ def test_config1_bench_rows_bit_exact(dev):
           f"choice; {len(set(want))} distinct tokens", flush=True)
     for b in (lb, hb, tok):
         b.free()
+
+
+def many(dev, rows, rp, window, hists, n_vocab):
+    """choose_many over rows [n][n_vocab] with per-row windows (hists [n][window], left-padded with n_vocab, an id
+    outside the vocabulary that neither kernel penalises) at len = window → tokens, penalised rows"""
+    n = len(rows)
+    hb = dev.upload(np.concatenate([np.asarray(hists, np.uint32), np.zeros((n, 1), np.uint32)], axis=1))
+    lb = dev.upload(np.ascontiguousarray(rows, np.float32))
+    tok = dev.alloc(n * 4)
+    htr.choose_many(dev, lb, n_vocab, n, hb, window + 1, window, window, rp, tok)
+    assert dev.last_kernel() == "k_choose_rows"
+    got = [int(t) for t in tok.download(np.uint32, n)]
+    pen = lb.download(np.float32).reshape(n, n_vocab)
+    h = hb.download(np.uint32).reshape(n, window + 1)
+    assert h[:, window].tolist() == got  # the token appended to each row's history
+    for b in (hb, lb, tok):
+        b.free()
+    return got, pen
+
+
+def padded(history, window, n_vocab):
+    w = list(history[-window:]) if history else []
+    return [n_vocab] * (window - len(w)) + w
+
+
+def test_many_rows_on_the_reference_matrix(dev):
+    """text.rs:1001-1054's cases without the frequency penalty (which the batched form does not take), every step of
+    a case a row of one launch (a workgroup a row, k_choose_rows): the tokens and the penalised rows bit for bit"""
+    for case in GOLD["gpu_choice_matrix"]["cases"]:
+        n_vocab, rp, window, fp, _ = case
+        if fp != 0:
+            continue
+        steps = list(gpu_choice_matrix_inputs(case))
+        got, pen = many(dev, [l for l, _, _, _ in steps], rp, window,
+                        [padded(h, window, n_vocab) for _, h, _, _ in steps], n_vocab)
+        for i, (l, history, _, want) in enumerate(steps):
+            ref = l.copy()
+            assert orc.choose(ref, rp, window, 0.0, history) == want
+            assert got[i] == want, f"vocab {n_vocab} rp {rp} window {window} step {i}"
+            assert np.array_equal(pen[i].view(np.uint32), ref.view(np.uint32)), (n_vocab, rp, window, i)
+
+
+@pytest.mark.parametrize("n_vocab", [1000, 1001])
+def test_many_rows_edge_rules(dev, n_vocab):
+    """the batched form's 16-byte path (1000 logits a row) and its logit-a-step path (1001): NaN at index 0 → 0, NaN
+    elsewhere never wins, every logit −inf → 0, every logit NaN → 0, exact ties and ±0 maxima → the lowest index, a
+    window id on the maximum (rp 1.3: the penalty reverses the choice, and rp 0.7 raises a negative one), a window
+    repeating one id (penalised once) — each row against the oracle's choose, penalised rows bit for bit"""
+    g = np.random.default_rng(n_vocab)
+    rows, hists = [], []
+    window = 5
+    base = lambda: g.normal(0, 3, n_vocab).astype(np.float32)  # noqa: E731
+    r = base(); r[0] = np.nan; rows.append(r)
+    r = base(); r[7] = np.nan; r[9] = 40.0; rows.append(r)
+    rows.append(np.full(n_vocab, -np.inf, np.float32))
+    rows.append(np.full(n_vocab, np.nan, np.float32))
+    r = base(); r[[3, 600, n_vocab - 1]] = 50.0; rows.append(r)
+    r = -np.abs(base()) - 1.0; r[5] = -0.0; r[900] = 0.0; rows.append(r)
+    r = base(); r[11] = 30.0; r[12] = 29.0; rows.append(r)
+    r = -np.abs(base()) - 10.0; r[13] = -2.0; r[14] = -1.9; rows.append(r)
+    wins = [[1, 2, 3, 4, 5], [7, 7, 7, 7, 7], [0, 1, 2, 3, 4], [0, 0, 1, 1, 2], [600, 600, 2, 2, 3],
+            [5, 900, 900, 5, 8], [11, 11, 11, 11, 11], [13, 13, 13, 13, 13]]
+    for rp in (1.3, 0.7):
+        got, pen = many(dev, rows, rp, window, wins, n_vocab)
+        for i, (row, w) in enumerate(zip(rows, wins)):
+            ref = row.copy()
+            want = orc.choose(ref, rp, window, 0.0, w)
+            assert got[i] == want, f"rp {rp} row {i}: {got[i]} against {want}"
+            a, b = pen[i], ref
+            assert np.array_equal(np.isnan(a), np.isnan(b))
+            assert np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)), (rp, i)
