@@ -392,6 +392,7 @@ def bench_choose(dev, n_steps=10000, n_buf=512, n_vocab=151936, window=64):
     # the 512 rows in one launch (independent rows, each with its own window), restored between launches
     toks = dev.alloc(n_buf * 4)
     htr.choose_many(dev, logits, n_vocab, n_buf, hist, window + 1, window, window, 1.1, toks)
+    batched_kernel = dev.last_kernel()
     batched_same = np.array_equal(toks.download(np.uint32, n_rows), passes[0])
     restore()
     ms = 0.0
@@ -402,6 +403,7 @@ def bench_choose(dev, n_steps=10000, n_buf=512, n_vocab=151936, window=64):
         restore()
     ms /= 5
     res["batched_rows_per_launch"] = n_buf
+    res["batched_kernel"] = batched_kernel
     res["batched_tokens_equal_single_steps"] = batched_same
     res["batched_us_per_row"] = ms / n_buf * 1e3
     res["batched_GBs"] = n_buf * CHOOSE_STEP_BYTES / (ms * 1e-3) / 1e9
@@ -731,7 +733,7 @@ def roofline_by_config(r: dict) -> dict:
         out["config1_choice_graph_node"] = {"bound": "hbm", "achieved_GBs": c["graph_node_GBs"],
                                             "frac": c["graph_node_frac"], "unit": "one step a graph node"}
         out["config1_choice_batched"] = {"bound": "hbm", "achieved_GBs": c["batched_GBs"], "frac": c["batched_frac"],
-                                         "unit": "512 steps in one launch"}
+                                         "kernel": c.get("batched_kernel"), "unit": "512 steps in one launch"}
     if "attention" in r:
         for L, a in r["attention"].items():
             out[f"config2_attention_{L}"] = {"bound": "hbm", "achieved_GBs": a["graph_node_GBs"],
