@@ -255,3 +255,30 @@ def test_many_rows_edge_rules(dev, n_vocab):
             a, b = pen[i], ref
             assert np.array_equal(np.isnan(a), np.isnan(b))
             assert np.array_equal(a[~np.isnan(a)].view(np.uint32), b[~np.isnan(b)].view(np.uint32)), (rp, i)
+
+
+def test_many_rows_past_the_bitmap_take_the_per_span_kernel(dev):
+    """a vocabulary whose window bitmap would pass 64 KB of LDS (600,000 ids): the batched form keeps the per-span
+    kernel (k_choose<4096>, atomics per row) — tokens and penalised rows against the oracle"""
+    n_vocab, n, window, rp = 600000, 3, 16, 1.2
+    g = np.random.default_rng(600)
+    rows = g.normal(0, 3, (n, n_vocab)).astype(np.float32)
+    rows[0, [5, 599999]] = 40.0          # a tie across the row's ends: the lower id
+    rows[1, 123456] = 50.0               # a window id on the maximum: reversed by the penalty
+    rows[2, :] = -np.inf
+    hists = [list(g.integers(0, n_vocab, window)), [123456] * window, list(g.integers(0, n_vocab, window))]
+    hb = dev.upload(np.concatenate([np.asarray(hists, np.uint32), np.zeros((n, 1), np.uint32)], axis=1))
+    lb = dev.upload(rows)
+    tok = dev.alloc(n * 4)
+    htr.choose_many(dev, lb, n_vocab, n, hb, window + 1, window, window, rp, tok)
+    assert dev.last_kernel() == "k_choose"
+    got = [int(t) for t in tok.download(np.uint32, n)]
+    pen = lb.download(np.float32).reshape(n, n_vocab)
+    for i in range(n):
+        ref = rows[i].copy()
+        want = orc.choose(ref, rp, window, 0.0, [int(t) for t in hists[i]])
+        assert got[i] == want, i
+        assert np.array_equal(pen[i].view(np.uint32), ref.view(np.uint32)), i
+    assert got[2] == 0
+    for b in (hb, lb, tok):
+        b.free()
