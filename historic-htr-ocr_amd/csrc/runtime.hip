@@ -131,6 +131,15 @@ extern "C" int htr_device_open(int ordinal, htr_device **out) {
         delete dev;
         return htr_fail("%s", keep.c_str());
     }
+    // how a launch places its workgroups on the 8 XCDs, and whether a word stored at workgroup scope is seen across an
+    // XCD's workgroups (token_step_xcds), checked once here: the one-launch decode step and the decode attention's
+    // XCD-local merge rest on both
+    const char *why = nullptr;
+    if (token_step_xcds(dev, &why) < 0) {
+        std::string keep = htr_last_error();
+        htr_device_close(dev);
+        return htr_fail("%s", keep.c_str());
+    }
     *out = dev;
     return 0;
 }
