@@ -64,6 +64,38 @@ def test_decode_attention_edge_lengths(dev, n_keys):
     assert rel_l2(got, orc.attn_f64(q, k, v, n_kv * 128, n_keys, n_head, n_kv, 1 / np.sqrt(128))) < 1e-5
 
 
+def test_decode_attention_merge_across_launches_and_scopes(dev):
+    """one launch after another on the same device scratch: 8 KV heads (a head's chunks on one XCD, the partials and
+    the ticket in its L2) at chunk counts that rise and fall (1 … 32 chunks a head), 2 KV heads (the merge through the
+    coherence point) in between, and the allocation-free entry point — every output against fp64, so a ticket left
+    off zero by any launch would show in the next"""
+    cases = []
+    for n_keys in (300, 17, 2048, 16, 1537, 8192, 33, 513):
+        cases.append((16, 8, n_keys))
+        if n_keys in (17, 1537):
+            cases.append((4, 2, n_keys))
+    sc = 1 / np.sqrt(128)
+    for i, (n_head, n_kv, n_keys) in enumerate(cases):
+        g = orc.Lcg(700 + i)
+        k = orc.f16_bits(g.f32(n_keys * n_kv * 128, 2.0)).reshape(n_keys, -1)
+        v = orc.f16_bits(g.f32(n_keys * n_kv * 128)).reshape(n_keys, -1)
+        q = g.f32(n_head * 128, 2.0)
+        want = orc.attn_f64(q, k, v, n_kv * 128, n_keys, n_head, n_kv, sc)
+        got = _attention_case(dev, n_head, n_kv, n_keys, n_keys + 3, q, k, v)
+        assert rel_l2(got, want) < 1e-5, (n_head, n_kv, n_keys)
+        if n_kv == 8 and n_keys <= 2048:
+            n_ctx = n_keys + 3
+            kc = dev.upload(kv_head_major(np.pad(k, ((0, 3), (0, 0))), n_kv))
+            vc = dev.upload(kv_head_major(np.pad(v, ((0, 3), (0, 0))), n_kv))
+            qb, out = dev.upload(q), dev.alloc(n_head * 128 * 4)
+            rc = htr.lib().htr_decode_attention_static(dev.h, qb.ptr, kc.ptr, vc.ptr, n_head, n_kv, n_ctx, n_keys,
+                                                       float(np.float32(sc)), out.ptr)
+            assert rc == 0, htr.last_error()
+            assert rel_l2(out.download(np.float32), want) < 1e-5, ("static", n_keys)
+            for b in (kc, vc, qb, out):
+                b.free()
+
+
 @pytest.mark.parametrize("L", [512, 2048, 8192])
 def test_config2_attention(dev, L):
     """16 q / 8 kv heads × 128, K / V ~ N(0,1) f16, q ~ N(0,1) → per-head RMSNorm (ε 1e-6, weights
