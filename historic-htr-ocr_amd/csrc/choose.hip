@@ -54,12 +54,16 @@ __device__ __forceinline__ void block_best(float &v, uint32_t &i) {
         }
 }
 
-template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
+// XL (one row): the launch holds 8 workgroups a span and only those of XCD 0 (blockIdx.x ≡ 0 mod 8 on a device whose
+// launches spread workgroups round-robin over its 8 XCDs, checked at open) work, so the row's best key and ticket are
+// atomics in that XCD's L2 (workgroup scope) instead of at the coherence point
+template <int SP, bool XL = false> __global__ __launch_bounds__(CW) void k_choose(const ChooseArgs a) {
+    if (XL && (blockIdx.x & 7)) return;
     constexpr int PER_ = SP / CW;  // logits a thread
     __shared__ float s_l[SP];
     __shared__ __attribute__((aligned(16))) uint8_t s_pen[SP];  // the span's logits whose id is in the window
     __shared__ int s_last;
-    const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int g = XL ? blockIdx.x >> 3 : blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int lo = g * SP, hi = min(a.n_vocab, lo + SP);
     float *logits = a.logits + (size_t)row * a.n_vocab;
     uint32_t *hist = a.hist + (size_t)row * a.hist_stride;
@@ -140,11 +144,13 @@ template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArg
         // a NaN at index 0 after the penalty decides token 0 (the CPU loop never finds a greater value): top key
         const bool nan0 = lo == 0 && s_l[0] != s_l[0];
         const uint64_t key = nan0 ? ~0ull : choose_key(bv, bi);
-        __hip_atomic_fetch_max(best, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (XL) __hip_atomic_fetch_max(best, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else __hip_atomic_fetch_max(best, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // the max is performed before the ticket: wait for its return
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 gridDim.x - 1;
+        s_last = (XL ? __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                     : __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) ==
+                 (XL ? gridDim.x >> 3 : gridDim.x) - 1;
     }
     __syncthreads();
     if (!s_last || tid != 0) return;
@@ -162,8 +168,13 @@ template <int SP> __global__ __launch_bounds__(CW) void k_choose(const ChooseArg
     if (a.len_dev) *(int *)a.len_dev = len + 1;
     if (a.advance) a.advance[0] += 1;
     // ready for the next launch (seen by it: a kernel boundary)
-    __hip_atomic_store(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (XL) {
+        __hip_atomic_store(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+        __hip_atomic_store(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // Many rows (no frequency penalty): one workgroup a row, nothing handed between workgroups. The window's ids set one bit
@@ -271,7 +282,14 @@ int launch_choose(htr_device *dev, hipStream_t st, const ChooseArgs &a) {
     // one row: 2048 logits a workgroup (75 over 151,936), a step 10.8 µs launched alone against 11.6 µs with 4096 and
     // 12.8 µs with 8192
     if (a.rows == 1) {
-        hipLaunchKernelGGL(k_choose<2048>, dim3(choose_groups(a.n_vocab, 2048), 1), dim3(CW), 0, st, a);
+        // on XCD 0 alone where the placement holds: 5.55 → 5.38 µs a step as a graph node (A/B twice on one box,
+        // tokens and penalised logits identical) — the L2's atomics gain a little more than one XCD's share of the
+        // read costs
+        if (dev->xcd_round_robin == 1)
+            hipLaunchKernelGGL((k_choose<2048, true>), dim3(8 * choose_groups(a.n_vocab, 2048), 1), dim3(CW), 0, st,
+                               a);
+        else
+            hipLaunchKernelGGL(k_choose<2048>, dim3(choose_groups(a.n_vocab, 2048), 1), dim3(CW), 0, st, a);
         return htr_launched(dev, "k_choose");
     }
     // many rows without the frequency penalty or the device-resident counters: a workgroup a row, the window's bitmap
