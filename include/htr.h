@@ -46,7 +46,7 @@ const char *htr_last_error(void);
  * a kernel reading what nothing wrote (or what was freed) reads NaN. The open also checks, with a few small launches,
  * how a launch places its workgroups on the device's 8 XCDs and whether a word stored at workgroup scope is seen by
  * the other workgroups of its XCD; the one-launch decode step, the decode attention's merge and the one-row choice
- * keep their XCD-local forms to a device where both hold. */
+ * use their XCD-local forms only on a device where both hold. */
 int htr_device_open(int ordinal, htr_device **out);
 int htr_device_close(htr_device *dev);
 /* 0 while the device is healthy; < 0 with the sticky reason once it is dead (gpu.rs:1386-1396 Gpu::alive) */
